@@ -1,0 +1,41 @@
+"""Build libg1env.so for gfx950 in-tree (g1.cu_amd/build/libg1env.so).
+
+    python g1.cu_amd/build.py
+
+The library lands where the reference's Python looks for it relative to its scripts folder
+(<root>/build/libg1env.so, reference scripts/ppo.py:20-24), with <root> = g1.cu_amd.
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SRC = os.path.join(HERE, "csrc", "g1env.hip")
+OUT_DIR = os.path.join(HERE, "build")
+OUT = os.path.join(OUT_DIR, "libg1env.so")
+ARCH = os.environ.get("G1_OFFLOAD_ARCH", "gfx950")
+
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    # no packed-FP32 VALU forms (v_pk_*_f32): some of their forms have produced silently wrong
+    # results on this GPU pool; hipcc's host pass warns that it does not know the feature
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # code-object v5 loads under both the ROCm 7.2 runtime and torch's bundled HIP 7.0 runtime
+    "-mcode-object-version=5",
+    "-Wno-pass-failed",
+]
+
+
+def build(verbose=False):
+    os.makedirs(OUT_DIR, exist_ok=True)
+    cmd = ["hipcc", *FLAGS, SRC, "-o", OUT + ".tmp"]
+    if verbose:
+        cmd.append("-Rpass-analysis=kernel-resource-usage")
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(OUT + ".tmp", OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

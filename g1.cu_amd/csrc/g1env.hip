@@ -1,0 +1,776 @@
+// g1env.hip -- MI355X (gfx950) implementation of g1.cu's batched G1 environment and fused PPO
+// rollout behind the reference's libg1env.so C ABI (reference: src/g1_env.cu:361-476).
+//
+// Rollout structure: g1_rollout enqueues, on the null stream and without any host sync,
+//   pack(W) -> [policy(t) -> physics(t)] for t < H -> policy(H) (bootstrap value)
+// policy(t): obs -> frozen normalisation -> MLP on fp32 MFMA over 32-world tiles -> sampling;
+// physics(t): S substeps of FK -> PD -> world_qacc -> Euler on 32-lane world groups, then reward,
+// termination and auto-reset. Trajectory tensors O/A/LP/V/R/D/Vlast are caller-owned device
+// buffers written in place, exactly as the reference's k_rollout does (src/g1_env.cu:278-338).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "../../include/g1env.h"
+#include "physics.h"
+#include "policy.h"
+
+using namespace g1k;
+
+#define HIPCHECK(call)                                                                          \
+  do {                                                                                          \
+    hipError_t e_ = (call);                                                                     \
+    if (e_ != hipSuccess) {                                                                     \
+      fprintf(stderr, "g1env HIP error %s:%d %s\n", __FILE__, __LINE__, hipGetErrorString(e_)); \
+      exit(1);                                                                                  \
+    }                                                                                           \
+  } while (0)
+
+static void fail(const char* msg) {
+  fprintf(stderr, "g1env: %s\n", msg);
+  exit(1);
+}
+
+// ====================================================================== physics kernels
+struct PhysArgs {
+  float* qp; float* qv; float* pa; int* steps; unsigned* rng;
+  int N, S, pgs, K;                // K control steps per launch (same action buffer row t0 + k*astep)
+  float mu;
+  const float* act; int t0, astep; // actions [*, N, 29]; row t = t0 + k * astep
+  const float* reset_noise;        // [*, N, 29] injected U(-1,1) or null (Philox)
+  float* R; float* D; int rstep;   // outputs [*, N], row t0 + k * rstep
+  unsigned long long seed;
+  unsigned long long* ncon_hist;   // [9] or null
+};
+
+constexpr int kPhysThreads = 64;   // one wave64 = two 32-lane world groups
+
+__global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
+  __shared__ WorldLds lds[2];
+  const int g = group_id(), l = group_lane();
+  const int w = blockIdx.x * 2 + g;
+  const bool wvalid = w < a.N;
+  const int wc = wvalid ? w : a.N - 1;
+  WorldLds& s = lds[g];
+  const LaneModel L = lane_model(l);
+
+  LaneState st;
+  const float* gq = a.qp + (long)wc * kNQ;
+  const float* gv = a.qv + (long)wc * kNV;
+#pragma unroll
+  for (int k = 0; k < 7; ++k) st.bq[k] = gq[k];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) st.bqd[k] = gv[k];
+  st.jq = L.hinge ? gq[L.b + 5] : 0.f;
+  st.jqd = L.hinge ? gv[L.b + 4] : 0.f;
+  const int ai = L.hinge ? L.b - 2 : 0;
+  float pa = L.hinge ? a.pa[(long)wc * kAct + ai] : 0.f;
+  int step = a.steps[wc];
+  unsigned rng = a.rng[wc];
+  const SolveParams P{a.pgs, a.mu, true, true};
+  unsigned hcnt = 0;   // lane q < 9 counts substeps with q contacts
+
+#pragma unroll 1
+  for (int k = 0; k < a.K; ++k) {
+    const int t = a.t0 + k * a.astep;
+    const float act = L.hinge ? a.act[((long)t * a.N + wc) * kAct + ai] : 0.f;
+    // PD target = clamp(stand + 0.5 a) (reference: src/g1_env.cu:123-130)
+    float target = L.qstand + 0.5f * act;
+    if (target < L.clo) target = L.clo;
+    if (target > L.chi) target = L.chi;
+    float vx_sum = 0.f, energy = 0.f;
+#pragma unroll 1
+    for (int sub = 0; sub < a.S; ++sub) {
+      float jtau = 0.f;
+      if (L.hinge) {
+        float pdt = L.kp * (target - st.jq) - L.kd * st.jqd;
+        if (pdt < L.flo) pdt = L.flo;
+        else if (pdt > L.fhi) pdt = L.fhi;
+        jtau = pdt;
+        energy += fabsf(pdt * st.jqd);
+      }
+      float bqacc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, jqacc = 0.f;
+      const int nc = world_qacc(l, s, st, jtau, P, bqacc, jqacc);
+      hcnt += (l == nc) ? 1u : 0u;
+      integrate_lane(L, st, bqacc, jqacc, true);
+      vx_sum += st.bqd[0];
+    }
+    // ---- reward / termination / auto-reset (reference: src/g1_env.cu:164-211), lane 1 decides
+    const float da = L.hinge ? act - pa : 0.f;
+    float act_pen = gsum(da * da);
+    const float energy_tot = gsum(energy);
+    int d_flag = 0;
+    float r = 0.f;
+    if (l == 1) {
+      const float vx = vx_sum / (float)a.S;
+      const float height = st.bq[2];
+      const float qw = st.bq[3], qx = st.bq[4], qy = st.bq[5];
+      const float up = 1.f - 2.f * (qx * qx + qy * qy);
+      const int alive = !(height < 0.45f || up < 0.5f);
+      (void)qw;
+      const float upc = up < 0.f ? 0.f : (up > 1.f ? 1.f : up);
+      float vx_c = vx > 0.8f ? 0.8f : vx;
+      if (vx_c < 0.f) vx_c = 0.f;
+      const float r_vel = 1.0f * vx_c * upc;
+      const float r_lat = -0.2f * fabsf(st.bqd[1]) - 0.05f * fabsf(st.bqd[5]);
+      const float r_up = 0.3f * upc;
+      const float r_h = -0.5f * fabsf(height - 0.78f);
+      if (act_pen > 10.f) act_pen = 10.f;
+      r = alive ? 1.0f + r_vel + r_lat + r_up + r_h - 0.005f * act_pen - 1e-4f * energy_tot : -5.0f;
+      const int won = alive && st.bq[0] >= 5.0f;
+      if (won) r += 50.0f;
+      d_flag = (!alive || won || step + 1 >= 1000) ? 1 : 0;
+    }
+    d_flag = gshfl(d_flag, 1);
+    step += 1;
+    pa = act;
+    if (d_flag) {
+      const float u = a.reset_noise ? a.reset_noise[((long)t * a.N + wc) * kAct + ai]
+                                    : rng_pm1(a.seed, wc, rng, kStreamReset, ai);
+      if (L.hinge) { st.jq = L.qstand + 0.05f * u; st.jqd = 0.f; pa = 0.f; }
+#pragma unroll
+      for (int q = 0; q < 7; ++q) st.bq[q] = MF::qpos_stand[q];
+#pragma unroll
+      for (int q = 0; q < 6; ++q) st.bqd[q] = 0.f;
+      step = 0;
+    }
+    rng += 1;
+    if (wvalid && l == 1) {
+      const long o = (long)(a.t0 + k * a.rstep) * a.N + w;
+      a.R[o] = r;
+      a.D[o] = (float)d_flag;
+    }
+  }
+  if (wvalid) {
+    float* oq = a.qp + (long)w * kNQ;
+    float* ov = a.qv + (long)w * kNV;
+    if (l == 1) {
+#pragma unroll
+      for (int q = 0; q < 7; ++q) oq[q] = st.bq[q];
+#pragma unroll
+      for (int q = 0; q < 6; ++q) ov[q] = st.bqd[q];
+      a.steps[w] = step;
+      a.rng[w] = rng;
+    }
+    if (L.hinge) {
+      oq[L.b + 5] = st.jq;
+      ov[L.b + 4] = st.jqd;
+      a.pa[(long)w * kAct + ai] = pa;
+    }
+    if (a.ncon_hist && l < 9 && hcnt) atomicAdd(&a.ncon_hist[l], (unsigned long long)hcnt);
+  }
+}
+
+// ---- probes: the same world_qacc device code on caller-given states (parity harnesses)
+struct ProbeArgs {
+  int n, mode;            // mode 0: qacc only; 1: one env substep (PD from targets, guard, integrate)
+  float* qp; float* qv;   // [n][36], [n][35]; updated in place by mode 1
+  const float* tau;       // mode 0: [n][35] generalized force on the hinge dofs (base entries ignored)
+  const float* target;    // mode 1: [n][29] PD joint targets
+  float* qacc; int* ncon; // [n][35], [n]
+  int pgs, damped, contact, guard, nsub;
+  float mu;
+};
+
+__global__ void __launch_bounds__(kPhysThreads) k_probe(ProbeArgs a) {
+  __shared__ WorldLds lds[2];
+  const int g = group_id(), l = group_lane();
+  const int w = blockIdx.x * 2 + g;
+  const bool wvalid = w < a.n;
+  const int wc = wvalid ? w : a.n - 1;
+  WorldLds& s = lds[g];
+  const LaneModel L = lane_model(l);
+  LaneState st;
+  const float* gq = a.qp + (long)wc * kNQ;
+  const float* gv = a.qv + (long)wc * kNV;
+#pragma unroll
+  for (int k = 0; k < 7; ++k) st.bq[k] = gq[k];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) st.bqd[k] = gv[k];
+  st.jq = L.hinge ? gq[L.b + 5] : 0.f;
+  st.jqd = L.hinge ? gv[L.b + 4] : 0.f;
+  const SolveParams P{a.pgs, a.mu, a.damped != 0, a.contact != 0};
+  float bqacc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, jqacc = 0.f;
+  int nc = 0;
+#pragma unroll 1
+  for (int sub = 0; sub < a.nsub; ++sub) {
+    float jtau = 0.f;
+    if (L.hinge) {
+      if (a.mode == 0) jtau = a.tau[(long)wc * kNV + L.b + 4];
+      else {
+        const float tg = a.target[(long)wc * kAct + L.b - 2];
+        float pdt = L.kp * (tg - st.jq) - L.kd * st.jqd;
+        if (pdt < L.flo) pdt = L.flo;
+        else if (pdt > L.fhi) pdt = L.fhi;
+        jtau = pdt;
+      }
+    }
+    nc = world_qacc(l, s, st, jtau, P, bqacc, jqacc);
+    if (a.mode == 1) integrate_lane(L, st, bqacc, jqacc, a.guard != 0);
+  }
+  if (!wvalid) return;
+  float* oa = a.qacc + (long)w * kNV;
+  if (l == 1) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) oa[k] = bqacc[k];
+    a.ncon[w] = nc;
+  }
+  if (L.hinge) oa[L.b + 4] = jqacc;
+  if (a.mode == 1) {
+    float* oq = a.qp + (long)w * kNQ;
+    float* ov = a.qv + (long)w * kNV;
+    if (l == 1) {
+#pragma unroll
+      for (int k = 0; k < 7; ++k) oq[k] = st.bq[k];
+#pragma unroll
+      for (int k = 0; k < 6; ++k) ov[k] = st.bqd[k];
+    }
+    if (L.hinge) { oq[L.b + 5] = st.jq; ov[L.b + 4] = st.jqd; }
+  }
+}
+
+// ====================================================================== policy kernels
+struct PolicyArgs {
+  int ldx;                          // LDS row pitch (floats) of the activation tiles
+  const float* qp; const float* qv; const float* pa; const unsigned* rng;
+  int N, t, H;                      // t == H: bootstrap value only
+  const float* mean; const float* var;
+  PackedPolicy pp; PolicyShape shape;
+  const float* act_noise;           // [H][N][29] or null (Philox)
+  unsigned long long seed;
+  float* O; float* A; float* LP; float* V; float* Vlast;
+  const float* obs_in;              // probe mode: normalised observations [N][100] (skips obs/O)
+  float* mu_out;                    // probe mode: [N][29] mean action
+};
+
+__global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
+  extern __shared__ float smem[];
+  const int kLdx = a.ldx;
+  float* X = smem;                          // [32][ldx]
+  float* Y = smem + kTileWorlds * kLdx;     // [32][ldx]
+  const int tid = threadIdx.x;
+  const int w0 = blockIdx.x * kTileWorlds;
+  // ---- observation + frozen normalisation (reference: src/g1_env.cu:297-304)
+  for (int idx = tid; idx < kTileWorlds * kObs; idx += kPolicyThreads) {
+    const int m = idx / kObs, i = idx - m * kObs;
+    const int w = w0 + m;
+    float z = 0.f;
+    if (w < a.N) {
+      if (a.obs_in) z = a.obs_in[(long)w * kObs + i];
+      else {
+        const float o = obs_value(a.qp + (long)w * kNQ, a.qv + (long)w * kNV, a.pa + (long)w * kAct, i);
+        if (a.t < a.H) a.O[((long)a.t * a.N + w) * kObs + i] = o;
+        z = (o - a.mean[i]) / sqrtf(a.var[i] + 1e-8f);
+        if (z < -10.f) z = -10.f; else if (z > 10.f) z = 10.f;
+      }
+    }
+    X[m * kLdx + i] = z;
+  }
+  __syncthreads();
+  // ---- hidden layers
+  float* in = X;
+  float* out = Y;
+  for (int ly = 0; ly < a.shape.nl; ++ly) {
+    mfma_layer(in, kLdx, out, kLdx, a.pp.Wp + a.pp.woff[ly], a.pp.Wp + a.pp.boff[ly], a.pp.K[ly], a.pp.Np[ly],
+               a.shape.act, true);
+    __syncthreads();
+    float* t = in; in = out; out = t;
+  }
+  // ---- fused head [mu(29) | v | pad]
+  mfma_layer(in, kLdx, out, kLdx, a.pp.Wp + a.pp.woff[a.shape.nl], a.pp.Wp + a.pp.boff[a.shape.nl],
+             a.pp.K[a.shape.nl], 32, 0, false);
+  __syncthreads();
+  // ---- sampling + log-prob, one thread per world, actions in order (reference: src/g1_env.cu:308-318)
+  if (tid < kTileWorlds) {
+    const int w = w0 + tid;
+    if (w < a.N) {
+      const float* h = out + tid * kLdx;
+      const float val = h[kAct];
+      if (a.mu_out) {
+        for (int i = 0; i < kAct; ++i) a.mu_out[(long)w * kAct + i] = h[i];
+        a.V[w] = val;
+      } else if (a.t == a.H) {
+        a.Vlast[w] = val;
+      } else {
+        const float LOG2PI = 1.8378770664093453f;
+        float lpsum = 0.f;
+        const long ab = ((long)a.t * a.N + w) * kAct;
+        for (int i = 0; i < kAct; ++i) {
+          const float ls = a.pp.log_std[i];
+          const float sd = expf(ls);
+          const float nz = a.act_noise ? a.act_noise[ab + i] : rng_normal(a.seed, w, a.rng[w], kStreamAction, i);
+          a.A[ab + i] = h[i] + sd * nz;
+          lpsum += -0.5f * nz * nz - ls - 0.5f * LOG2PI;
+        }
+        a.LP[(long)a.t * a.N + w] = lpsum;
+        a.V[(long)a.t * a.N + w] = val;
+      }
+    }
+  }
+}
+
+// Pack torch-order weights W0,b0,..,Wmu,bmu,Wv,bv,log_std into MFMA layout (k-pair major).
+struct PackArgs {
+  const float* W; float* Wp; PackedPolicy pp; PolicyShape shape; long total;
+};
+__global__ void k_pack(PackArgs a) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= a.total) return;
+  // locate layer
+  int ly = 0;
+  while (ly < a.shape.nl && idx >= a.pp.woff[ly + 1]) ++ly;
+  const long base = a.pp.woff[ly];
+  const long rel = idx - base;
+  const int K = a.pp.K[ly], Np = a.pp.Np[ly];
+  const long wsize = (long)(K / 2) * Np * 2;
+  // source offsets in torch order
+  long src = 0;
+  int in = kObs;
+  for (int q = 0; q < ly; ++q) { src += (long)a.shape.hid[q] * in + a.shape.hid[q]; in = a.shape.hid[q]; }
+  const int Kin = in;
+  if (rel < wsize) {
+    const int kk = (int)(rel / (Np * 2)), rem = (int)(rel % (Np * 2));
+    const int n = rem / 2, k = 2 * kk + (rem & 1);
+    float v = 0.f;
+    if (ly < a.shape.nl) {
+      if (n < a.shape.hid[ly] && k < Kin) v = a.W[src + (long)n * Kin + k];
+    } else if (k < Kin) {
+      if (n < kAct) v = a.W[src + (long)n * Kin + k];                       // Wmu
+      else if (n == kAct) v = a.W[src + (long)kAct * Kin + kAct + k];        // Wv
+    }
+    a.Wp[idx] = v;
+  } else {
+    const int n = (int)(rel - wsize);
+    float v = 0.f;
+    if (ly < a.shape.nl) {
+      if (n < a.shape.hid[ly]) v = a.W[src + (long)a.shape.hid[ly] * Kin + n];
+    } else {
+      if (n < kAct) v = a.W[src + (long)kAct * Kin + n];                          // bmu
+      else if (n == kAct) v = a.W[src + (long)kAct * Kin + kAct + Kin];            // bv
+    }
+    a.Wp[idx] = v;
+  }
+}
+
+// ---- reset (reference: src/g1_env.cu:97-111) and observation export
+__global__ void k_reset(float* qp, float* qv, float* pa, int* steps, unsigned* rng, int N, float noise,
+                        const float* inj, unsigned long long seed) {
+  const int w = blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= N) return;
+  float* gq = qp + (long)w * kNQ;
+  for (int i = 0; i < kNQ; ++i) gq[i] = MF::qpos_stand[i];
+  for (int i = 0; i < kAct; ++i) {
+    const float u = inj ? inj[(long)w * kAct + i] : rng_pm1(seed, w, rng[w], kStreamInit, i);
+    gq[act_qadr[i]] += noise * u;
+  }
+  for (int i = 0; i < kNV; ++i) qv[(long)w * kNV + i] = 0.f;
+  for (int i = 0; i < kAct; ++i) pa[(long)w * kAct + i] = 0.f;
+  steps[w] = 0;
+  rng[w] += 1;
+}
+
+__global__ void k_obs(const float* qp, const float* qv, const float* pa, int N, float* obs) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)N * kObs) return;
+  const int w = (int)(idx / kObs), i = (int)(idx % kObs);
+  obs[idx] = obs_value(qp + (long)w * kNQ, qv + (long)w * kNV, pa + (long)w * kAct, i);
+}
+
+__global__ void k_philox(const unsigned* in, unsigned* out, int n, unsigned k0, unsigned k1) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  U4 r = philox4x32_10(U4{in[4 * i], in[4 * i + 1], in[4 * i + 2], in[4 * i + 3]}, k0, k1);
+  out[4 * i] = r.x; out[4 * i + 1] = r.y; out[4 * i + 2] = r.z; out[4 * i + 3] = r.w;
+}
+
+// ====================================================================== host side
+struct EnvState {
+  int N, S, pgs;
+  unsigned long long seed;
+  float mu;
+  PolicyShape shape;
+  float *qp, *qv, *pa;
+  int* steps;
+  unsigned* rng;
+  float *dact, *dobs, *drew, *ddone, *zero_act, *bench_r, *bench_d;
+  float* Wp;
+  long Wp_cap;
+  unsigned long long* ncon_hist;
+  int hist_on;
+  // per-launch HIP events of the rollout's physics / policy kernels (null stream)
+  int prof_on;
+  std::vector<hipEvent_t> ev_phys, ev_pol;
+  size_t n_phys, n_pol;
+};
+
+static void prof_mark(std::vector<hipEvent_t>& v, size_t& n) {
+  if (n == v.size()) {
+    hipEvent_t e;
+    HIPCHECK(hipEventCreate(&e));
+    v.push_back(e);
+  }
+  HIPCHECK(hipEventRecord(v[n++], 0));
+}
+
+static PackedPolicy make_packed(const PolicyShape& sh, float* Wp, const float* W, long* total) {
+  PackedPolicy pp{};
+  pp.Wp = Wp;
+  long off = 0;
+  int in = kObs;
+  for (int ly = 0; ly <= sh.nl; ++ly) {
+    const int out = ly < sh.nl ? sh.hid[ly] : 32;
+    pp.K[ly] = (in + 1) & ~1;
+    pp.Np[ly] = (out + 31) & ~31;
+    pp.woff[ly] = off;
+    off += (long)(pp.K[ly] / 2) * pp.Np[ly] * 2;
+    pp.boff[ly] = off;
+    off += pp.Np[ly];
+    if (ly < sh.nl) in = sh.hid[ly];
+  }
+  // pack-kernel layer search uses woff[nl+1] as the end sentinel
+  if (sh.nl + 1 <= kMaxLayers) pp.woff[sh.nl + 1] = off;
+  *total = off;
+  long nparam = 0;
+  in = kObs;
+  for (int ly = 0; ly < sh.nl; ++ly) { nparam += (long)sh.hid[ly] * in + sh.hid[ly]; in = sh.hid[ly]; }
+  nparam += (long)kAct * in + kAct + in + 1;
+  pp.log_std = W ? W + nparam : nullptr;
+  return pp;
+}
+
+static long policy_param_count(const PolicyShape& sh) {
+  long n = 0;
+  int in = kObs;
+  for (int ly = 0; ly < sh.nl; ++ly) { n += (long)sh.hid[ly] * in + sh.hid[ly]; in = sh.hid[ly]; }
+  return n + (long)kAct * in + kAct + in + 1 + kAct;
+}
+
+static int max_width(const PolicyShape& sh) {
+  int m = kObs;
+  for (int ly = 0; ly < sh.nl; ++ly) m = sh.hid[ly] > m ? sh.hid[ly] : m;
+  return m;
+}
+
+static void pack_policy(EnvState* E, const float* W, PackedPolicy* out) {
+  long total = 0;
+  PackedPolicy pp = make_packed(E->shape, nullptr, W, &total);
+  if (total > E->Wp_cap) {
+    if (E->Wp) HIPCHECK(hipFree(E->Wp));
+    HIPCHECK(hipMalloc(&E->Wp, total * sizeof(float)));
+    E->Wp_cap = total;
+  }
+  pp = make_packed(E->shape, E->Wp, W, &total);
+  PackArgs pa{W, E->Wp, pp, E->shape, total};
+  hipLaunchKernelGGL(k_pack, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, 0, pa);
+  HIPCHECK(hipGetLastError());
+  *out = pp;
+}
+
+// activation tile pitch: widest layer + 4 floats (keeps rows off the same LDS banks)
+static int policy_ldx(const PolicyShape& sh) { return max_width(sh) + 4; }
+static size_t policy_smem(const PolicyShape& sh) { return 2 * (size_t)kTileWorlds * policy_ldx(sh) * sizeof(float); }
+
+static void launch_policy_kernel(const PolicyArgs& a, int N, const PolicyShape& sh) {
+  const size_t smem = policy_smem(sh);
+  static size_t granted = 0;
+  if (smem > granted) {
+    HIPCHECK(hipFuncSetAttribute((const void*)k_policy, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    granted = smem;
+  }
+  hipLaunchKernelGGL(k_policy, dim3((N + kTileWorlds - 1) / kTileWorlds), dim3(kPolicyThreads), smem, 0, a);
+  HIPCHECK(hipGetLastError());
+}
+
+static void launch_policy(EnvState* E, const PackedPolicy& pp, int t, int H, const float* mean, const float* var,
+                          const float* act_noise, float* O, float* A, float* LP, float* V, float* Vlast) {
+  PolicyArgs a{};
+  a.qp = E->qp; a.qv = E->qv; a.pa = E->pa; a.rng = E->rng;
+  a.N = E->N; a.t = t; a.H = H; a.mean = mean; a.var = var; a.pp = pp; a.shape = E->shape;
+  a.act_noise = act_noise; a.seed = E->seed;
+  a.O = O; a.A = A; a.LP = LP; a.V = V; a.Vlast = Vlast;
+  a.ldx = policy_ldx(E->shape);
+  launch_policy_kernel(a, E->N, E->shape);
+}
+
+static PhysArgs phys_args(EnvState* E) {
+  PhysArgs a{};
+  a.qp = E->qp; a.qv = E->qv; a.pa = E->pa; a.steps = E->steps; a.rng = E->rng;
+  a.N = E->N; a.S = E->S; a.pgs = E->pgs; a.K = 1; a.mu = E->mu; a.seed = E->seed;
+  a.ncon_hist = E->hist_on ? E->ncon_hist : nullptr;
+  return a;
+}
+
+static void launch_physics(const PhysArgs& a) {
+  hipLaunchKernelGGL(k_physics, dim3((a.N + 1) / 2), dim3(kPhysThreads), 0, 0, a);
+  HIPCHECK(hipGetLastError());
+}
+
+static void rollout_impl(EnvState* E, int H, const float* W, const float* mean, const float* var, float* O, float* A,
+                         float* LP, float* V, float* R, float* D, float* Vlast, const float* act_noise,
+                         const float* reset_noise) {
+  if (H <= 0) fail("g1_rollout: H must be positive");
+  PackedPolicy pp;
+  pack_policy(E, W, &pp);
+  PhysArgs pa = phys_args(E);
+  pa.act = A; pa.astep = 1; pa.rstep = 1; pa.R = R; pa.D = D; pa.reset_noise = reset_noise;
+  const bool prof = E->prof_on != 0;
+  for (int t = 0; t < H; ++t) {
+    if (prof) prof_mark(E->ev_pol, E->n_pol);
+    launch_policy(E, pp, t, H, mean, var, act_noise, O, A, LP, V, Vlast);
+    if (prof) { prof_mark(E->ev_pol, E->n_pol); prof_mark(E->ev_phys, E->n_phys); }
+    pa.t0 = t;
+    launch_physics(pa);
+    if (prof) prof_mark(E->ev_phys, E->n_phys);
+  }
+  if (prof) prof_mark(E->ev_pol, E->n_pol);
+  launch_policy(E, pp, H, H, mean, var, act_noise, O, A, LP, V, Vlast);
+  if (prof) prof_mark(E->ev_pol, E->n_pol);
+}
+
+extern "C" {
+
+int g1_env_obs_dim(void) { return kObs; }
+int g1_env_act_dim(void) { return kAct; }
+
+void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
+  if (N <= 0 || substeps <= 0 || pgs_iters < 0) fail("g1_env_create: invalid N/substeps/pgs_iters");
+  EnvState* E = new EnvState();
+  E->N = N; E->S = substeps; E->pgs = pgs_iters; E->seed = seed; E->mu = MF::foot_mu;
+  E->shape = PolicyShape{2, {256, 256, 0, 0}, 0};
+  HIPCHECK(hipMalloc(&E->qp, (size_t)N * kNQ * 4));
+  HIPCHECK(hipMalloc(&E->qv, (size_t)N * kNV * 4));
+  HIPCHECK(hipMalloc(&E->pa, (size_t)N * kAct * 4));
+  HIPCHECK(hipMalloc(&E->steps, (size_t)N * 4));
+  HIPCHECK(hipMalloc(&E->rng, (size_t)N * 4));
+  HIPCHECK(hipMalloc(&E->dact, (size_t)N * kAct * 4));
+  HIPCHECK(hipMalloc(&E->dobs, (size_t)N * kObs * 4));
+  HIPCHECK(hipMalloc(&E->drew, (size_t)N * 4));
+  HIPCHECK(hipMalloc(&E->ddone, (size_t)N * 4));
+  HIPCHECK(hipMalloc(&E->zero_act, (size_t)N * kAct * 4));
+  HIPCHECK(hipMalloc(&E->bench_r, (size_t)N * 4));
+  HIPCHECK(hipMalloc(&E->bench_d, (size_t)N * 4));
+  HIPCHECK(hipMalloc(&E->ncon_hist, 9 * sizeof(unsigned long long)));
+  HIPCHECK(hipMemset(E->zero_act, 0, (size_t)N * kAct * 4));
+  HIPCHECK(hipMemset(E->rng, 0, (size_t)N * 4));
+  HIPCHECK(hipMemset(E->ncon_hist, 0, 9 * sizeof(unsigned long long)));
+  // defined start state (the reference leaves it undefined until reset)
+  hipLaunchKernelGGL(k_reset, dim3((N + 255) / 256), dim3(256), 0, 0, E->qp, E->qv, E->pa, E->steps, E->rng, N, 0.f,
+                     (const float*)nullptr, E->seed);
+  HIPCHECK(hipGetLastError());
+  HIPCHECK(hipMemset(E->rng, 0, (size_t)N * 4));
+  HIPCHECK(hipDeviceSynchronize());
+  return E;
+}
+
+void g1_env_destroy(void* h) {
+  EnvState* E = (EnvState*)h;
+  if (!E) return;
+  HIPCHECK(hipDeviceSynchronize());
+  void* bufs[] = {E->qp, E->qv, E->pa, E->steps, E->rng, E->dact, E->dobs, E->drew, E->ddone,
+                  E->zero_act, E->bench_r, E->bench_d, E->ncon_hist, E->Wp};
+  for (void* b : bufs)
+    if (b) HIPCHECK(hipFree(b));
+  for (auto e : E->ev_phys) (void)hipEventDestroy(e);
+  for (auto e : E->ev_pol) (void)hipEventDestroy(e);
+  delete E;
+}
+
+void g1_env_reset(void* h, float* obs_out) {
+  EnvState* E = (EnvState*)h;
+  const int N = E->N;
+  hipLaunchKernelGGL(k_reset, dim3((N + 255) / 256), dim3(256), 0, 0, E->qp, E->qv, E->pa, E->steps, E->rng, N, 0.02f,
+                     (const float*)nullptr, E->seed);
+  HIPCHECK(hipGetLastError());
+  hipLaunchKernelGGL(k_obs, dim3((unsigned)(((long)N * kObs + 255) / 256)), dim3(256), 0, 0, E->qp, E->qv, E->pa, N,
+                     E->dobs);
+  HIPCHECK(hipGetLastError());
+  HIPCHECK(hipMemcpy(obs_out, E->dobs, (size_t)N * kObs * 4, hipMemcpyDeviceToHost));
+}
+
+void g1_env_step(void* h, const float* act, float* obs, float* rew, float* done) {
+  EnvState* E = (EnvState*)h;
+  const int N = E->N;
+  HIPCHECK(hipMemcpy(E->dact, act, (size_t)N * kAct * 4, hipMemcpyHostToDevice));
+  PhysArgs pa = phys_args(E);
+  pa.act = E->dact; pa.t0 = 0; pa.astep = 0; pa.rstep = 0; pa.R = E->drew; pa.D = E->ddone;
+  launch_physics(pa);
+  hipLaunchKernelGGL(k_obs, dim3((unsigned)(((long)N * kObs + 255) / 256)), dim3(256), 0, 0, E->qp, E->qv, E->pa, N,
+                     E->dobs);
+  HIPCHECK(hipGetLastError());
+  HIPCHECK(hipMemcpy(obs, E->dobs, (size_t)N * kObs * 4, hipMemcpyDeviceToHost));
+  HIPCHECK(hipMemcpy(rew, E->drew, (size_t)N * 4, hipMemcpyDeviceToHost));
+  HIPCHECK(hipMemcpy(done, E->ddone, (size_t)N * 4, hipMemcpyDeviceToHost));
+}
+
+void g1_rollout(void* h, int H, const float* W, const float* mean, const float* var, float* O, float* A, float* LP,
+                float* V, float* R, float* D, float* Vlast) {
+  rollout_impl((EnvState*)h, H, W, mean, var, O, A, LP, V, R, D, Vlast, nullptr, nullptr);
+}
+
+void g1_rollout_ex(void* h, int H, const float* W, const float* mean, const float* var, float* O, float* A, float* LP,
+                   float* V, float* R, float* D, float* Vlast, const float* act_noise, const float* reset_noise) {
+  rollout_impl((EnvState*)h, H, W, mean, var, O, A, LP, V, R, D, Vlast, act_noise, reset_noise);
+}
+
+void g1_env_bench_phys(void* h, int K) {
+  EnvState* E = (EnvState*)h;
+  PhysArgs pa = phys_args(E);
+  pa.K = K; pa.act = E->zero_act; pa.t0 = 0; pa.astep = 0; pa.rstep = 0; pa.R = E->bench_r; pa.D = E->bench_d;
+  launch_physics(pa);
+  HIPCHECK(hipDeviceSynchronize());
+}
+
+void g1_env_qpos(void* h, float* out) {
+  EnvState* E = (EnvState*)h;
+  HIPCHECK(hipMemcpy(out, E->qp, (size_t)kNQ * 4, hipMemcpyDeviceToHost));
+}
+
+void g1_env_qpos_all(void* h, float* out) {
+  EnvState* E = (EnvState*)h;
+  HIPCHECK(hipMemcpy(out, E->qp, (size_t)E->N * kNQ * 4, hipMemcpyDeviceToHost));
+}
+
+void g1_occupancy_report(void) {
+  int dev = 0;
+  HIPCHECK(hipGetDevice(&dev));
+  hipDeviceProp_t p;
+  HIPCHECK(hipGetDeviceProperties(&p, dev));
+  printf("%s (%s): %d CUs, LDS/block %zu B, regs/block %d\n", p.name, p.gcnArchName, p.multiProcessorCount,
+         p.sharedMemPerBlock, p.regsPerBlock);
+  struct { const char* nm; const void* fn; int threads; size_t smem; } ks[] = {
+      {"k_physics", (const void*)k_physics, kPhysThreads, 0},
+      {"k_policy", (const void*)k_policy, kPolicyThreads, policy_smem(PolicyShape{2, {256, 256, 0, 0}, 0})},
+      {"k_probe", (const void*)k_probe, kPhysThreads, 0}};
+  for (auto& k : ks) {
+    hipFuncAttributes fa;
+    HIPCHECK(hipFuncGetAttributes(&fa, k.fn));
+    int mb = 0;
+    HIPCHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&mb, k.fn, k.threads, k.smem));
+    printf("  %-10s regs=%d scratch=%zuB lds=%zuB maxBlocks/CU=%d waves/CU=%d\n", k.nm, fa.numRegs, fa.localSizeBytes,
+           fa.sharedSizeBytes + k.smem, mb, mb * k.threads / 64);
+  }
+}
+
+// ---- additive exports (no counterpart in the reference ABI) --------------------------------
+void g1_env_set_state(void* h, const float* qp, const float* qv, const float* pa, const int* steps) {
+  EnvState* E = (EnvState*)h;
+  const size_t N = E->N;
+  HIPCHECK(hipMemcpy(E->qp, qp, N * kNQ * 4, hipMemcpyHostToDevice));
+  HIPCHECK(hipMemcpy(E->qv, qv, N * kNV * 4, hipMemcpyHostToDevice));
+  HIPCHECK(hipMemcpy(E->pa, pa, N * kAct * 4, hipMemcpyHostToDevice));
+  HIPCHECK(hipMemcpy(E->steps, steps, N * 4, hipMemcpyHostToDevice));
+}
+
+void g1_env_get_state(void* h, float* qp, float* qv, float* pa, int* steps) {
+  EnvState* E = (EnvState*)h;
+  const size_t N = E->N;
+  HIPCHECK(hipMemcpy(qp, E->qp, N * kNQ * 4, hipMemcpyDeviceToHost));
+  HIPCHECK(hipMemcpy(qv, E->qv, N * kNV * 4, hipMemcpyDeviceToHost));
+  HIPCHECK(hipMemcpy(pa, E->pa, N * kAct * 4, hipMemcpyDeviceToHost));
+  HIPCHECK(hipMemcpy(steps, E->steps, N * 4, hipMemcpyDeviceToHost));
+}
+
+int g1_env_set_policy(void* h, int nlayers, const int* hidden, int activation) {
+  EnvState* E = (EnvState*)h;
+  if (nlayers < 1 || nlayers > kMaxLayers - 1 || (activation != 0 && activation != 1)) {
+    fprintf(stderr, "g1_env_set_policy: need 1..%d hidden layers and activation 0 (tanh) or 1 (ELU)\n", kMaxLayers - 1);
+    return -1;
+  }
+  PolicyShape sh{nlayers, {0, 0, 0, 0}, activation};
+  for (int i = 0; i < nlayers; ++i) {
+    if (hidden[i] < 1 || hidden[i] > kMaxHidden) {
+      fprintf(stderr, "g1_env_set_policy: hidden width must be in 1..%d\n", kMaxHidden);
+      return -1;
+    }
+    sh.hid[i] = hidden[i];
+  }
+  E->shape = sh;
+  return 0;
+}
+
+long g1_env_policy_params(void* h) { return policy_param_count(((EnvState*)h)->shape); }
+
+void g1_env_set_contact(void* h, float mu, int pgs_iters) {
+  EnvState* E = (EnvState*)h;
+  if (!(mu >= 0.f) || pgs_iters < 0) fail("g1_env_set_contact: invalid mu/pgs_iters");
+  E->mu = mu;
+  E->pgs = pgs_iters;
+}
+
+void g1_env_ncon_hist(void* h, int enable, unsigned long long* out9) {
+  EnvState* E = (EnvState*)h;
+  if (out9) HIPCHECK(hipMemcpy(out9, E->ncon_hist, 9 * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+  HIPCHECK(hipMemset(E->ncon_hist, 0, 9 * sizeof(unsigned long long)));
+  E->hist_on = enable;
+}
+
+void g1_env_profile(void* h, int enable) {
+  EnvState* E = (EnvState*)h;
+  E->prof_on = enable;
+  E->n_phys = E->n_pol = 0;
+}
+
+void g1_env_profile_read(void* h, double* out4) {
+  EnvState* E = (EnvState*)h;
+  HIPCHECK(hipDeviceSynchronize());
+  double tp = 0.0, tq = 0.0;
+  for (size_t i = 0; i + 1 < E->n_phys; i += 2) {
+    float ms = 0.f;
+    HIPCHECK(hipEventElapsedTime(&ms, E->ev_phys[i], E->ev_phys[i + 1]));
+    tp += ms;
+  }
+  for (size_t i = 0; i + 1 < E->n_pol; i += 2) {
+    float ms = 0.f;
+    HIPCHECK(hipEventElapsedTime(&ms, E->ev_pol[i], E->ev_pol[i + 1]));
+    tq += ms;
+  }
+  out4[0] = tp; out4[1] = (double)(E->n_phys / 2); out4[2] = tq; out4[3] = (double)(E->n_pol / 2);
+}
+
+void g1_probe_qacc(int n, float* qpos, float* qvel, const float* tau, int damped, int contact, int pgs, float mu,
+                   float* qacc, int* ncon) {
+  if (n <= 0) return;
+  ProbeArgs a{};
+  a.n = n; a.mode = 0; a.qp = qpos; a.qv = qvel; a.tau = tau; a.qacc = qacc; a.ncon = ncon;
+  a.pgs = pgs; a.damped = damped; a.contact = contact; a.guard = 0; a.nsub = 1; a.mu = mu;
+  hipLaunchKernelGGL(k_probe, dim3((n + 1) / 2), dim3(kPhysThreads), 0, 0, a);
+  HIPCHECK(hipGetLastError());
+}
+
+void g1_probe_substep(int n, float* qpos, float* qvel, const float* target, int nsub, int pgs, float mu, float* qacc,
+                      int* ncon) {
+  if (n <= 0) return;
+  ProbeArgs a{};
+  a.n = n; a.mode = 1; a.qp = qpos; a.qv = qvel; a.target = target; a.qacc = qacc; a.ncon = ncon;
+  a.pgs = pgs; a.damped = 1; a.contact = 1; a.guard = 1; a.nsub = nsub; a.mu = mu;
+  hipLaunchKernelGGL(k_probe, dim3((n + 1) / 2), dim3(kPhysThreads), 0, 0, a);
+  HIPCHECK(hipGetLastError());
+}
+
+int g1_probe_policy(int n, int nlayers, const int* hidden, int activation, const float* W, const float* obs_norm,
+                    float* mu_out, float* v_out) {
+  if (n <= 0) return 0;
+  EnvState tmp{};
+  tmp.N = n;
+  if (g1_env_set_policy(&tmp, nlayers, hidden, activation) != 0) return -1;
+  PackedPolicy pp;
+  pack_policy(&tmp, W, &pp);
+  PolicyArgs a{};
+  a.N = n; a.t = 0; a.H = 1; a.pp = pp; a.shape = tmp.shape; a.obs_in = obs_norm; a.mu_out = mu_out; a.V = v_out;
+  a.ldx = policy_ldx(tmp.shape);
+  launch_policy_kernel(a, n, tmp.shape);
+  HIPCHECK(hipDeviceSynchronize());
+  HIPCHECK(hipFree(tmp.Wp));
+  return 0;
+}
+
+void g1_probe_philox(int n, const unsigned* ctr, unsigned* out, unsigned k0, unsigned k1) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_philox, dim3((n + 255) / 256), dim3(256), 0, 0, ctr, out, n, k0, k1);
+  HIPCHECK(hipGetLastError());
+}
+
+}  // extern "C"

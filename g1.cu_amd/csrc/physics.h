@@ -1,0 +1,817 @@
+// physics.h -- one G1 physics substep for one world on a 32-lane group (gfx950 / CDNA4).
+//
+// Mapping (two worlds per wave64, see lanes.h):
+//   * tree sweeps (FK, RNE velocity/acceleration, RNE force gather, articulated-inertia
+//     downdate): lane l == body l (0 = world, 1 = pelvis/free joint, 2..30 hinges, 31 idle).
+//     Sweeps run level-synchronously over tree depth; a parent gathers its children's
+//     contributions in descending child index, exactly the order of the reference's serial
+//     leaf->root loops, so every accumulated value has the reference's rounding sequence.
+//   * M^-1 solves: lane j == right-hand side j (0: smooth (M+dtB)^-1(tau-bias); 1+3c+a: contact
+//     basis e_{c,a}); the tree traversal is fully unrolled over the static topology so the
+//     per-column articulated bias forces stay in registers; the shared factor is read from LDS
+//     (same address on all lanes = broadcast).
+//   * contact rows: lane i == constraint row i (4 per contact); lane i holds column i of A
+//     (== row i, A is symmetric bit-for-bit) in registers for the projected Gauss-Seidel sweeps.
+//
+// Reference algorithm (Infatoshi/g1.cu): FK src/dynamics.cuh:47-88; motion axes + RNE bias
+// src/aba_bias.cuh:17-121; damped ABA factor src/aba_factor.cuh:44-109; M^-1 apply
+// src/aba_factor.cuh:121-165; foot contact + 3-basis Gram + PGS src/env_qacc.cuh:52-211,
+// src/contact.cuh:31-57,97-109,159-171; Euler + quaternion integration src/dynamics.cuh:333-355,
+// src/g1_env.cu:154-162.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "g1_model_tables.h"
+#include "lanes.h"
+
+namespace g1k {
+
+using namespace g1;
+using MF = ModelT<float>;
+
+constexpr int kCols = 1 + 3 * kNFoot;  // smooth column + 3 basis columns per contact
+constexpr int kMmStride = 37;          // odd stride: column-parallel LDS reads are conflict-free
+constexpr int kPairs = kNFoot * (kNFoot + 1) / 2;
+
+struct V3 { float x, y, z; };
+struct Q4 { float w, x, y, z; };
+
+__device__ __forceinline__ V3 vadd(V3 a, V3 b) { return {a.x + b.x, a.y + b.y, a.z + b.z}; }
+__device__ __forceinline__ V3 vsub(V3 a, V3 b) { return {a.x - b.x, a.y - b.y, a.z - b.z}; }
+__device__ __forceinline__ V3 cross(V3 a, V3 b) {
+  return {a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+}
+__device__ __forceinline__ float dot3(V3 a, V3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+__device__ __forceinline__ Q4 qmul(Q4 a, Q4 b) {
+  return {a.w * b.w - a.x * b.x - a.y * b.y - a.z * b.z, a.w * b.x + a.x * b.w + a.y * b.z - a.z * b.y,
+          a.w * b.y - a.x * b.z + a.y * b.w + a.z * b.x, a.w * b.z + a.x * b.y - a.y * b.x + a.z * b.w};
+}
+__device__ __forceinline__ V3 qrot(Q4 q, V3 v) {
+  V3 u{q.x, q.y, q.z};
+  V3 t{2.f * (u.y * v.z - u.z * v.y), 2.f * (u.z * v.x - u.x * v.z), 2.f * (u.x * v.y - u.y * v.x)};
+  return {v.x + q.w * t.x + (u.y * t.z - u.z * t.y), v.y + q.w * t.y + (u.z * t.x - u.x * t.z),
+          v.z + q.w * t.z + (u.x * t.y - u.y * t.x)};
+}
+__device__ __forceinline__ Q4 qnorm(Q4 q) {
+  float n = rsqrtf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+  return {q.w * n, q.x * n, q.y * n, q.z * n};
+}
+struct M3 { float m[9]; };
+__device__ __forceinline__ M3 quat2mat(Q4 q) {
+  float w = q.w, x = q.x, y = q.y, z = q.z;
+  M3 r;
+  r.m[0] = 1 - 2 * (y * y + z * z); r.m[1] = 2 * (x * y - w * z);     r.m[2] = 2 * (x * z + w * y);
+  r.m[3] = 2 * (x * y + w * z);     r.m[4] = 1 - 2 * (x * x + z * z); r.m[5] = 2 * (y * z - w * x);
+  r.m[6] = 2 * (x * z - w * y);     r.m[7] = 2 * (y * z + w * x);     r.m[8] = 1 - 2 * (x * x + y * y);
+  return r;
+}
+__device__ __forceinline__ void crossm(V3 w1, V3 v1, V3 w2, V3 v2, V3& ow, V3& ov) {
+  ow = cross(w1, w2);
+  V3 a = cross(w1, v2), b = cross(v1, w2);
+  ov = {a.x + b.x, a.y + b.y, a.z + b.z};
+}
+
+__device__ __forceinline__ int symidx(int i, int j) {
+  if (i > j) { int t = i; i = j; j = t; }
+  return i * 6 - (i * (i - 1)) / 2 + (j - i);
+}
+__device__ __forceinline__ float dot6(const float* a, const float* b) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) s += a[i] * b[i];
+  return s;
+}
+
+// Scheduling pin for the unrolled tree traversals: forces the six carried values through a
+// (no-op) volatile asm so each body's arithmetic completes before the next body's LDS reads are
+// issued. Without it the unrolled code hoists every body's loads up front and runs out of
+// registers.
+#define G1_PIN6(v) __asm__ volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5])::"memory")
+
+// MuJoCo solimp impedance sigmoid (reference: src/contact.cuh:97-109)
+__device__ __forceinline__ float foot_impedance(float pos) {
+  const float dmin = MF::foot_solimp[0], dmax = MF::foot_solimp[1], width = MF::foot_solimp[2];
+  const float mid = MF::foot_solimp[3], power = MF::foot_solimp[4];
+  float x = fabsf(pos) / width;
+  float y;
+  if (x >= 1.f) y = 1.f;
+  else {
+    float a = 1.f / powf(mid, power - 1.f);
+    float b = 1.f / powf(1.f - mid, power - 1.f);
+    y = (x < mid) ? a * powf(x, power) : 1.f - b * powf(1.f - x, power);
+  }
+  return dmin + y * (dmax - dmin);
+}
+
+// ---------------------------------------------------------------- per-world LDS
+struct WorldLds {
+  union {
+    struct {
+      float S[kNV][6];      // motion axes (world axes about the pelvis origin)
+      float U[kNBody][6];   // hinge factor columns I^A S
+      float invD[kNBody];   // hinge 1/(S'I^A S + armature + dt kd)
+      float Dfac[36];       // Cholesky factor of the free-joint 6x6 block
+      float rhs[kNV + 1];   // smooth right-hand side tau - bias
+    } fac;
+    float G[kPairs][9];     // 3x3 Gram blocks of contact pairs c <= c' (after the solves)
+  } u;
+  float qvel[kNV + 1];
+  float Mm[kCols][kMmStride];          // solve outputs: column 0 = qacc_smooth, 1+3c+a = M^-1 e_{c,a}
+  float Eb[kNFoot][3][kContactDofs];   // contact basis rows over the contact's 12 ancestor dofs
+  float con[kNFoot][4];                // contact point x, y, z (= pen/2), penetration
+  float con_w0[kNFoot];                // invweight0 of the foot body
+  int con_leg[kNFoot];                 // 0: left foot (body 7), 1: right foot (body 13)
+  float bvec[kMaxEfc];
+  float aref[kMaxEfc];
+  float Rc[kNFoot];
+  float f[kMaxEfc];
+  float qacc[kNV + 1];
+};
+
+// ---------------------------------------------------------------- per-lane model constants
+struct LaneModel {
+  int l, b, par, depth, c0, c1, c2, nchild;
+  bool body, hinge;
+  V3 bpos, ipos, axis, inert;
+  Q4 bquat, iquat;
+  float mass;
+  // actuator of hinge lanes (actuator index b - 2, dof b + 4, qpos b + 5)
+  float kp, kd, clo, chi, flo, fhi, qstand, bdt, arm;
+};
+
+__device__ __forceinline__ LaneModel lane_model(int l) {
+  LaneModel L;
+  L.l = l;
+  L.body = (l >= 1 && l < kNBody);
+  L.hinge = (l >= 2 && l < kNBody);
+  const int b = L.body ? l : 0;
+  L.b = b;
+  L.par = L.body ? body_parent[b] : l;
+  L.depth = L.body ? body_depth[b] : 0;
+  L.nchild = L.body ? body_nchild[b] : 0;
+  int c0 = body_child[3 * b], c1 = body_child[3 * b + 1], c2 = body_child[3 * b + 2];
+  L.c0 = (L.nchild > 0) ? c0 : l;
+  L.c1 = (L.nchild > 1) ? c1 : l;
+  L.c2 = (L.nchild > 2) ? c2 : l;
+  L.bpos = {MF::body_pos[3 * b], MF::body_pos[3 * b + 1], MF::body_pos[3 * b + 2]};
+  L.bquat = {MF::body_quat[4 * b], MF::body_quat[4 * b + 1], MF::body_quat[4 * b + 2], MF::body_quat[4 * b + 3]};
+  L.ipos = {MF::body_ipos[3 * b], MF::body_ipos[3 * b + 1], MF::body_ipos[3 * b + 2]};
+  L.iquat = {MF::body_iquat[4 * b], MF::body_iquat[4 * b + 1], MF::body_iquat[4 * b + 2], MF::body_iquat[4 * b + 3]};
+  L.inert = {MF::body_inertia[3 * b], MF::body_inertia[3 * b + 1], MF::body_inertia[3 * b + 2]};
+  L.mass = MF::body_mass[b];
+  const int j = L.body ? b - 1 : 0;   // one joint per moving body (generator-checked)
+  L.axis = {MF::jnt_axis[3 * j], MF::jnt_axis[3 * j + 1], MF::jnt_axis[3 * j + 2]};
+  const int i = L.hinge ? b - 2 : 0;
+  L.kp = MF::act_kp[i]; L.kd = MF::act_kd[i];
+  L.clo = MF::act_ctrl_lo[i]; L.chi = MF::act_ctrl_hi[i];
+  L.flo = MF::act_frc_lo[i]; L.fhi = MF::act_frc_hi[i];
+  L.qstand = L.hinge ? MF::qpos_stand[b + 5] : 0.f;
+  L.bdt = MF::dt * MF::act_kd[i];
+  L.arm = L.hinge ? MF::dof_armature[b + 4] : 0.f;
+  return L;
+}
+
+// ---------------------------------------------------------------- per-lane world state
+// Lane 1 carries the free joint (qpos[0:7], qvel[0:6]); hinge lane b carries qpos[b+5], qvel[b+4]
+// and actuator b-2 (PD target, previous and current action).
+struct LaneState {
+  float bq[7], bqd[6];
+  float jq, jqd;
+};
+
+struct SolveParams {
+  int pgs;
+  float mu;
+  bool damped;   // fold dt*kd into the factor (the env's implicit PD); false = plain M^-1
+  bool contact;  // foot-ground contact on/off
+};
+
+// ================================================================ substep: qacc of one world
+// Inputs: lane state, PD torque of the lane's hinge dof (jtau). Output: qacc of the lane's dofs
+// (lane 1: 6 base dofs into bqacc[], hinge lanes: jqacc). Returns this world's contact count.
+// Must be called by all 64 lanes of the block in uniform control flow.
+__device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState& st, float jtau,
+                                          const SolveParams& P, float (&bqacc)[6], float& jqacc) {
+  // The lane index goes through an opaque asm on every call so the per-lane model constants are
+  // re-read from the (cached) tables each substep instead of being hoisted out of the caller's
+  // substep loop, where they would occupy ~150 registers for the whole kernel.
+  int l = lane;
+  __asm__ volatile("" : "+v"(l));
+  const LaneModel L = lane_model(l);
+  const bool base = (l == 1);
+
+  // ---------------- forward kinematics (reference: src/dynamics.cuh:47-88)
+  // Hinge anchors sit at the body origin (jnt_pos == 0, generator-checked), so the reference's
+  // anchor shift pos = (pos + q*0) - q'*0 is the identity and is omitted.
+  V3 xp{0.f, 0.f, 0.f};
+  Q4 xq{1.f, 0.f, 0.f, 0.f};
+  if (base) {
+    xp = {st.bq[0], st.bq[1], st.bq[2]};
+    xq = qnorm(Q4{st.bq[3], st.bq[4], st.bq[5], st.bq[6]});
+  }
+  Q4 aa;
+  {
+    float h = 0.5f * st.jq, sn = sinf(h);
+    aa = {cosf(h), L.axis.x * sn, L.axis.y * sn, L.axis.z * sn};
+  }
+#pragma unroll 1
+  for (int r = 2; r <= kMaxDepth; ++r) {
+    Q4 qp{gshfl(xq.w, L.par), gshfl(xq.x, L.par), gshfl(xq.y, L.par), gshfl(xq.z, L.par)};
+    V3 pp{gshfl(xp.x, L.par), gshfl(xp.y, L.par), gshfl(xp.z, L.par)};
+    if (L.depth == r) {
+      xp = vadd(pp, qrot(qp, L.bpos));
+      xq = qmul(qmul(qp, L.bquat), aa);
+    }
+  }
+  const V3 xip = vadd(xp, qrot(xq, L.ipos));
+  const V3 p{gshfl(xp.x, 1), gshfl(xp.y, 1), gshfl(xp.z, 1)};   // pelvis origin
+
+  // ---------------- motion axes (reference: src/aba_bias.cuh:25-43)
+  V3 sw{0.f, 0.f, 0.f}, sv{0.f, 0.f, 0.f};   // hinge axis (angular; linear)
+  M3 R1{};
+  if (L.hinge) {
+    sw = qrot(xq, L.axis);
+    sv = cross(vsub(xp, p), sw);
+    const int d = L.b + 4;
+    s.u.fac.S[d][0] = sw.x; s.u.fac.S[d][1] = sw.y; s.u.fac.S[d][2] = sw.z;
+    s.u.fac.S[d][3] = sv.x; s.u.fac.S[d][4] = sv.y; s.u.fac.S[d][5] = sv.z;
+    s.qvel[d] = st.jqd;
+  }
+  if (base) {
+    R1 = quat2mat(xq);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+#pragma unroll
+      for (int i = 0; i < 6; ++i) s.u.fac.S[k][i] = (i == 3 + k) ? 1.f : 0.f;
+      s.u.fac.S[3 + k][0] = R1.m[k]; s.u.fac.S[3 + k][1] = R1.m[3 + k]; s.u.fac.S[3 + k][2] = R1.m[6 + k];
+      s.u.fac.S[3 + k][3] = 0.f; s.u.fac.S[3 + k][4] = 0.f; s.u.fac.S[3 + k][5] = 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k) s.qvel[k] = st.bqd[k];
+  }
+
+  // ---------------- body inertia about the pelvis origin (reference: src/aba_bias.cuh:45-55)
+  M3 Iw;
+  V3 cc{0.f, 0.f, 0.f};
+  {
+    M3 Ri = quat2mat(qmul(xq, L.iquat));
+    const float d[3] = {L.inert.x, L.inert.y, L.inert.z};
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        Iw.m[3 * i + j] = Ri.m[3 * i + 0] * d[0] * Ri.m[3 * j + 0] + Ri.m[3 * i + 1] * d[1] * Ri.m[3 * j + 1] +
+                          Ri.m[3 * i + 2] * d[2] * Ri.m[3 * j + 2];
+    cc = vsub(xip, p);
+  }
+  const float m = L.body ? L.mass : 0.f;
+
+  // ---------------- RNE velocities / accelerations, qacc = 0 (reference: src/aba_bias.cuh:57-102)
+  V3 vw{0.f, 0.f, 0.f}, vv{0.f, 0.f, 0.f}, aw{0.f, 0.f, 0.f}, av{0.f, 0.f, 0.f};
+  if (l == 0) av = {-MF::gravity[0], -MF::gravity[1], -MF::gravity[2]};
+  if (base) {
+    // free joint: translations accumulate normally; the three rotational cdof_dot use the
+    // post-translation partial velocity (reference: src/aba_bias.cuh:68-85)
+    V3 w{0.f, 0.f, 0.f}, v{0.f, 0.f, 0.f};
+    V3 Sdw[6], Sdv[6];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      V3 tw{0.f, 0.f, 0.f}, tv{k == 0 ? 1.f : 0.f, k == 1 ? 1.f : 0.f, k == 2 ? 1.f : 0.f};
+      crossm(w, v, tw, tv, Sdw[k], Sdv[k]);
+      const float qd = st.bqd[k];
+      w = {w.x + tw.x * qd, w.y + tw.y * qd, w.z + tw.z * qd};
+      v = {v.x + tv.x * qd, v.y + tv.y * qd, v.z + tv.z * qd};
+    }
+    const V3 wr = w, vr = v;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      V3 tw{R1.m[k], R1.m[3 + k], R1.m[6 + k]}, tv{0.f, 0.f, 0.f};
+      crossm(wr, vr, tw, tv, Sdw[3 + k], Sdv[3 + k]);
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const float qd = st.bqd[3 + k];
+      w = {w.x + R1.m[k] * qd, w.y + R1.m[3 + k] * qd, w.z + R1.m[6 + k] * qd};
+      v = {v.x + 0.f * qd, v.y + 0.f * qd, v.z + 0.f * qd};
+    }
+    vw = w; vv = v;
+    V3 a_w{0.f, 0.f, 0.f}, a_v{-MF::gravity[0], -MF::gravity[1], -MF::gravity[2]};
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const float qd = st.bqd[k];
+      a_w = {a_w.x + Sdw[k].x * qd, a_w.y + Sdw[k].y * qd, a_w.z + Sdw[k].z * qd};
+      a_v = {a_v.x + Sdv[k].x * qd, a_v.y + Sdv[k].y * qd, a_v.z + Sdv[k].z * qd};
+    }
+    aw = a_w; av = a_v;
+  }
+#pragma unroll 1
+  for (int r = 2; r <= kMaxDepth; ++r) {
+    V3 pw{gshfl(vw.x, L.par), gshfl(vw.y, L.par), gshfl(vw.z, L.par)};
+    V3 pv{gshfl(vv.x, L.par), gshfl(vv.y, L.par), gshfl(vv.z, L.par)};
+    V3 paw{gshfl(aw.x, L.par), gshfl(aw.y, L.par), gshfl(aw.z, L.par)};
+    V3 pav{gshfl(av.x, L.par), gshfl(av.y, L.par), gshfl(av.z, L.par)};
+    if (L.depth == r) {
+      V3 Sdw, Sdv;
+      crossm(pw, pv, sw, sv, Sdw, Sdv);
+      const float qd = st.jqd;
+      vw = {pw.x + sw.x * qd, pw.y + sw.y * qd, pw.z + sw.z * qd};
+      vv = {pv.x + sv.x * qd, pv.y + sv.y * qd, pv.z + sv.z * qd};
+      aw = {paw.x + Sdw.x * qd, paw.y + Sdw.y * qd, paw.z + Sdw.z * qd};
+      av = {pav.x + Sdv.x * qd, pav.y + Sdv.y * qd, pav.z + Sdv.z * qd};
+    }
+  }
+
+  // ---------------- body forces f = I a + v x* (I v) (reference: src/aba_bias.cuh:103-111,
+  // inertia application src/dynamics.cuh:126-139)
+  auto apply_I = [&](V3 xw, V3 xv, V3& fw, V3& fv) {
+    V3 Asw{Iw.m[0] * xw.x + Iw.m[1] * xw.y + Iw.m[2] * xw.z, Iw.m[3] * xw.x + Iw.m[4] * xw.y + Iw.m[5] * xw.z,
+           Iw.m[6] * xw.x + Iw.m[7] * xw.y + Iw.m[8] * xw.z};
+    const float c2 = dot3(cc, cc), csw = dot3(cc, xw);
+    Asw = {Asw.x + m * (c2 * xw.x - csw * cc.x), Asw.y + m * (c2 * xw.y - csw * cc.y),
+           Asw.z + m * (c2 * xw.z - csw * cc.z)};
+    V3 mc = cross(cc, xv);
+    fw = {Asw.x + m * mc.x, Asw.y + m * mc.y, Asw.z + m * mc.z};
+    V3 cs = cross(cc, xw);
+    fv = {-m * cs.x + m * xv.x, -m * cs.y + m * xv.y, -m * cs.z + m * xv.z};
+  };
+  V3 Fw{0.f, 0.f, 0.f}, Fv{0.f, 0.f, 0.f};
+  if (L.body) {
+    V3 Iaw, Iav, Ivw, Ivv;
+    apply_I(aw, av, Iaw, Iav);
+    apply_I(vw, vv, Ivw, Ivv);
+    V3 a = cross(vw, Ivw), b = cross(vv, Ivv);
+    V3 cw{a.x + b.x, a.y + b.y, a.z + b.z};
+    V3 cv = cross(vw, Ivv);
+    Fw = {Iaw.x + cw.x, Iaw.y + cw.y, Iaw.z + cw.z};
+    Fv = {Iav.x + cv.x, Iav.y + cv.y, Iav.z + cv.z};
+  }
+  // ---------------- leaf->root force gather (reference: src/aba_bias.cuh:112-120)
+#pragma unroll 1
+  for (int cd = kMaxDepth; cd >= 2; --cd) {
+    const bool gather = (L.depth == cd - 1);
+    V3 gw{gshfl(Fw.x, L.c0), gshfl(Fw.y, L.c0), gshfl(Fw.z, L.c0)};
+    V3 gv{gshfl(Fv.x, L.c0), gshfl(Fv.y, L.c0), gshfl(Fv.z, L.c0)};
+    if (gather && L.nchild > 0) { Fw = vadd(Fw, gw); Fv = vadd(Fv, gv); }
+    if (cd == body_depth[17] || cd == 2) {   // multi-child parents: torso (depth 4), pelvis (depth 1)
+      gw = {gshfl(Fw.x, L.c1), gshfl(Fw.y, L.c1), gshfl(Fw.z, L.c1)};
+      gv = {gshfl(Fv.x, L.c1), gshfl(Fv.y, L.c1), gshfl(Fv.z, L.c1)};
+      if (gather && L.nchild > 1) { Fw = vadd(Fw, gw); Fv = vadd(Fv, gv); }
+      if (cd == 2) {
+        gw = {gshfl(Fw.x, L.c2), gshfl(Fw.y, L.c2), gshfl(Fw.z, L.c2)};
+        gv = {gshfl(Fv.x, L.c2), gshfl(Fv.y, L.c2), gshfl(Fv.z, L.c2)};
+        if (gather && L.nchild > 2) { Fw = vadd(Fw, gw); Fv = vadd(Fv, gv); }
+      }
+    }
+  }
+  if (L.hinge) {
+    const float bias = sw.x * Fw.x + sw.y * Fw.y + sw.z * Fw.z + sv.x * Fv.x + sv.y * Fv.y + sv.z * Fv.z;
+    s.u.fac.rhs[L.b + 4] = -bias + jtau;
+  }
+  if (base) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      // translation axis e_k: S = (0,0,0, e_k); rotation axis R1 col k: S = (R1 col, 0,0,0)
+      const float bt = 0.f * Fw.x + 0.f * Fw.y + 0.f * Fw.z + (k == 0 ? 1.f : 0.f) * Fv.x +
+                       (k == 1 ? 1.f : 0.f) * Fv.y + (k == 2 ? 1.f : 0.f) * Fv.z;
+      const float br = R1.m[k] * Fw.x + R1.m[3 + k] * Fw.y + R1.m[6 + k] * Fw.z + 0.f * Fv.x + 0.f * Fv.y + 0.f * Fv.z;
+      s.u.fac.rhs[k] = -bt + 0.f;
+      s.u.fac.rhs[3 + k] = -br + 0.f;
+    }
+  }
+
+  // ---------------- damped articulated-inertia factor (reference: src/aba_factor.cuh:51-108)
+  float IA[21];
+  {
+    const float c2 = dot3(cc, cc);
+    float A[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) A[i] = Iw.m[i];
+    A[0] += m * (c2 - cc.x * cc.x); A[1] += m * (-cc.x * cc.y); A[2] += m * (-cc.x * cc.z);
+    A[3] += m * (-cc.y * cc.x);     A[4] += m * (c2 - cc.y * cc.y); A[5] += m * (-cc.y * cc.z);
+    A[6] += m * (-cc.z * cc.x);     A[7] += m * (-cc.z * cc.y); A[8] += m * (c2 - cc.z * cc.z);
+    const float Bx[9] = {0.f, -cc.z, cc.y, cc.z, 0.f, -cc.x, -cc.y, cc.x, 0.f};
+    float M6[36];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        M6[6 * i + j] = A[3 * i + j];
+        M6[6 * i + (j + 3)] = m * Bx[3 * i + j];
+        M6[6 * (i + 3) + j] = -m * Bx[3 * i + j];
+        M6[6 * (i + 3) + (j + 3)] = (i == j) ? m : 0.f;
+      }
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+#pragma unroll
+      for (int j = i; j < 6; ++j) IA[symidx(i, j)] = M6[i * 6 + j];
+  }
+  const float S6[6] = {sw.x, sw.y, sw.z, sv.x, sv.y, sv.z};
+#pragma unroll 1
+  for (int cd = kMaxDepth; cd >= 2; --cd) {
+    float Dl[21];
+    {
+      float U[6];
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < 6; ++j) a += IA[symidx(i, j)] * S6[j];
+        U[i] = a;
+      }
+      float D = dot6(S6, U) + L.arm;
+      if (P.damped) D += L.bdt;
+      const float invD = 1.f / D;
+#pragma unroll
+      for (int i = 0; i < 6; ++i)
+#pragma unroll
+        for (int j = i; j < 6; ++j) Dl[symidx(i, j)] = IA[symidx(i, j)] - U[i] * U[j] * invD;
+      if (L.hinge && L.depth == cd) {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) s.u.fac.U[L.b][k] = U[k];
+        s.u.fac.invD[L.b] = invD;
+      }
+    }
+    const bool gather = (L.depth == cd - 1);
+#pragma unroll
+    for (int k = 0; k < 21; ++k) {
+      const float g = gshfl(Dl[k], L.c0);
+      if (gather && L.nchild > 0) IA[k] += g;
+    }
+    if (cd == body_depth[17] || cd == 2) {
+#pragma unroll
+      for (int k = 0; k < 21; ++k) {
+        const float g = gshfl(Dl[k], L.c1);
+        if (gather && L.nchild > 1) IA[k] += g;
+      }
+      if (cd == 2) {
+#pragma unroll
+        for (int k = 0; k < 21; ++k) {
+          const float g = gshfl(Dl[k], L.c2);
+          if (gather && L.nchild > 2) IA[k] += g;
+        }
+      }
+    }
+  }
+  __syncthreads();   // S complete in LDS
+  if (base) {
+    // free-joint 6x6 block: U6 = I^A S_base, D = S_base' U6 (+ armature 0), Cholesky
+    float U6[6][6];
+#pragma unroll
+    for (int c = 0; c < 6; ++c)
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < 6; ++j) a += IA[symidx(i, j)] * s.u.fac.S[c][j];
+        U6[i][c] = a;
+      }
+    float Dm[36];
+#pragma unroll
+    for (int k = 0; k < 6; ++k)
+#pragma unroll
+      for (int c = 0; c < 6; ++c) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 6; ++i) a += s.u.fac.S[k][i] * U6[i][c];
+        Dm[k * 6 + c] = a + (k == c ? 0.f : 0.f);
+      }
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+#pragma unroll
+      for (int j = 0; j <= i; ++j) {
+        float a = Dm[i * 6 + j];
+#pragma unroll
+        for (int k = 0; k < j; ++k) a -= Dm[i * 6 + k] * Dm[j * 6 + k];
+        if (i == j) Dm[i * 6 + i] = sqrtf(a); else Dm[i * 6 + j] = a / Dm[j * 6 + j];
+      }
+#pragma unroll
+    for (int i = 0; i < 36; ++i) s.u.fac.Dfac[i] = Dm[i];
+  }
+
+  // ---------------- contact detection: lane s = foot sphere s (reference: src/contact.cuh:31-46)
+  int ncon = 0;
+  if (P.contact) {
+    const int sph = l < kNFoot ? l : 0;
+    const int fb = foot_body[sph];
+    Q4 fq{gshfl(xq.w, fb), gshfl(xq.x, fb), gshfl(xq.y, fb), gshfl(xq.z, fb)};
+    V3 fp{gshfl(xp.x, fb), gshfl(xp.y, fb), gshfl(xp.z, fb)};
+    V3 lp{MF::foot_lpos[3 * sph], MF::foot_lpos[3 * sph + 1], MF::foot_lpos[3 * sph + 2]};
+    V3 c = vadd(fp, qrot(fq, lp));
+    const float pen = c.z - MF::foot_radius;
+    const bool hit = (l < kNFoot) && (pen < 0.f);
+    const unsigned mask = group_ballot8(hit);
+    ncon = __popc(mask);
+    if (hit) {
+      const int idx = __popc(mask & ((1u << l) - 1u));
+      s.con[idx][0] = c.x; s.con[idx][1] = c.y; s.con[idx][2] = pen * 0.5f; s.con[idx][3] = pen;
+      s.con_w0[idx] = MF::foot_invweight0[sph];
+      s.con_leg[idx] = (fb == foot_body[kNFoot - 1]) ? 1 : 0;
+    }
+  }
+  const int ncon_max = wave_max(ncon);
+  __syncthreads();
+
+  // ---------------- PASS 1: basis rows, R, aref (reference: src/env_qacc.cuh:67-136)
+  const float mu = P.mu;
+  if (ncon_max > 0 && l < ncon) {
+    const int c = l;
+    const int legbase = s.con_leg[c] ? 12 : 6;
+    const V3 r = vsub(V3{s.con[c][0], s.con[c][1], s.con[c][2]}, p);
+    float v0 = 0.f, v1 = 0.f, v2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < kContactDofs; ++k) {
+      // ancestor dofs walked foot -> root: leg hinges (foot first), then the free base 0..5
+      const int a = (k < 6) ? legbase + 5 - k : k - 6;
+      V3 w{s.u.fac.S[a][0], s.u.fac.S[a][1], s.u.fac.S[a][2]};
+      V3 lv{s.u.fac.S[a][3], s.u.fac.S[a][4], s.u.fac.S[a][5]};
+      V3 jc = vadd(cross(w, r), lv);
+      const float e0 = jc.z, e1 = mu * jc.y, e2 = -mu * jc.x;
+      s.Eb[c][0][k] = e0; s.Eb[c][1][k] = e1; s.Eb[c][2][k] = e2;
+      const float qd = s.qvel[a];
+      v0 += e0 * qd; v1 += e1 * qd; v2 += e2 * qd;
+    }
+    const float dmax = MF::foot_solimp[1], tc = MF::foot_solref[0], dr = MF::foot_solref[1];
+    const float bcoef = 2.f / (dmax * tc);
+    const float kcoef = 1.f / (dmax * dmax * tc * tc * dr * dr);
+    const float pyr = (1.f + mu * mu) * (2.f * mu * mu / MF::foot_impratio);
+    const float pen = s.con[c][3], imp = foot_impedance(pen);
+    s.Rc[c] = s.con_w0[c] * pyr * (1.f - imp) / imp;
+    const float kip = kcoef * imp * pen;
+    s.aref[4 * c + 0] = -bcoef * (v0 + v1) - kip;
+    s.aref[4 * c + 1] = -bcoef * (v0 - v1) - kip;
+    s.aref[4 * c + 2] = -bcoef * (v0 + v2) - kip;
+    s.aref[4 * c + 3] = -bcoef * (v0 - v2) - kip;
+  }
+  __syncthreads();
+
+  // ---------------- PASS 2: M^-1 solves, lane j = column j (reference: src/aba_factor.cuh:121-165)
+  // The traversal is unrolled over the static tree. Articulated bias forces travel as explicit
+  // carries along each chain (arm chains end in the torso 16, leg and waist chains in the pelvis 1);
+  // parents with several children accumulate them in the reference's descending-child order.
+  {
+    const int j = l;
+    const int cj = (j >= 1 && j < kCols) ? (j - 1) / 3 : 0, aj = (j >= 1) ? (j - 1) % 3 : 0;
+    const bool basis = (j >= 1) && (j < kCols) && (cj < ncon);
+    const bool smooth = (j == 0);
+    const bool right = s.con_leg[cj] != 0;
+    const float* eb = s.Eb[cj][aj];
+    // right-hand side entry of dof d, read on demand: tau - bias for the smooth column, the
+    // contact basis row e_{c,a} (12 ancestor dofs) for the basis columns, 0 otherwise
+    auto xrhs = [&](int d) -> float {
+      float v = smooth ? s.u.fac.rhs[d] : 0.f;
+      if (d < 6) return basis ? eb[6 + d] : v;
+      if (d < 12) return (basis && !right) ? eb[11 - d] : v;
+      if (d < 18) return (basis && right) ? eb[17 - d] : v;
+      return v;
+    };
+    float u[kNBody];
+    float car[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float p16[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float p1[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = kNBody - 1; b >= 2; --b) {
+      const int par = body_parent[b], d = b + 4;
+      float pb[6];
+#pragma unroll
+      for (int k = 0; k < 6; ++k) pb[k] = (b == 16) ? p16[k] : (body_nchild[b] == 0 ? 0.f : car[k]);
+      const float* Sd = s.u.fac.S[d];
+      const float* Ub = s.u.fac.U[b];
+      const float ub = xrhs(d) - dot6(Sd, pb);
+      u[b] = ub;
+      const float ud = ub * s.u.fac.invD[b];
+#pragma unroll
+      for (int k = 0; k < 6; ++k) {
+        const float c = pb[k] + Ub[k] * ud;
+        if (par == 16) p16[k] += c;
+        else if (par == 1) p1[k] += c;
+        else car[k] = 0.f + c;
+      }
+      if (par == 16) G1_PIN6(p16);
+      else if (par == 1) G1_PIN6(p1);
+      else G1_PIN6(car);
+      __asm__ volatile("" : "+v"(u[b]));
+    }
+    // free joint: D qdd = x_base - S_base.pA_1 with D = L L'
+    float qdd[6];
+    {
+      float rhs6[6];
+#pragma unroll
+      for (int k = 0; k < 6; ++k) rhs6[k] = xrhs(k) - dot6(s.u.fac.S[k], p1);
+      const float* Lf = s.u.fac.Dfac;
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        float a = rhs6[i];
+#pragma unroll
+        for (int k = 0; k < i; ++k) a -= Lf[i * 6 + k] * qdd[k];
+        qdd[i] = a / Lf[i * 6 + i];
+      }
+#pragma unroll
+      for (int i = 5; i >= 0; --i) {
+        float a = qdd[i];
+#pragma unroll
+        for (int k = i + 1; k < 6; ++k) a -= Lf[k * 6 + i] * qdd[k];
+        qdd[i] = a / Lf[i * 6 + i];
+      }
+    }
+    float* ycol = s.Mm[j < kCols ? j : kCols - 1];
+    const bool wr = j < kCols;
+    float a1[6], a16[6], ac[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      float a = 0.f;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) a += s.u.fac.S[k][i] * qdd[k];
+      a1[i] = 0.f + a;
+      a16[i] = 0.f;
+      ac[i] = 0.f;
+    }
+    if (wr) {
+#pragma unroll
+      for (int k = 0; k < 6; ++k) ycol[k] = qdd[k];
+    }
+    G1_PIN6(a1);
+#pragma unroll
+    for (int b = 2; b < kNBody; ++b) {
+      const int par = body_parent[b], d = b + 4;
+      float ap[6];
+#pragma unroll
+      for (int k = 0; k < 6; ++k) ap[k] = (par == 1) ? a1[k] : (par == 16 ? a16[k] : ac[k]);
+      const float* Ub = s.u.fac.U[b];
+      const float* Sd = s.u.fac.S[d];
+      const float q = (u[b] - dot6(Ub, ap)) * s.u.fac.invD[b];
+      if (wr) ycol[d] = q;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) {
+        ac[k] = ap[k] + Sd[k] * q;
+        if (b == 16) a16[k] = ac[k];
+      }
+      G1_PIN6(ac);
+    }
+  }
+  __syncthreads();
+
+  if (ncon_max == 0) {
+    if (base) {
+#pragma unroll
+      for (int k = 0; k < 6; ++k) bqacc[k] = s.Mm[0][k];
+    }
+    jqacc = L.hinge ? s.Mm[0][L.b + 4] : 0.f;
+    __syncthreads();
+    return ncon;
+  }
+
+  // ---------------- Gram blocks + b (reference: src/env_qacc.cuh:154-192); G aliases the factor
+  float bb0 = 0.f, bb1 = 0.f, bb2 = 0.f;
+  if (l < ncon) {
+    const int legbase = s.con_leg[l] ? 12 : 6;
+#pragma unroll
+    for (int k = 0; k < kContactDofs; ++k) {
+      const int a = (k < 6) ? legbase + 5 - k : k - 6;
+      const float qa = s.Mm[0][a];
+      bb0 += s.Eb[l][0][k] * qa; bb1 += s.Eb[l][1][k] * qa; bb2 += s.Eb[l][2][k] * qa;
+    }
+  }
+  __syncthreads();   // factor region is dead from here on: the Gram blocks overwrite it
+  {
+    const int j = l;
+    const int cp = (j >= 1) ? (j - 1) / 3 : 0, bcol = (j >= 1) ? (j - 1) % 3 : 0;
+    const bool active = (j >= 1) && (cp < ncon);
+#pragma unroll 1
+    for (int c = 0; c < ncon_max; ++c) {
+      if (active && c <= cp) {
+        const int legbase = s.con_leg[c] ? 12 : 6;
+        float g0 = 0.f, g1 = 0.f, g2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < kContactDofs; ++k) {
+          const int a = (k < 6) ? legbase + 5 - k : k - 6;
+          const float mv = s.Mm[j][a];
+          g0 += s.Eb[c][0][k] * mv; g1 += s.Eb[c][1][k] * mv; g2 += s.Eb[c][2][k] * mv;
+        }
+        const int pr = cp * (cp + 1) / 2 + c;
+        s.u.G[pr][0 * 3 + bcol] = g0; s.u.G[pr][1 * 3 + bcol] = g1; s.u.G[pr][2 * 3 + bcol] = g2;
+      }
+    }
+  }
+  if (l < ncon) {
+    s.bvec[4 * l + 0] = 1.f * bb0 + 1.f * bb1 + 0.f * bb2 - s.aref[4 * l + 0];
+    s.bvec[4 * l + 1] = 1.f * bb0 + -1.f * bb1 + 0.f * bb2 - s.aref[4 * l + 1];
+    s.bvec[4 * l + 2] = 1.f * bb0 + 0.f * bb1 + 1.f * bb2 - s.aref[4 * l + 2];
+    s.bvec[4 * l + 3] = 1.f * bb0 + 0.f * bb1 + -1.f * bb2 - s.aref[4 * l + 3];
+  }
+  __syncthreads();
+
+  // ---------------- A column of row-lane i (reference: src/env_qacc.cuh:154-190); pyramid
+  // directions d0=(1,1,0) d1=(1,-1,0) d2=(1,0,1) d3=(1,0,-1). For a pair c < c' the reference
+  // expands d_k' G[c][c'] d_k'' once and mirrors it; within one contact it keeps the value
+  // computed with (k, k') = (larger, smaller).
+  const int nefc = 4 * ncon, nefc_max = 4 * ncon_max;
+  const int ci = l >> 2, ki = l & 3;
+  const bool row = l < nefc;
+  auto dcoef = [](int k, int a) -> float {
+    return a == 0 ? 1.f : (a == 1 ? (k == 0 ? 1.f : (k == 1 ? -1.f : 0.f)) : (k == 2 ? 1.f : (k == 3 ? -1.f : 0.f)));
+  };
+  float Acol[kMaxEfc];
+#pragma unroll
+  for (int ii = 0; ii < kMaxEfc; ++ii) {
+    const int c2 = ii >> 2, k2 = ii & 3;
+    float val = 0.f;
+    if (row && ii < nefc) {
+      int lo, hi, klo, khi;
+      if (c2 < ci) { lo = c2; hi = ci; klo = k2; khi = ki; }
+      else if (c2 > ci) { lo = ci; hi = c2; klo = ki; khi = k2; }
+      else { lo = ci; hi = ci; klo = ki > k2 ? ki : k2; khi = ki > k2 ? k2 : ki; }
+      const float* G = s.u.G[hi * (hi + 1) / 2 + lo];
+      const float d0 = dcoef(klo, 0), d1 = dcoef(klo, 1), d2 = dcoef(klo, 2);
+      const float t0 = d0 * G[0] + d1 * G[3] + d2 * G[6];
+      const float t1 = d0 * G[1] + d1 * G[4] + d2 * G[7];
+      const float t2 = d0 * G[2] + d1 * G[5] + d2 * G[8];
+      val = t0 * dcoef(khi, 0) + t1 * dcoef(khi, 1) + t2 * dcoef(khi, 2);
+      if (ii == l) val += s.Rc[ci];
+    }
+    Acol[ii] = val;
+  }
+  const float bi = row ? s.bvec[l] : 0.f;
+  float Aii = 1.f;
+#pragma unroll
+  for (int ii = 0; ii < kMaxEfc; ++ii) Aii = (ii == l && row) ? Acol[ii] : Aii;
+
+  // ---------------- projected Gauss-Seidel (reference: src/contact.cuh:159-171)
+  float fi = 0.f;
+#pragma unroll 1
+  for (int it = 0; it < P.pgs; ++it) {
+#pragma unroll
+    for (int ii = 0; ii < kMaxEfc; ++ii) {
+      if (ii < nefc_max) {
+        const float sum = gsum(Acol[ii] * fi);   // sum_j A[ii][j] f_j (lane j holds column j)
+        if (l == ii && row) {
+          const float ri = (bi + sum) - Aii * fi;
+          const float fn = -ri / Aii;
+          fi = fn > 0.f ? fn : 0.f;
+        }
+      }
+    }
+  }
+  if (row) s.f[l] = fi;
+  __syncthreads();
+
+  // ---------------- qacc = qacc_smooth + sum_c sum_a fb_c[a] m_{c,a} (reference: src/env_qacc.cuh:196-211)
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int d = pass == 0 ? l : kGroup + l;
+    if (d < kNV) {
+      float dq = 0.f;
+#pragma unroll 1
+      for (int c = 0; c < ncon; ++c) {
+        const float f0 = s.f[4 * c], f1 = s.f[4 * c + 1], f2 = s.f[4 * c + 2], f3 = s.f[4 * c + 3];
+        const float fb0 = f0 + f1 + f2 + f3, fb1 = f0 - f1, fb2 = f2 - f3;
+        dq += fb0 * s.Mm[1 + 3 * c][d] + fb1 * s.Mm[2 + 3 * c][d] + fb2 * s.Mm[3 + 3 * c][d];
+      }
+      s.qacc[d] = s.Mm[0][d] + dq;
+    }
+  }
+  __syncthreads();
+  if (base) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) bqacc[k] = s.qacc[k];
+  }
+  jqacc = L.hinge ? s.qacc[L.b + 4] : 0.f;
+  __syncthreads();
+  return ncon;
+}
+
+// ================================================================ Euler + position integration
+// v += dt qacc with the reference's NaN/clamp guard (src/g1_env.cu:154-160), then q += dt v,
+// base quaternion q <- normalize(q (x) exp(w dt)) (src/dynamics.cuh:333-355).
+__device__ __forceinline__ void integrate_lane(const LaneModel& L, LaneState& st, const float (&bqacc)[6], float jqacc,
+                                               bool guard) {
+  const float dt = MF::dt;
+  auto upd = [&](float v, float a) {
+    float n = v + dt * a;
+    if (guard) {
+      if (!isfinite(n)) n = 0.f;
+      if (n > 50.f) n = 50.f; else if (n < -50.f) n = -50.f;
+    }
+    return n;
+  };
+  if (L.hinge) {
+    st.jqd = upd(st.jqd, jqacc);
+    st.jq += dt * st.jqd;
+  }
+  if (L.l == 1) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) st.bqd[k] = upd(st.bqd[k], bqacc[k]);
+    st.bq[0] += dt * st.bqd[0]; st.bq[1] += dt * st.bqd[1]; st.bq[2] += dt * st.bqd[2];
+    V3 v{st.bqd[3] * dt, st.bqd[4] * dt, st.bqd[5] * dt};
+    const float ang = sqrtf(v.x * v.x + v.y * v.y + v.z * v.z);
+    Q4 dq;
+    if (ang < 1e-9f) dq = {1.f, 0.5f * v.x, 0.5f * v.y, 0.5f * v.z};
+    else {
+      const float sn = sinf(0.5f * ang) / ang;
+      dq = {cosf(0.5f * ang), v.x * sn, v.y * sn, v.z * sn};
+    }
+    Q4 qn = qnorm(qmul(Q4{st.bq[3], st.bq[4], st.bq[5], st.bq[6]}, dq));
+    st.bq[3] = qn.w; st.bq[4] = qn.x; st.bq[5] = qn.y; st.bq[6] = qn.z;
+  }
+}
+
+}  // namespace g1k

@@ -536,7 +536,7 @@ template <class R> struct ContactDebug {
 // coefficient (model value 0.6; configurable for the contact-only benchmark configuration).
 template <class R>
 int env_qacc(const R* qp, const R* qv, const Frames<R>& F, const R* tau, const R* Bdt, R* S, R* qacc, int pgs,
-             R mu, ContactDebug<R>* dbg = nullptr) {
+             R mu, ContactDebug<R>* dbg = nullptr, bool contact = true) {
   (void)qp;
   R bias[kNV], negbias[kNV], qacc_s[kNV];
   compute_bias(qv, F, S, bias);
@@ -547,6 +547,10 @@ int env_qacc(const R* qp, const R* qv, const Frames<R>& F, const R* tau, const R
   for (int i = 0; i < kNV; ++i) rhs[i] = negbias[i] + tau[i];
   solveM(fac, S, rhs, qacc_s);
   if (dbg) { std::memcpy(dbg->qacc_smooth, qacc_s, sizeof(qacc_s)); dbg->ncon = 0; }
+  if (!contact) {   // smooth-only evaluation (no foot contacts)
+    for (int i = 0; i < kNV; ++i) qacc[i] = qacc_s[i];
+    return 0;
+  }
 
   // detect: 8 foot spheres vs the z = 0 plane (reference: src/contact.cuh:31-46)
   int cbody[kNFoot]; R cpt[kNFoot][3], cpen[kNFoot], invw0[kNFoot];
@@ -922,13 +926,13 @@ template <class R> static void solve_batch(int n, const R* qpos, const R* Bdt, c
 }
 template <class R>
 static void qacc_batch(int n, const R* qpos, const R* qvel, const R* tau, const R* Bdt, int pgs, R mu, R* qacc,
-                       int* ncon, int nthreads) {
+                       int* ncon, int nthreads, int contact) {
 #pragma omp parallel for num_threads(nthreads) schedule(dynamic, 16)
   for (int w = 0; w < n; ++w) {
     Frames<R> F; R S[kNV * 6];
     fk(qpos + (long)w * kNQ, F.xpos, F.xquat, F.xipos);
     int nc = env_qacc(qpos + (long)w * kNQ, qvel + (long)w * kNV, F, tau + (long)w * kNV, Bdt, S, qacc + (long)w * kNV,
-                      pgs, mu);
+                      pgs, mu, (ContactDebug<R>*)nullptr, contact != 0);
     if (ncon) ncon[w] = nc;
   }
 }
@@ -1040,9 +1044,11 @@ void orc_mass_d(int n, const double* q, double* Mo) { mass_batch(n, q, Mo); }
 void orc_solve_f(int n, const float* q, const float* Bdt, const float* x, float* y, int multi) { solve_batch(n, q, Bdt, x, y, multi); }
 void orc_solve_d(int n, const double* q, const double* Bdt, const double* x, double* y, int multi) { solve_batch(n, q, Bdt, x, y, multi); }
 void orc_qacc_f(int n, const float* q, const float* v, const float* tau, const float* Bdt, int pgs, float mu, float* qacc,
-                int* ncon, int nthreads) { qacc_batch(n, q, v, tau, Bdt, pgs, mu, qacc, ncon, nthreads); }
+                int* ncon, int nthreads, int contact) { qacc_batch(n, q, v, tau, Bdt, pgs, mu, qacc, ncon, nthreads, contact); }
 void orc_qacc_d(int n, const double* q, const double* v, const double* tau, const double* Bdt, int pgs, double mu,
-                double* qacc, int* ncon, int nthreads) { qacc_batch(n, q, v, tau, Bdt, pgs, mu, qacc, ncon, nthreads); }
+                double* qacc, int* ncon, int nthreads, int contact) {
+  qacc_batch(n, q, v, tau, Bdt, pgs, mu, qacc, ncon, nthreads, contact);
+}
 void orc_substep_f(int n, float* q, float* v, const float* target, int pgs, float mu, float* qacc, int* ncon,
                    int nthreads) { substep_batch(n, q, v, target, pgs, mu, qacc, ncon, nthreads); }
 void orc_substep_d(int n, double* q, double* v, const double* target, int pgs, double mu, double* qacc, int* ncon,

@@ -35,7 +35,7 @@ def _load():
         getattr(lib, f"orc_mass_{suf}").argtypes = [_c.c_int, fp, fp]
         getattr(lib, f"orc_solve_{suf}").argtypes = [_c.c_int, fp, _c.c_void_p, fp, fp, _c.c_int]
         getattr(lib, f"orc_qacc_{suf}").argtypes = [_c.c_int, fp, fp, fp, _c.c_void_p, _c.c_int, real, fp,
-                                                    _c.c_void_p, _c.c_int]
+                                                    _c.c_void_p, _c.c_int, _c.c_int]
         getattr(lib, f"orc_substep_{suf}").argtypes = [_c.c_int, fp, fp, fp, _c.c_int, real, _c.c_void_p,
                                                        _c.c_void_p, _c.c_int]
         getattr(lib, f"orc_pgs_{suf}").argtypes = [_c.c_int, fp, fp, fp, _c.c_int]
@@ -115,14 +115,14 @@ def solve(qpos, x, Bdt=None, multi=False, dtype=np.float64):
     return y
 
 
-def qacc(qpos, qvel, tau=None, Bdt=None, pgs=8, mu=MU_MODEL, dtype=np.float32, threads=1):
+def qacc(qpos, qvel, tau=None, Bdt=None, pgs=8, mu=MU_MODEL, dtype=np.float32, threads=1, contact=True):
     q = _arr(np.atleast_2d(qpos), dtype); v = _arr(np.atleast_2d(qvel), dtype)
     n = q.shape[0]
     t = np.zeros((n, NV), dtype) if tau is None else _arr(np.atleast_2d(tau), dtype)
     B = None if Bdt is None else _arr(Bdt, dtype)
     out = np.zeros((n, NV), dtype); nc = np.zeros(n, np.int32)
     getattr(lib(), f"orc_qacc_{_dt(dtype)}")(n, q, v, t, None if B is None else B.ctypes.data, pgs, mu, out,
-                                             nc.ctypes.data, threads)
+                                             nc.ctypes.data, threads, int(contact))
     return out, nc
 
 

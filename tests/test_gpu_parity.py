@@ -1,0 +1,178 @@
+"""GPU parity of the HIP path (libg1env.so, called through its C ABI) against the CPU oracle and the
+reference's fixtures. Tolerances: fp32 per-state ||a-b||/||b|| <= 1e-5 on teacher-forced qacc
+(the reference's own gate, src/test_envqacc.cu:74-90); MuJoCo contact fixture <= 3e-5 at 2000 PGS
+sweeps (reference worst 2.24e-5)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import relerr_rows, load_contact_validate
+
+pytestmark = pytest.mark.gpu
+
+TOL_QACC = 1e-5
+
+
+@pytest.fixture(scope="module")
+def g1():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import ppo
+    return ppo
+
+
+def _dev(x, dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(x))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def gpu_qacc(g1, qpos, qvel, tau=None, damped=True, contact=True, pgs=8, mu=0.6):
+    import torch
+    n = qpos.shape[0]
+    q = _dev(qpos.astype(np.float32)); v = _dev(qvel.astype(np.float32))
+    t = _dev(np.zeros((n, 35), np.float32) if tau is None else tau.astype(np.float32))
+    out = torch.zeros(n, 35, device="cuda"); nc = torch.zeros(n, dtype=torch.int32, device="cuda")
+    g1._lib.g1_probe_qacc(n, g1._dp(q), g1._dp(v), g1._dp(t), int(damped), int(contact), pgs, mu, g1._dp(out),
+                          g1._dp(nc))
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), nc.cpu().numpy()
+
+
+def envqacc_states(n, seed=999):
+    """The reference gate's state family (src/test_envqacc.cu:29-39): stand pose + U(-0.2,0.2) on
+    every qpos entry, base dropped up to 0.15 m, renormalised quaternion, qvel U(-1,1)."""
+    import g1_model as gm
+    rng = np.random.default_rng(seed)
+    qp = (gm.qpos_stand.astype(np.float32)[None] + 0.2 * (rng.random((n, 36), np.float32) * 2 - 1)).astype(np.float32)
+    qp[:, 2] -= 0.15 * rng.random(n, np.float32)
+    qp[:, 3:7] /= np.linalg.norm(qp[:, 3:7], axis=1, keepdims=True)
+    qv = (rng.random((n, 35), np.float32) * 2 - 1).astype(np.float32)
+    return qp, qv
+
+
+def test_env_qacc_gate_states(g1, orc):
+    """Teacher-forced env_qacc (zero torque, implicit kd damping, pgs=8) on the reference gate's
+    random-state family, worst per-state relerr <= 1e-5."""
+    qp, qv = envqacc_states(4096)
+    Bdt = orc.bdt(np.float32)
+    ref, nref = orc.qacc(qp, qv, Bdt=Bdt, pgs=8, mu=0.6, dtype=np.float32, threads=8)
+    out, nc = gpu_qacc(g1, qp, qv, pgs=8, mu=0.6)
+    assert np.array_equal(nc, nref)
+    assert (nref > 0).mean() > 0.5     # the family exercises the contact path
+    rel = relerr_rows(out, ref)
+    print(f"env_qacc gate: worst relerr {rel.max():.3e}, median {np.median(rel):.3e}, contact share {(nref>0).mean():.2f}")
+    assert rel.max() <= TOL_QACC
+
+
+@pytest.mark.parametrize("mu", [0.6, 1.0])
+def test_contact_config_states(g1, orc, mu):
+    """Config-2 states (0..8 penetrating spheres, tangential foot velocity) at pgs=8."""
+    import configs
+    qp, qv, k = configs.config2(lambda q: orc.fk(q, dtype=np.float64), n=2048)
+    Bdt = orc.bdt(np.float32)
+    ref, nref = orc.qacc(qp, qv, Bdt=Bdt, pgs=8, mu=mu, dtype=np.float32, threads=8)
+    out, nc = gpu_qacc(g1, qp, qv, pgs=8, mu=mu)
+    assert np.array_equal(nc, nref)
+    assert set(np.unique(nref)) >= {0, 4, 8}
+    rel = relerr_rows(out, ref)
+    print(f"config2 mu={mu}: worst relerr {rel.max():.3e}; ncon hist {np.bincount(nref, minlength=9)}")
+    assert rel.max() <= TOL_QACC
+
+
+def test_smooth_qacc_config0(g1, orc):
+    """No contact, plain M^-1 (tau - bias) on config-0 states: vs fp32 and fp64 oracle."""
+    import configs
+    qp, qv, tau = configs.config0()
+    ref32, _ = orc.qacc(qp, qv, tau=tau, pgs=0, dtype=np.float32, contact=False)
+    ref64, _ = orc.qacc(qp, qv, tau=tau, pgs=0, dtype=np.float64, contact=False)
+    out, _ = gpu_qacc(g1, qp, qv, tau=tau, damped=False, contact=False)
+    r32, r64 = relerr_rows(out, ref32), relerr_rows(out, ref64)
+    print(f"config0 smooth: vs fp32 oracle {r32.max():.3e}, vs fp64 oracle {r64.max():.3e}")
+    assert r32.max() <= TOL_QACC
+    assert r64.max() <= 1e-4
+
+
+def test_smooth_qacc_vs_mujoco(g1, ref_traj):
+    sel = ref_traj["sel"]
+    prev = np.maximum(sel - 1, 0)
+    out, nc = gpu_qacc(g1, ref_traj["qpos"][prev], ref_traj["qvel"][prev], damped=False, contact=True)
+    assert (nc == 0).all()
+    rel = relerr_rows(out, ref_traj["qacc"])
+    print(f"smooth qacc vs MuJoCo: worst {rel.max():.3e}")
+    assert rel.max() <= 2e-5
+
+
+def test_contact_vs_mujoco_fixture(g1):
+    """Pure foot-ground states at 2000 PGS sweeps vs MuJoCo's qacc (reference worst 2.24e-5)."""
+    cv = load_contact_validate()
+    out, nc = gpu_qacc(g1, cv["qpos"], cv["qvel"], damped=False, contact=True, pgs=2000, mu=0.6)
+    assert list(nc) == [0, 0, 0, 8, 8, 4, 8, 8, 8]
+    rel = relerr_rows(out, cv["qacc"])
+    print("contact_validate relerr:", np.array2string(rel, precision=2))
+    assert rel.max() <= 3e-5
+
+
+def test_substep_teacher_forced(g1, orc):
+    """One env substep (FK -> clamped PD -> qacc -> guarded Euler -> integration) on config-2 states
+    with random PD targets: qacc relerr <= 1e-5, next-state deviation at rounding level."""
+    import torch
+    import configs
+    import g1_model as gm
+    qp, qv, _ = configs.config2(lambda q: orc.fk(q, dtype=np.float64), n=1024, seed=5)
+    rng = np.random.default_rng(6)
+    tg = (gm.qpos_stand[7:][None] + 0.5 * rng.uniform(-1, 1, (1024, 29))).astype(np.float32)
+    tg = np.clip(tg, gm.act_ctrl_lo, gm.act_ctrl_hi).astype(np.float32)
+    q1, v1, qa_ref, n_ref = orc.substep(qp, qv, tg, pgs=8, mu=0.6, threads=8)
+    q = _dev(qp.astype(np.float32)); v = _dev(qv.astype(np.float32)); t = _dev(tg)
+    qa = torch.zeros(1024, 35, device="cuda"); nc = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    g1._lib.g1_probe_substep(1024, g1._dp(q), g1._dp(v), g1._dp(t), 1, 8, 0.6, g1._dp(qa), g1._dp(nc))
+    torch.cuda.synchronize()
+    assert np.array_equal(nc.cpu().numpy(), n_ref)
+    rel = relerr_rows(qa.cpu().numpy(), qa_ref)
+    dq = np.abs(q.cpu().numpy() - q1).max()
+    dv = relerr_rows(v.cpu().numpy(), v1).max()
+    print(f"substep: qacc worst {rel.max():.3e}, qpos maxabs {dq:.3e}, qvel worst rel {dv:.3e}")
+    assert rel.max() <= TOL_QACC
+    assert dq <= 1e-6 and dv <= 1e-5
+
+
+@pytest.mark.parametrize("hidden,act", [((256, 256), 0), ((512, 512, 256), 1)])
+def test_policy_mlp(g1, orc, hidden, act):
+    """Policy MLP on fp32 MFMA vs the oracle's serial MLP and torch (config 3 and config 4 shapes)."""
+    import torch
+    import configs
+    rng = np.random.default_rng(3)
+    W = configs.policy_init(rng, hidden=hidden)
+    n = 1000
+    x = np.clip(rng.normal(0, 1.5, (n, 100)), -10, 10).astype(np.float32)
+    mu_ref, _, v_ref = orc.mlp(W, x, hidden=hidden, act=act)
+    mu = torch.zeros(n, 29, device="cuda"); v = torch.zeros(n, device="cuda")
+    h = np.asarray(hidden, np.int32)
+    rc = g1._lib.g1_probe_policy(n, len(hidden), h.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), act,
+                                 g1._dp(_dev(W)), g1._dp(_dev(x)), g1._dp(mu), g1._dp(v))
+    assert rc == 0
+    mu = mu.cpu().numpy(); v = v.cpu().numpy()
+    rm = relerr_rows(mu, mu_ref)
+    rv = np.abs(v - v_ref) / (np.abs(v_ref) + 1e-3)
+    print(f"mlp {hidden}: mu worst relerr {rm.max():.3e}, v worst {rv.max():.3e}")
+    assert rm.max() <= 1e-5 and rv.max() <= 1e-5
+
+
+def test_philox_known_answers(g1):
+    """Philox4x32-10 known-answer vectors (Random123 kat_vectors)."""
+    import torch
+    ctr = np.array([[0, 0, 0, 0], [0xffffffff] * 4, [0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344]], np.uint32)
+    keys = [(0, 0), (0xffffffff, 0xffffffff), (0xa4093822, 0x299f31d0)]
+    want = [[0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8], [0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd],
+            [0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1]]
+    for i, (k0, k1) in enumerate(keys):
+        c = torch.from_numpy(ctr[i:i + 1].view(np.int32).copy()).cuda()
+        o = torch.zeros(4, dtype=torch.int32, device="cuda")
+        g1._lib.g1_probe_philox(1, g1._dp(c), g1._dp(o), k0, k1)
+        got = o.cpu().numpy().view(np.uint32)
+        assert list(got) == want[i], [hex(x) for x in got]
