@@ -37,7 +37,7 @@ def cpu_baseline(cfg, threads, seed=0):
     import configs
     oracle.build()
     rng = np.random.default_rng(seed)
-    n = 512 if cfg["N"] >= 512 else cfg["N"]
+    n = min(4096, cfg["N"])
     H, S = cfg["H"], cfg["S"]
     qp, qv, pa, st = configs.reset_states(rng, n)
     W = configs.policy_init(rng, hidden=cfg["hidden"])

@@ -52,8 +52,17 @@ __device__ __forceinline__ V3 qrot(Q4 q, V3 v) {
   return {v.x + q.w * t.x + (u.y * t.z - u.z * t.y), v.y + q.w * t.y + (u.z * t.x - u.x * t.z),
           v.z + q.w * t.z + (u.x * t.y - u.y * t.x)};
 }
+// Correctly rounded fp32 transcendentals (evaluated in fp64, rounded once; fp64 VALU runs at the
+// fp32 rate on CDNA4 and these sit outside the inner loops). The contact force is stiff in the
+// foot height, so a 1-ulp difference in an FK rotation moves qacc by up to ~1e-4 relative on
+// shallow penetrations; correct rounding makes every transcendental reproducible bit-for-bit.
+__device__ __forceinline__ float sin_rn(float x) { return (float)sin((double)x); }
+__device__ __forceinline__ float cos_rn(float x) { return (float)cos((double)x); }
+__device__ __forceinline__ float pow_rn(float x, float y) { return (float)pow((double)x, (double)y); }
+__device__ __forceinline__ float rsqrt_rn(float x) { return 1.f / sqrtf(x); }
+
 __device__ __forceinline__ Q4 qnorm(Q4 q) {
-  float n = rsqrtf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+  float n = rsqrt_rn(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
   return {q.w * n, q.x * n, q.y * n, q.z * n};
 }
 struct M3 { float m[9]; };
@@ -96,9 +105,9 @@ __device__ __forceinline__ float foot_impedance(float pos) {
   float y;
   if (x >= 1.f) y = 1.f;
   else {
-    float a = 1.f / powf(mid, power - 1.f);
-    float b = 1.f / powf(1.f - mid, power - 1.f);
-    y = (x < mid) ? a * powf(x, power) : 1.f - b * powf(1.f - x, power);
+    float a = 1.f / pow_rn(mid, power - 1.f);
+    float b = 1.f / pow_rn(1.f - mid, power - 1.f);
+    y = (x < mid) ? a * pow_rn(x, power) : 1.f - b * pow_rn(1.f - x, power);
   }
   return dmin + y * (dmax - dmin);
 }
@@ -211,8 +220,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   }
   Q4 aa;
   {
-    float h = 0.5f * st.jq, sn = sinf(h);
-    aa = {cosf(h), L.axis.x * sn, L.axis.y * sn, L.axis.z * sn};
+    float h = 0.5f * st.jq, sn = sin_rn(h);
+    aa = {cos_rn(h), L.axis.x * sn, L.axis.y * sn, L.axis.z * sn};
   }
 #pragma unroll 1
   for (int r = 2; r <= kMaxDepth; ++r) {
@@ -806,8 +815,8 @@ __device__ __forceinline__ void integrate_lane(const LaneModel& L, LaneState& st
     Q4 dq;
     if (ang < 1e-9f) dq = {1.f, 0.5f * v.x, 0.5f * v.y, 0.5f * v.z};
     else {
-      const float sn = sinf(0.5f * ang) / ang;
-      dq = {cosf(0.5f * ang), v.x * sn, v.y * sn, v.z * sn};
+      const float sn = sin_rn(0.5f * ang) / ang;
+      dq = {cos_rn(0.5f * ang), v.x * sn, v.y * sn, v.z * sn};
     }
     Q4 qn = qnorm(qmul(Q4{st.bq[3], st.bq[4], st.bq[5], st.bq[6]}, dq));
     st.bq[3] = qn.w; st.bq[4] = qn.x; st.bq[5] = qn.y; st.bq[6] = qn.z;

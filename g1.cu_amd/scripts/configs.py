@@ -73,7 +73,8 @@ def config2(fk, seed=2, n=8192):
     k = rng.integers(0, 9, size=n)
     depth = rng.uniform(0.0, 0.005, size=n)
     h = np.sort(_foot_bottoms(qpos, fk), axis=1)
-    shift = np.where(k == 0, -h[:, 0] + depth + 1e-4, -h[:, np.maximum(k - 1, 0)] - depth)
+    kth = h[np.arange(n), np.maximum(k - 1, 0)]
+    shift = np.where(k == 0, -h[:, 0] + depth + 1e-4, -kth - depth)
     qpos[:, 2] += shift
     return qpos, qvel, k
 

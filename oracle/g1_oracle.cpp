@@ -58,6 +58,12 @@ template <class R> static inline V3<R> qrot(Q4<R> q, V3<R> v) {
           v.y + q.w * t.y + (u.z * t.x - u.x * t.z),
           v.z + q.w * t.z + (u.x * t.y - u.y * t.x)};
 }
+// fp32 transcendentals are correctly rounded (evaluated in fp64, rounded once), so every
+// implementation of the algorithm that does the same yields bit-identical values: the contact
+// force is stiff in the foot height and amplifies 1-ulp differences in FK rotations.
+template <class R> static inline R sin_(R x) { return R(std::sin(double(x))); }
+template <class R> static inline R cos_(R x) { return R(std::cos(double(x))); }
+template <class R> static inline R pow_(R x, R y) { return R(std::pow(double(x), double(y))); }
 template <class R> static inline R rsqrt_(R x) { return R(1) / std::sqrt(x); }
 // (reference: src/dynamics.cuh:36-39)
 template <class R> static inline Q4<R> qnorm(Q4<R> q) {
@@ -66,8 +72,8 @@ template <class R> static inline Q4<R> qnorm(Q4<R> q) {
 }
 // (reference: src/dynamics.cuh:40-43)
 template <class R> static inline Q4<R> axisangle(V3<R> a, R ang) {
-  R h = R(0.5) * ang, s = std::sin(h);
-  return {std::cos(h), a.x * s, a.y * s, a.z * s};
+  R h = R(0.5) * ang, s = sin_(h);
+  return {cos_(h), a.x * s, a.y * s, a.z * s};
 }
 
 template <class R> struct M3 { R m[9]; };
@@ -503,9 +509,9 @@ template <class R> R foot_impedance(R pos) {
   R y;
   if (x >= R(1)) y = 1;
   else {
-    R a = R(1) / std::pow(mid, power - R(1));
-    R b = R(1) / std::pow(R(1) - mid, power - R(1));
-    y = (x < mid) ? a * std::pow(x, power) : R(1) - b * std::pow(R(1) - x, power);
+    R a = R(1) / pow_(mid, power - R(1));
+    R b = R(1) / pow_(R(1) - mid, power - R(1));
+    y = (x < mid) ? a * pow_(x, power) : R(1) - b * pow_(R(1) - x, power);
   }
   return dmin + y * (dmax - dmin);
 }
@@ -690,8 +696,8 @@ template <class R> void quat_integrate(R* q, V3<R> w, R dt) {
   Q4<R> dq;
   if (ang < R(1e-9)) dq = {R(1), R(0.5) * v.x, R(0.5) * v.y, R(0.5) * v.z};
   else {
-    R s = std::sin(R(0.5) * ang) / ang;
-    dq = {std::cos(R(0.5) * ang), v.x * s, v.y * s, v.z * s};
+    R s = sin_(R(0.5) * ang) / ang;
+    dq = {cos_(R(0.5) * ang), v.x * s, v.y * s, v.z * s};
   }
   Q4<R> qn = qnorm(qmul(Q4<R>{q[0], q[1], q[2], q[3]}, dq));
   q[0] = qn.w; q[1] = qn.x; q[2] = qn.y; q[3] = qn.z;
