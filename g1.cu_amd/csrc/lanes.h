@@ -1,9 +1,8 @@
 // Lane-group primitives for the world-per-32-lanes mapping on CDNA4 (wave64 = two worlds).
 //
 // A "group" is the 32 lanes of one half of a wave64; each group owns one world. Cross-lane
-// traffic goes through ds_bpermute (__shfl) restricted to the group, and the butterfly sum gives
-// every lane of the group the bit-identical result (IEEE addition is commutative, and each
-// butterfly stage combines the same two partial sums on both partner lanes).
+// gathers go through ds_bpermute (__shfl) restricted to the group; the group sum runs on DPP and
+// v_permlane16_swap (VALU latency) and gives every lane of the group the bit-identical result.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -17,9 +16,26 @@ __device__ __forceinline__ int group_id() { return threadIdx.x >> 5; }
 __device__ __forceinline__ float gshfl(float v, int src) { return __shfl(v, src, kGroup); }
 __device__ __forceinline__ int gshfl(int v, int src) { return __shfl(v, src, kGroup); }
 
+// Row rotate (DPP row_ror:N): lane i of each 16-lane row reads lane (i - N) mod 16 of its row.
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false));
+}
+
+// Sum over the 32 lanes of the group, the same value in every lane. Stage 1 adds the partner
+// row (lane i and i^16) with v_permlane16_swap, which exchanges rows 0<->1 and 2<->3 between two
+// registers; stages 2-5 add row rotations by 8, 4, 2, 1. After the stage that rotates by m the
+// partial sums are periodic with period m within the row, so lane i's partner (i - m) mod 16
+// holds the same partial sum as lane i ^ m: every stage adds exactly the operands of the xor
+// butterfly (16, 8, 4, 2, 1), and since IEEE addition is commutative the result is bit-identical
+// to that butterfly in every lane, without a round trip through the LDS crossbar.
 __device__ __forceinline__ float gsum(float v) {
-#pragma unroll
-  for (int m = kGroup / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kGroup);
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
   return v;
 }
 

@@ -58,7 +58,6 @@ __device__ __forceinline__ V3 qrot(Q4 q, V3 v) {
 // shallow penetrations; correct rounding makes every transcendental reproducible bit-for-bit.
 __device__ __forceinline__ float sin_rn(float x) { return (float)sin((double)x); }
 __device__ __forceinline__ float cos_rn(float x) { return (float)cos((double)x); }
-__device__ __forceinline__ float pow_rn(float x, float y) { return (float)pow((double)x, (double)y); }
 __device__ __forceinline__ float rsqrt_rn(float x) { return 1.f / sqrtf(x); }
 
 __device__ __forceinline__ Q4 qnorm(Q4 q) {
@@ -105,9 +104,12 @@ __device__ __forceinline__ float foot_impedance(float pos) {
   float y;
   if (x >= 1.f) y = 1.f;
   else {
-    float a = 1.f / pow_rn(mid, power - 1.f);
-    float b = 1.f / pow_rn(1.f - mid, power - 1.f);
-    y = (x < mid) ? a * pow_rn(x, power) : 1.f - b * pow_rn(1.f - x, power);
+    // The model's solimp power is 2: x^2 of a float is exact in fp64, so the correctly rounded
+    // pow(x, 2) is the fp32 product x*x, and mid^(power-1) = mid.
+    static_assert(MF::foot_solimp[4] == 2.f, "impedance power 2 assumed");
+    float a = 1.f / mid;
+    float b = 1.f / (1.f - mid);
+    y = (x < mid) ? a * (x * x) : 1.f - b * ((1.f - x) * (1.f - x));
   }
   return dmin + y * (dmax - dmin);
 }
@@ -121,6 +123,8 @@ struct WorldLds {
       float invD[kNBody];   // hinge 1/(S'I^A S + armature + dt kd)
       float Dfac[36];       // Cholesky factor of the free-joint 6x6 block
       float rhs[kNV + 1];   // smooth right-hand side tau - bias
+      float IA1[21];        // articulated inertia of the pelvis (packed)
+      float Dm[36];         // free-joint 6x6 block before factoring
     } fac;
     float G[kPairs][9];     // 3x3 Gram blocks of contact pairs c <= c' (after the solves)
   } u;
@@ -372,9 +376,12 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       }
     }
   }
+  // smooth right-hand side tau - bias of the lane's dofs (lane 1: the six base dofs, tau = 0)
+  float xr = 0.f, xb[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (L.hinge) {
     const float bias = sw.x * Fw.x + sw.y * Fw.y + sw.z * Fw.z + sv.x * Fv.x + sv.y * Fv.y + sv.z * Fv.z;
-    s.u.fac.rhs[L.b + 4] = -bias + jtau;
+    xr = -bias + jtau;
+    s.u.fac.rhs[L.b + 4] = xr;
   }
   if (base) {
 #pragma unroll
@@ -383,8 +390,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const float bt = 0.f * Fw.x + 0.f * Fw.y + 0.f * Fw.z + (k == 0 ? 1.f : 0.f) * Fv.x +
                        (k == 1 ? 1.f : 0.f) * Fv.y + (k == 2 ? 1.f : 0.f) * Fv.z;
       const float br = R1.m[k] * Fw.x + R1.m[3 + k] * Fw.y + R1.m[6 + k] * Fw.z + 0.f * Fv.x + 0.f * Fv.y + 0.f * Fv.z;
-      s.u.fac.rhs[k] = -bt + 0.f;
-      s.u.fac.rhs[3 + k] = -br + 0.f;
+      xb[k] = -bt + 0.f;
+      xb[3 + k] = -br + 0.f;
+      s.u.fac.rhs[k] = xb[k];
+      s.u.fac.rhs[3 + k] = xb[3 + k];
     }
   }
 
@@ -415,9 +424,16 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       for (int j = i; j < 6; ++j) IA[symidx(i, j)] = M6[i * 6 + j];
   }
   const float S6[6] = {sw.x, sw.y, sw.z, sv.x, sv.y, sv.z};
+  // Leaf -> root, fused: articulated-inertia downdate (reference: src/aba_factor.cuh:77-88) and
+  // the leaf -> root sweep of the smooth solve y = (M + dtB)^-1 (tau - bias) (reference:
+  // src/aba_factor.cuh:128-136). pAs is the lane's articulated bias force; children contribute in
+  // the reference's order, so the result is the reference's serial sweep bit for bit.
+  float pAs[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float Uk[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // this body's factor column, kept for root -> leaf
+  float iD = 0.f, us = 0.f;
 #pragma unroll 1
   for (int cd = kMaxDepth; cd >= 2; --cd) {
-    float Dl[21];
+    float Dl[21], cs[6];
     {
       float U[6];
 #pragma unroll
@@ -434,7 +450,16 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       for (int i = 0; i < 6; ++i)
 #pragma unroll
         for (int j = i; j < 6; ++j) Dl[symidx(i, j)] = IA[symidx(i, j)] - U[i] * U[j] * invD;
-      if (L.hinge && L.depth == cd) {
+      const float u = xr - dot6(S6, pAs);
+      const float ud = u * invD;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) cs[k] = pAs[k] + U[k] * ud;
+      const bool mine = (L.depth == cd);
+#pragma unroll
+      for (int k = 0; k < 6; ++k) Uk[k] = mine ? U[k] : Uk[k];
+      iD = mine ? invD : iD;
+      us = mine ? u : us;
+      if (L.hinge && mine) {
 #pragma unroll
         for (int k = 0; k < 6; ++k) s.u.fac.U[L.b][k] = U[k];
         s.u.fac.invD[L.b] = invD;
@@ -446,11 +471,21 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const float g = gshfl(Dl[k], L.c0);
       if (gather && L.nchild > 0) IA[k] += g;
     }
-    if (cd == body_depth[17] || cd == 2) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const float g = gshfl(cs[k], L.c0);
+      if (gather && L.nchild > 0) pAs[k] += g;
+    }
+    if (cd == body_depth[17] || cd == 2) {   // multi-child parents: torso (depth 4), pelvis (depth 1)
 #pragma unroll
       for (int k = 0; k < 21; ++k) {
         const float g = gshfl(Dl[k], L.c1);
         if (gather && L.nchild > 1) IA[k] += g;
+      }
+#pragma unroll
+      for (int k = 0; k < 6; ++k) {
+        const float g = gshfl(cs[k], L.c1);
+        if (gather && L.nchild > 1) pAs[k] += g;
       }
       if (cd == 2) {
 #pragma unroll
@@ -458,32 +493,47 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
           const float g = gshfl(Dl[k], L.c2);
           if (gather && L.nchild > 2) IA[k] += g;
         }
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+          const float g = gshfl(cs[k], L.c2);
+          if (gather && L.nchild > 2) pAs[k] += g;
+        }
       }
     }
   }
-  __syncthreads();   // S complete in LDS
+  // ---------------- free-joint 6x6 block (reference: src/aba_factor.cuh:90-108): lane c < 6
+  // builds column c of U6 = I^A S_base and of D = S_base' U6; lane 1 factors D and solves the
+  // base of the smooth system.
   if (base) {
-    // free-joint 6x6 block: U6 = I^A S_base, D = S_base' U6 (+ armature 0), Cholesky
-    float U6[6][6];
 #pragma unroll
-    for (int c = 0; c < 6; ++c)
+    for (int k = 0; k < 21; ++k) s.u.fac.IA1[k] = IA[k];
+  }
+  __syncthreads();   // S and I^A of the pelvis complete in LDS
+  if (l < 6) {
+    float Sc[6], U6c[6];
 #pragma unroll
-      for (int i = 0; i < 6; ++i) {
-        float a = 0.f;
+    for (int j = 0; j < 6; ++j) Sc[j] = s.u.fac.S[l][j];
 #pragma unroll
-        for (int j = 0; j < 6; ++j) a += IA[symidx(i, j)] * s.u.fac.S[c][j];
-        U6[i][c] = a;
-      }
+    for (int i = 0; i < 6; ++i) {
+      float a = 0.f;
+#pragma unroll
+      for (int j = 0; j < 6; ++j) a += s.u.fac.IA1[symidx(i, j)] * Sc[j];
+      U6c[i] = a;
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < 6; ++i) a += s.u.fac.S[k][i] * U6c[i];
+      s.u.fac.Dm[k * 6 + l] = a + 0.f;   // + armature (0) + dt*damping (0) on the free joint
+    }
+  }
+  __syncthreads();
+  float a6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (base) {
     float Dm[36];
 #pragma unroll
-    for (int k = 0; k < 6; ++k)
-#pragma unroll
-      for (int c = 0; c < 6; ++c) {
-        float a = 0.f;
-#pragma unroll
-        for (int i = 0; i < 6; ++i) a += s.u.fac.S[k][i] * U6[i][c];
-        Dm[k * 6 + c] = a + (k == c ? 0.f : 0.f);
-      }
+    for (int i = 0; i < 36; ++i) Dm[i] = s.u.fac.Dm[i];
 #pragma unroll
     for (int i = 0; i < 6; ++i)
 #pragma unroll
@@ -495,6 +545,51 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       }
 #pragma unroll
     for (int i = 0; i < 36; ++i) s.u.fac.Dfac[i] = Dm[i];
+    // smooth solve, free joint: L L' qdd = x_base - S_base.pA_1 (reference: src/aba_factor.cuh:139-155)
+    float qdd[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      float Sk[6];
+#pragma unroll
+      for (int i = 0; i < 6; ++i) Sk[i] = s.u.fac.S[k][i];
+      qdd[k] = xb[k] - dot6(Sk, pAs);
+    }
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      float a = qdd[i];
+#pragma unroll
+      for (int k = 0; k < i; ++k) a -= Dm[i * 6 + k] * qdd[k];
+      qdd[i] = a / Dm[i * 6 + i];
+    }
+#pragma unroll
+    for (int i = 5; i >= 0; --i) {
+      float a = qdd[i];
+#pragma unroll
+      for (int k = i + 1; k < 6; ++k) a -= Dm[k * 6 + i] * qdd[k];
+      qdd[i] = a / Dm[i * 6 + i];
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k) s.Mm[0][k] = qdd[k];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      float a = 0.f;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) a += s.u.fac.S[k][i] * qdd[k];
+      a6[i] = 0.f + a;
+    }
+  }
+  // ---------------- smooth solve root -> leaf (reference: src/aba_factor.cuh:156-164)
+#pragma unroll 1
+  for (int r = 2; r <= kMaxDepth; ++r) {
+    float ap[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) ap[k] = gshfl(a6[k], L.par);
+    if (L.depth == r) {
+      const float q = (us - dot6(Uk, ap)) * iD;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) a6[k] = ap[k] + S6[k] * q;
+      s.Mm[0][L.b + 4] = q;
+    }
   }
 
   // ---------------- contact detection: lane s = foot sphere s (reference: src/contact.cuh:31-46)
@@ -557,11 +652,11 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // The traversal is unrolled over the static tree. Articulated bias forces travel as explicit
   // carries along each chain (arm chains end in the torso 16, leg and waist chains in the pelvis 1);
   // parents with several children accumulate them in the reference's descending-child order.
-  {
+  if (ncon_max > 0) {
     const int j = l;
     const int cj = (j >= 1 && j < kCols) ? (j - 1) / 3 : 0, aj = (j >= 1) ? (j - 1) % 3 : 0;
     const bool basis = (j >= 1) && (j < kCols) && (cj < ncon);
-    const bool smooth = (j == 0);
+    const bool smooth = false;   // the smooth column was solved by the tree sweeps above
     const bool right = s.con_leg[cj] != 0;
     const float* eb = s.Eb[cj][aj];
     // right-hand side entry of dof d, read on demand: tau - bias for the smooth column, the
@@ -622,8 +717,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         qdd[i] = a / Lf[i * 6 + i];
       }
     }
-    float* ycol = s.Mm[j < kCols ? j : kCols - 1];
-    const bool wr = j < kCols;
+    float* ycol = s.Mm[(j >= 1 && j < kCols) ? j : kCols - 1];
+    const bool wr = j >= 1 && j < kCols;
     float a1[6], a16[6], ac[6];
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
@@ -745,18 +840,25 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   for (int ii = 0; ii < kMaxEfc; ++ii) Aii = (ii == l && row) ? Acol[ii] : Aii;
 
   // ---------------- projected Gauss-Seidel (reference: src/contact.cuh:159-171)
+  // Row ii's update f_ii = max(0, -(b_ii + A_ii.f - A_ii,ii f_ii) / A_ii,ii) is evaluated by every
+  // lane and kept by lane ii only (branch-free). The quotient x / A_ii uses the correctly rounded
+  // reciprocal y = RN(1/A_ii) once per solve and one exact-residual correction per row:
+  // q0 = RN(x y), r = x - A_ii q0 (exact with fma), q = RN(q0 + r y) equals RN(x / A_ii)
+  // (Markstein's theorem), i.e. the IEEE quotient, on a 3-op dependency chain.
   float fi = 0.f;
+  const float yi = 1.f / Aii;
 #pragma unroll 1
   for (int it = 0; it < P.pgs; ++it) {
 #pragma unroll
     for (int ii = 0; ii < kMaxEfc; ++ii) {
       if (ii < nefc_max) {
         const float sum = gsum(Acol[ii] * fi);   // sum_j A[ii][j] f_j (lane j holds column j)
-        if (l == ii && row) {
-          const float ri = (bi + sum) - Aii * fi;
-          const float fn = -ri / Aii;
-          fi = fn > 0.f ? fn : 0.f;
-        }
+        const float ri = (bi + sum) - Aii * fi;
+        const float x = -ri;
+        const float q0 = x * yi;
+        const float fn = __builtin_fmaf(__builtin_fmaf(-q0, Aii, x), yi, q0);
+        const float fnew = fn > 0.f ? fn : 0.f;
+        fi = (row && l == ii) ? fnew : fi;
       }
     }
   }
