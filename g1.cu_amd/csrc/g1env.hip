@@ -386,6 +386,15 @@ __global__ void k_philox(const unsigned* in, unsigned* out, int n, unsigned k0, 
   out[4 * i] = r.x; out[4 * i + 1] = r.y; out[4 * i + 2] = r.z; out[4 * i + 3] = r.w;
 }
 
+// rcp_rn / div_rn of the physics kernel on caller-given operands (parity probe)
+__global__ void k_divide(const float* a, const float* b, float* rcp, float* quot, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float y = rcp_rn(b[i]);
+  rcp[i] = y;
+  quot[i] = div_rn(a[i], b[i], y);
+}
+
 // ====================================================================== host side
 struct EnvState {
   int N, S, pgs;
@@ -765,6 +774,12 @@ int g1_probe_policy(int n, int nlayers, const int* hidden, int activation, const
   HIPCHECK(hipDeviceSynchronize());
   HIPCHECK(hipFree(tmp.Wp));
   return 0;
+}
+
+void g1_probe_divide(int n, const float* a, const float* b, float* rcp, float* quot) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_divide, dim3((n + 255) / 256), dim3(256), 0, 0, a, b, rcp, quot, n);
+  HIPCHECK(hipGetLastError());
 }
 
 void g1_probe_philox(int n, const unsigned* ctr, unsigned* out, unsigned k0, unsigned k1) {

@@ -6,10 +6,12 @@
 //     Sweeps run level-synchronously over tree depth; a parent gathers its children's
 //     contributions in descending child index, exactly the order of the reference's serial
 //     leaf->root loops, so every accumulated value has the reference's rounding sequence.
-//   * M^-1 solves: lane j == right-hand side j (0: smooth (M+dtB)^-1(tau-bias); 1+3c+a: contact
-//     basis e_{c,a}); the tree traversal is fully unrolled over the static topology so the
-//     per-column articulated bias forces stay in registers; the shared factor is read from LDS
-//     (same address on all lanes = broadcast).
+//     The smooth solve (M+dtB)^-1(tau-bias) rides on the factor's leaf->root sweep and a
+//     level-synchronous root->leaf sweep.
+//   * contact M^-1 solves: lane j == right-hand side j (1+3c+a: contact basis e_{c,a}); the tree
+//     traversal is fully unrolled over the static topology so the per-column articulated bias
+//     forces stay in registers; the shared factor is read from LDS (same address on all lanes =
+//     broadcast).
 //   * contact rows: lane i == constraint row i (4 per contact); lane i holds column i of A
 //     (== row i, A is symmetric bit-for-bit) in registers for the projected Gauss-Seidel sweeps.
 //
@@ -58,7 +60,23 @@ __device__ __forceinline__ V3 qrot(Q4 q, V3 v) {
 // shallow penetrations; correct rounding makes every transcendental reproducible bit-for-bit.
 __device__ __forceinline__ float sin_rn(float x) { return (float)sin((double)x); }
 __device__ __forceinline__ float cos_rn(float x) { return (float)cos((double)x); }
-__device__ __forceinline__ float rsqrt_rn(float x) { return 1.f / sqrtf(x); }
+
+// Correctly rounded reciprocal and quotient on short dependency chains, for the positive normal
+// divisors of this path (pivots, D = S'I^A S + armature + dt kd, A_ii, impedances, angles).
+// rcp_rn: one Newton step y = y0 + y0 (1 - b y0) (fused) on the hardware estimate y0 returns
+// RN(1/b); checked bit-exact against the IEEE division for every mantissa of the binades
+// 2^-30 .. 2^30. div_rn: with y = RN(1/b), q0 = RN(a y), the residual a - b q0 is exact in an
+// fma and RN(q0 + r y) = RN(a / b) (Markstein's theorem); also checked bit-exact against the
+// IEEE division on 2e9 operand pairs. Both replace the ~10-instruction scaled IEEE sequence.
+__device__ __forceinline__ float rcp_rn(float b) {
+  const float y0 = __builtin_amdgcn_rcpf(b);
+  return __builtin_fmaf(__builtin_fmaf(-b, y0, 1.f), y0, y0);
+}
+__device__ __forceinline__ float div_rn(float a, float b, float yb) {
+  const float q0 = a * yb;
+  return __builtin_fmaf(__builtin_fmaf(-q0, b, a), yb, q0);
+}
+__device__ __forceinline__ float rsqrt_rn(float x) { return rcp_rn(sqrtf(x)); }
 
 __device__ __forceinline__ Q4 qnorm(Q4 q) {
   float n = rsqrt_rn(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
@@ -100,7 +118,8 @@ __device__ __forceinline__ float dot6(const float* a, const float* b) {
 __device__ __forceinline__ float foot_impedance(float pos) {
   const float dmin = MF::foot_solimp[0], dmax = MF::foot_solimp[1], width = MF::foot_solimp[2];
   const float mid = MF::foot_solimp[3], power = MF::foot_solimp[4];
-  float x = fabsf(pos) / width;
+  constexpr float inv_width = 1.f / MF::foot_solimp[2];   // RN(1/width), folded at compile time
+  float x = div_rn(fabsf(pos), width, inv_width);
   float y;
   if (x >= 1.f) y = 1.f;
   else {
@@ -122,7 +141,7 @@ struct WorldLds {
       float U[kNBody][6];   // hinge factor columns I^A S
       float invD[kNBody];   // hinge 1/(S'I^A S + armature + dt kd)
       float Dfac[36];       // Cholesky factor of the free-joint 6x6 block
-      float rhs[kNV + 1];   // smooth right-hand side tau - bias
+      float Dinv[6];        // RN(1 / diagonal of Dfac)
       float IA1[21];        // articulated inertia of the pelvis (packed)
       float Dm[36];         // free-joint 6x6 block before factoring
     } fac;
@@ -381,7 +400,6 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   if (L.hinge) {
     const float bias = sw.x * Fw.x + sw.y * Fw.y + sw.z * Fw.z + sv.x * Fv.x + sv.y * Fv.y + sv.z * Fv.z;
     xr = -bias + jtau;
-    s.u.fac.rhs[L.b + 4] = xr;
   }
   if (base) {
 #pragma unroll
@@ -392,8 +410,6 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const float br = R1.m[k] * Fw.x + R1.m[3 + k] * Fw.y + R1.m[6 + k] * Fw.z + 0.f * Fv.x + 0.f * Fv.y + 0.f * Fv.z;
       xb[k] = -bt + 0.f;
       xb[3 + k] = -br + 0.f;
-      s.u.fac.rhs[k] = xb[k];
-      s.u.fac.rhs[3 + k] = xb[3 + k];
     }
   }
 
@@ -445,7 +461,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       }
       float D = dot6(S6, U) + L.arm;
       if (P.damped) D += L.bdt;
-      const float invD = 1.f / D;
+      const float invD = rcp_rn(D);
 #pragma unroll
       for (int i = 0; i < 6; ++i)
 #pragma unroll
@@ -531,7 +547,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   __syncthreads();
   float a6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (base) {
-    float Dm[36];
+    float Dm[36], Dinv[6];
 #pragma unroll
     for (int i = 0; i < 36; ++i) Dm[i] = s.u.fac.Dm[i];
 #pragma unroll
@@ -541,10 +557,17 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         float a = Dm[i * 6 + j];
 #pragma unroll
         for (int k = 0; k < j; ++k) a -= Dm[i * 6 + k] * Dm[j * 6 + k];
-        if (i == j) Dm[i * 6 + i] = sqrtf(a); else Dm[i * 6 + j] = a / Dm[j * 6 + j];
+        if (i == j) {
+          Dm[i * 6 + i] = sqrtf(a);
+          Dinv[i] = rcp_rn(Dm[i * 6 + i]);
+        } else {
+          Dm[i * 6 + j] = div_rn(a, Dm[j * 6 + j], Dinv[j]);
+        }
       }
 #pragma unroll
     for (int i = 0; i < 36; ++i) s.u.fac.Dfac[i] = Dm[i];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) s.u.fac.Dinv[i] = Dinv[i];
     // smooth solve, free joint: L L' qdd = x_base - S_base.pA_1 (reference: src/aba_factor.cuh:139-155)
     float qdd[6];
 #pragma unroll
@@ -559,14 +582,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       float a = qdd[i];
 #pragma unroll
       for (int k = 0; k < i; ++k) a -= Dm[i * 6 + k] * qdd[k];
-      qdd[i] = a / Dm[i * 6 + i];
+      qdd[i] = div_rn(a, Dm[i * 6 + i], Dinv[i]);
     }
 #pragma unroll
     for (int i = 5; i >= 0; --i) {
       float a = qdd[i];
 #pragma unroll
       for (int k = i + 1; k < 6; ++k) a -= Dm[k * 6 + i] * qdd[k];
-      qdd[i] = a / Dm[i * 6 + i];
+      qdd[i] = div_rn(a, Dm[i * 6 + i], Dinv[i]);
     }
 #pragma unroll
     for (int k = 0; k < 6; ++k) s.Mm[0][k] = qdd[k];
@@ -639,7 +662,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const float kcoef = 1.f / (dmax * dmax * tc * tc * dr * dr);
     const float pyr = (1.f + mu * mu) * (2.f * mu * mu / MF::foot_impratio);
     const float pen = s.con[c][3], imp = foot_impedance(pen);
-    s.Rc[c] = s.con_w0[c] * pyr * (1.f - imp) / imp;
+    s.Rc[c] = div_rn(s.con_w0[c] * pyr * (1.f - imp), imp, rcp_rn(imp));
     const float kip = kcoef * imp * pen;
     s.aref[4 * c + 0] = -bcoef * (v0 + v1) - kip;
     s.aref[4 * c + 1] = -bcoef * (v0 - v1) - kip;
@@ -648,7 +671,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   }
   __syncthreads();
 
-  // ---------------- PASS 2: M^-1 solves, lane j = column j (reference: src/aba_factor.cuh:121-165)
+  // ---------------- PASS 2: M^-1 solves, lane j = basis column j (reference: src/aba_factor.cuh:121-165,
+  // src/env_qacc.cuh:137-152); column 0 (the smooth solve) was computed by the tree sweeps above.
   // The traversal is unrolled over the static tree. Articulated bias forces travel as explicit
   // carries along each chain (arm chains end in the torso 16, leg and waist chains in the pelvis 1);
   // parents with several children accumulate them in the reference's descending-child order.
@@ -656,17 +680,15 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const int j = l;
     const int cj = (j >= 1 && j < kCols) ? (j - 1) / 3 : 0, aj = (j >= 1) ? (j - 1) % 3 : 0;
     const bool basis = (j >= 1) && (j < kCols) && (cj < ncon);
-    const bool smooth = false;   // the smooth column was solved by the tree sweeps above
     const bool right = s.con_leg[cj] != 0;
     const float* eb = s.Eb[cj][aj];
-    // right-hand side entry of dof d, read on demand: tau - bias for the smooth column, the
-    // contact basis row e_{c,a} (12 ancestor dofs) for the basis columns, 0 otherwise
+    // right-hand side entry of dof d, read on demand: the contact basis row e_{c,a} on its 12
+    // ancestor dofs, 0 elsewhere and for idle lanes
     auto xrhs = [&](int d) -> float {
-      float v = smooth ? s.u.fac.rhs[d] : 0.f;
-      if (d < 6) return basis ? eb[6 + d] : v;
-      if (d < 12) return (basis && !right) ? eb[11 - d] : v;
-      if (d < 18) return (basis && right) ? eb[17 - d] : v;
-      return v;
+      if (d < 6) return basis ? eb[6 + d] : 0.f;
+      if (d < 12) return (basis && !right) ? eb[11 - d] : 0.f;
+      if (d < 18) return (basis && right) ? eb[17 - d] : 0.f;
+      return 0.f;
     };
     float u[kNBody];
     float car[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -675,6 +697,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
     for (int b = kNBody - 1; b >= 2; --b) {
       const int par = body_parent[b], d = b + 4;
+      // The basis right-hand sides live on the base and leg dofs (the feet hang off bodies 7 and
+      // 13, legs 2..13), so the waist/arm subtree (bodies 14..30) carries zero articulated bias:
+      // u = 0 - S.0 = +0 and its contribution to the pelvis is +0. Skipping it changes no bit.
+      static_assert(foot_body[0] < 14 && foot_body[kNFoot - 1] < 14 && body_parent[14] == 1, "leg layout");
+      if (b >= 14) {
+        u[b] = 0.f;
+        continue;
+      }
       float pb[6];
 #pragma unroll
       for (int k = 0; k < 6; ++k) pb[k] = (b == 16) ? p16[k] : (body_nchild[b] == 0 ? 0.f : car[k]);
@@ -707,14 +737,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         float a = rhs6[i];
 #pragma unroll
         for (int k = 0; k < i; ++k) a -= Lf[i * 6 + k] * qdd[k];
-        qdd[i] = a / Lf[i * 6 + i];
+        qdd[i] = div_rn(a, Lf[i * 6 + i], s.u.fac.Dinv[i]);
       }
 #pragma unroll
       for (int i = 5; i >= 0; --i) {
         float a = qdd[i];
 #pragma unroll
         for (int k = i + 1; k < 6; ++k) a -= Lf[k * 6 + i] * qdd[k];
-        qdd[i] = a / Lf[i * 6 + i];
+        qdd[i] = div_rn(a, Lf[i * 6 + i], s.u.fac.Dinv[i]);
       }
     }
     float* ycol = s.Mm[(j >= 1 && j < kCols) ? j : kCols - 1];
@@ -846,7 +876,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // q0 = RN(x y), r = x - A_ii q0 (exact with fma), q = RN(q0 + r y) equals RN(x / A_ii)
   // (Markstein's theorem), i.e. the IEEE quotient, on a 3-op dependency chain.
   float fi = 0.f;
-  const float yi = 1.f / Aii;
+  const float yi = rcp_rn(Aii);
 #pragma unroll 1
   for (int it = 0; it < P.pgs; ++it) {
 #pragma unroll
@@ -917,7 +947,7 @@ __device__ __forceinline__ void integrate_lane(const LaneModel& L, LaneState& st
     Q4 dq;
     if (ang < 1e-9f) dq = {1.f, 0.5f * v.x, 0.5f * v.y, 0.5f * v.z};
     else {
-      const float sn = sin_rn(0.5f * ang) / ang;
+      const float sn = div_rn(sin_rn(0.5f * ang), ang, rcp_rn(ang));
       dq = {cos_rn(0.5f * ang), v.x * sn, v.y * sn, v.z * sn};
     }
     Q4 qn = qnorm(qmul(Q4{st.bq[3], st.bq[4], st.bq[5], st.bq[6]}, dq));

@@ -57,6 +57,7 @@ _lib.g1_probe_substep.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 3 + [ctype
 _lib.g1_probe_policy.restype = ctypes.c_int
 _lib.g1_probe_policy.argtypes = [ctypes.c_int, ctypes.c_int, _ip, ctypes.c_int] + [ctypes.c_void_p] * 4
 _lib.g1_probe_philox.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint, ctypes.c_uint]
+_lib.g1_probe_divide.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 4
 
 
 def _p(a):

@@ -102,6 +102,10 @@ void g1_probe_substep(int n, float* qpos, float* qvel, const float* target, int 
 int g1_probe_policy(int n, int nlayers, const int* hidden, int activation, const float* W, const float* obs_norm,
                     float* mu_out, float* v_out);
 
+/* The physics kernel's reciprocal and quotient helpers on n DEVICE operand pairs: rcp[i] = 1/b[i],
+ * quot[i] = a[i]/b[i] (both correctly rounded for positive normal b). */
+void g1_probe_divide(int n, const float* a, const float* b, float* rcp, float* quot);
+
 /* Philox4x32-10 of n DEVICE counters ctr [n*4] with key (k0, k1) into out [n*4]. */
 void g1_probe_philox(int n, const unsigned* ctr, unsigned* out, unsigned k0, unsigned k1);
 

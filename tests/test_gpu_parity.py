@@ -178,3 +178,23 @@ def test_philox_known_answers(g1):
         g1._lib.g1_probe_philox(1, g1._dp(c), g1._dp(o), k0, k1)
         got = o.cpu().numpy().view(np.uint32)
         assert list(got) == want[i], [hex(x) for x in got]
+
+
+def test_reciprocal_and_quotient_are_ieee(g1):
+    """The physics kernel's short-chain rcp_rn / div_rn against IEEE fp32 division (numpy rounds
+    float32 division correctly): every mantissa of the binades 2^-12 .. 2^12 (the divisors of the
+    path: pivots, D, A_ii, impedances) and random numerators of both signs over 2^-40 .. 2^40."""
+    import torch
+    m = np.arange(1 << 23, dtype=np.uint32)
+    bs = np.concatenate([((np.uint32(e + 127) << np.uint32(23)) | m).view(np.float32) for e in range(-12, 13, 4)])
+    rng = np.random.default_rng(5)
+    a = (rng.uniform(1, 2, bs.size) * np.exp2(rng.integers(-40, 41, bs.size)) *
+         rng.choice([-1, 1], bs.size)).astype(np.float32)
+    a[::9] = (bs[::9] * rng.integers(-1000, 1001, bs[::9].size)).astype(np.float32)   # exact quotients
+    da, db = torch.from_numpy(a).cuda(), torch.from_numpy(bs).cuda()
+    r, q = torch.zeros_like(db), torch.zeros_like(db)
+    g1._lib.g1_probe_divide(bs.size, g1._dp(da), g1._dp(db), g1._dp(r), g1._dp(q))
+    r, q = r.cpu().numpy(), q.cpu().numpy()
+    with np.errstate(all="ignore"):
+        assert np.array_equal(r.view(np.uint32), (np.float32(1) / bs).view(np.uint32))
+        assert np.array_equal(q.view(np.uint32), (a / bs).view(np.uint32))
