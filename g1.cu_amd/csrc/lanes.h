@@ -46,6 +46,13 @@ __device__ __forceinline__ int wave_max(int v) {
   return v > o ? v : o;
 }
 
+// Value of lane I of this lane's aligned 8-lane chain (ds_swizzle bit mode within 32 lanes:
+// and_mask 0x18 keeps the chain bits, or_mask selects lane I).
+template <int I>
+__device__ __forceinline__ float chain_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (I << 5)));
+}
+
 // 8-bit contact mask of this group from a wave ballot
 __device__ __forceinline__ unsigned group_ballot8(bool pred) {
   unsigned long long m = __ballot(pred);

@@ -142,6 +142,7 @@ struct WorldLds {
       float invD[kNBody];   // hinge 1/(S'I^A S + armature + dt kd)
       float Dfac[36];       // Cholesky factor of the free-joint 6x6 block
       float Dinv[6];        // RN(1 / diagonal of Dfac)
+      float us[kNBody];     // hinge bias u = x - S.pA of the smooth solve
       float IA1[21];        // articulated inertia of the pelvis (packed)
       float Dm[36];         // free-joint 6x6 block before factoring
     } fac;
@@ -413,9 +414,12 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
   }
 
-  // ---------------- damped articulated-inertia factor (reference: src/aba_factor.cuh:51-108)
-  float IA[21];
-  {
+  // ---------------- body spatial inertia about the pelvis origin, 21-packed (reference:
+  // src/aba_factor.cuh:51-76), staged in LDS for the chain-parallel factor. The solve-output
+  // region (Mm) is free until the factor is done and holds it.
+  static_assert(kCols * kMmStride >= kNBody * 21, "I6 staging fits the solve-output region");
+  float* const I6 = &s.Mm[0][0];
+  if (L.body) {
     const float c2 = dot3(cc, cc);
     float A[9];
 #pragma unroll
@@ -437,94 +441,108 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
     for (int i = 0; i < 6; ++i)
 #pragma unroll
-      for (int j = i; j < 6; ++j) IA[symidx(i, j)] = M6[i * 6 + j];
+      for (int j = i; j < 6; ++j) I6[L.b * 21 + symidx(i, j)] = M6[i * 6 + j];
   }
   const float S6[6] = {sw.x, sw.y, sw.z, sv.x, sv.y, sv.z};
-  // Leaf -> root, fused: articulated-inertia downdate (reference: src/aba_factor.cuh:77-88) and
-  // the leaf -> root sweep of the smooth solve y = (M + dtB)^-1 (tau - bias) (reference:
-  // src/aba_factor.cuh:128-136). pAs is the lane's articulated bias force; children contribute in
-  // the reference's order, so the result is the reference's serial sweep bit for bit.
-  float pAs[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float Uk[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // this body's factor column, kept for root -> leaf
-  float iD = 0.f, us = 0.f;
+  __syncthreads();   // S and I6 of every body in LDS
+
+  // ---------------- damped articulated-inertia factor, chain-parallel (reference:
+  // src/aba_factor.cuh:77-88), fused with the leaf -> root sweep of the smooth solve
+  // y = (M + dtB)^-1 (tau - bias) (reference: src/aba_factor.cuh:128-136).
+  // The hinge bodies form four chains processed leaf -> root in lock-step over tree depth cd:
+  // left leg 7..2, right leg 13..8, left arm 23..17 then waist 16..14, right arm 30..24.
+  // Chain g runs on lanes 8g..8g+5 of the group and lane 8g+r holds row r of the current body's
+  // articulated inertia; U = I^A S is exchanged within the chain, D, the bias u and the
+  // articulated bias force pA are computed redundantly by the six lanes. Every entry sees the
+  // reference's operations in the reference's order: I^A_b = I6_b + the children's downdates in
+  // descending child order (torso: + D_24 then + D_17), U_i = sum_j I^A_ij S_j, D = S.U + arm
+  // (+ dt kd), downdate I^A_ij - U_i U_j / D; the products U_i U_j commute, so row r of the
+  // symmetric downdate equals the packed entries bit for bit.
+  const int grp = l >> 3, crow = l & 7, rowc = crow < 6 ? crow : 5;
+  const int c_off = grp == 0 ? 0 : (grp == 1 ? 6 : (grp == 2 ? 12 : 19));
+  const int c_lo = grp == 3 ? 5 : 2, c_hi = grp >= 2 ? kMaxDepth : 7;
+  float Dlr[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // row `crow` of the last body's downdate
+  float cs[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};    // last body's pA + U u / D (all six components)
+  // this round's body inputs (motion axis, I6 row, right-hand side), loaded one round ahead
+  auto chain_body = [&](int cd) { return (cd >= c_lo && cd <= c_hi) ? cd + c_off : 2; };
+  float Sn[6], In[6], xn;
+  {
+    const int b = chain_body(kMaxDepth);
+#pragma unroll
+    for (int j = 0; j < 6; ++j) { Sn[j] = s.u.fac.S[b + 4][j]; In[j] = I6[b * 21 + symidx(rowc, j)]; }
+    xn = gshfl(xr, b);
+  }
 #pragma unroll 1
   for (int cd = kMaxDepth; cd >= 2; --cd) {
-    float Dl[21], cs[6];
-    {
-      float U[6];
+    const bool act = cd >= c_lo && cd <= c_hi;
+    const int b = chain_body(cd);
+    const bool leaf = cd == c_hi;
+    float Sd[6], IAr[6], pA[6];
+    const float xb_ = xn;
 #pragma unroll
-      for (int i = 0; i < 6; ++i) {
-        float a = 0.f;
+    for (int j = 0; j < 6; ++j) { Sd[j] = Sn[j]; IAr[j] = In[j]; pA[j] = 0.f; }
+    if (cd > 2) {
+      const int bn = chain_body(cd - 1);
 #pragma unroll
-        for (int j = 0; j < 6; ++j) a += IA[symidx(i, j)] * S6[j];
-        U[i] = a;
-      }
-      float D = dot6(S6, U) + L.arm;
-      if (P.damped) D += L.bdt;
-      const float invD = rcp_rn(D);
+      for (int j = 0; j < 6; ++j) { Sn[j] = s.u.fac.S[bn + 4][j]; In[j] = I6[bn * 21 + symidx(rowc, j)]; }
+      xn = gshfl(xr, bn);
+    }
+    if (cd == body_depth[16]) {
+      // the right arm's last downdate and bias force join the torso first (lanes 24.. hold
+      // chain 3; the torso's own child 17 follows below)
+      const bool torso = grp == 2;
 #pragma unroll
-      for (int i = 0; i < 6; ++i)
-#pragma unroll
-        for (int j = i; j < 6; ++j) Dl[symidx(i, j)] = IA[symidx(i, j)] - U[i] * U[j] * invD;
-      const float u = xr - dot6(S6, pAs);
-      const float ud = u * invD;
-#pragma unroll
-      for (int k = 0; k < 6; ++k) cs[k] = pAs[k] + U[k] * ud;
-      const bool mine = (L.depth == cd);
-#pragma unroll
-      for (int k = 0; k < 6; ++k) Uk[k] = mine ? U[k] : Uk[k];
-      iD = mine ? invD : iD;
-      us = mine ? u : us;
-      if (L.hinge && mine) {
-#pragma unroll
-        for (int k = 0; k < 6; ++k) s.u.fac.U[L.b][k] = U[k];
-        s.u.fac.invD[L.b] = invD;
+      for (int j = 0; j < 6; ++j) {
+        const float gD = gshfl(Dlr[j], 24 + rowc), gc = gshfl(cs[j], 24 + rowc);
+        if (torso) { IAr[j] = IAr[j] + gD; pA[j] = pA[j] + gc; }
       }
     }
-    const bool gather = (L.depth == cd - 1);
 #pragma unroll
-    for (int k = 0; k < 21; ++k) {
-      const float g = gshfl(Dl[k], L.c0);
-      if (gather && L.nchild > 0) IA[k] += g;
+    for (int j = 0; j < 6; ++j) {
+      if (!leaf) { IAr[j] = IAr[j] + Dlr[j]; pA[j] = pA[j] + cs[j]; }
     }
+    float ur = 0.f;
 #pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      const float g = gshfl(cs[k], L.c0);
-      if (gather && L.nchild > 0) pAs[k] += g;
+    for (int j = 0; j < 6; ++j) ur += IAr[j] * Sd[j];
+    const float Ub[6] = {chain_bcast<0>(ur), chain_bcast<1>(ur), chain_bcast<2>(ur),
+                         chain_bcast<3>(ur), chain_bcast<4>(ur), chain_bcast<5>(ur)};
+    float D = dot6(Sd, Ub) + MF::dof_armature[b + 4];
+    if (P.damped) D += MF::dt * MF::act_kd[b - 2];
+    const float invD = rcp_rn(D);
+    const float u = xb_ - dot6(Sd, pA);
+    const float ud = u * invD;
+    if (act) {
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        Dlr[j] = IAr[j] - Ub[rowc] * Ub[j] * invD;
+        cs[j] = pA[j] + Ub[j] * ud;
+      }
+      if (crow < 6) s.u.fac.U[b][crow] = ur;
+      if (crow == 0) { s.u.fac.invD[b] = invD; s.u.fac.us[b] = u; }
     }
-    if (cd == body_depth[17] || cd == 2) {   // multi-child parents: torso (depth 4), pelvis (depth 1)
+  }
+  // pelvis: I^A_1 = I6_1 + D_14 + D_8 + D_2 and pA_1 = cs_14 + cs_8 + cs_2 (descending children),
+  // row r on lane r of chain 0; lane 1 keeps pA_1 for the base solve
+  float pAs[6];
+  {
+    float I1[6];
 #pragma unroll
-      for (int k = 0; k < 21; ++k) {
-        const float g = gshfl(Dl[k], L.c1);
-        if (gather && L.nchild > 1) IA[k] += g;
-      }
+    for (int j = 0; j < 6; ++j) {
+      const float d14 = gshfl(Dlr[j], 16 + rowc), d8 = gshfl(Dlr[j], 8 + rowc);
+      const float c14 = gshfl(cs[j], 16 + rowc), c8 = gshfl(cs[j], 8 + rowc);
+      I1[j] = ((I6[1 * 21 + symidx(rowc, j)] + d14) + d8) + Dlr[j];
+      pAs[j] = ((0.f + c14) + c8) + cs[j];
+    }
+    if (l < 6) {
 #pragma unroll
-      for (int k = 0; k < 6; ++k) {
-        const float g = gshfl(cs[k], L.c1);
-        if (gather && L.nchild > 1) pAs[k] += g;
-      }
-      if (cd == 2) {
-#pragma unroll
-        for (int k = 0; k < 21; ++k) {
-          const float g = gshfl(Dl[k], L.c2);
-          if (gather && L.nchild > 2) IA[k] += g;
-        }
-#pragma unroll
-        for (int k = 0; k < 6; ++k) {
-          const float g = gshfl(cs[k], L.c2);
-          if (gather && L.nchild > 2) pAs[k] += g;
-        }
-      }
+      for (int j = 0; j < 6; ++j)
+        if (j >= l) s.u.fac.IA1[symidx(l, j)] = I1[j];
     }
   }
   // ---------------- free-joint 6x6 block (reference: src/aba_factor.cuh:90-108): lane c < 6
   // builds column c of U6 = I^A S_base and of D = S_base' U6; lane 1 factors D and solves the
   // base of the smooth system.
-  if (base) {
-#pragma unroll
-    for (int k = 0; k < 21; ++k) s.u.fac.IA1[k] = IA[k];
-  }
-  __syncthreads();   // S and I^A of the pelvis complete in LDS
+  __syncthreads();   // I^A of the pelvis and the hinge factor complete in LDS
   if (l < 6) {
     float Sc[6], U6c[6];
 #pragma unroll
@@ -602,13 +620,17 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
   }
   // ---------------- smooth solve root -> leaf (reference: src/aba_factor.cuh:156-164)
+  float Uk[6];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) Uk[k] = s.u.fac.U[L.b][k];
+  const float usk = s.u.fac.us[L.b], iDk = s.u.fac.invD[L.b];
 #pragma unroll 1
   for (int r = 2; r <= kMaxDepth; ++r) {
     float ap[6];
 #pragma unroll
     for (int k = 0; k < 6; ++k) ap[k] = gshfl(a6[k], L.par);
     if (L.depth == r) {
-      const float q = (us - dot6(Uk, ap)) * iD;
+      const float q = (usk - dot6(Uk, ap)) * iDk;
 #pragma unroll
       for (int k = 0; k < 6; ++k) a6[k] = ap[k] + S6[k] * q;
       s.Mm[0][L.b + 4] = q;
