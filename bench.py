@@ -21,6 +21,9 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0            # MI355X published HBM3E bandwidth
 RTX3090_SUBSTEPS_PER_S = 4.96e6  # reference's published fused-rollout number (N=8192, H=32, S=10)
+# HBM bytes per k_physics dispatch at config 3 from rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled
+# by the same counter on a copy of known size (profiles/k_physics_config3_pmc.md)
+PHYS_TRAFFIC_BYTES = {3: 11.81e6}
 
 
 def bytes_per_world_substep(c, p):
@@ -129,7 +132,7 @@ def main():
                                f"policy 100-{'-'.join(map(str, cfg['hidden']))} {'tanh' if cfg['act'] == 0 else 'ELU'}",
                    "N": N, "H": H, "substeps": S, "pgs": pgs, "ms_per_rollout": ms_rollout},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": PHYS_TRAFFIC_BYTES.get(args.config),
                      "kernel": "k_physics", "avg_launch_ms": phys_ms / max(launches, 1),
                      "algorithmic_bytes_per_launch": bytes_per_launch, "mean_ncon": cbar},
         "phases": {"physics_ms_per_rollout": phys_ms / args.steps, "policy_ms_per_rollout": pol_ms / args.steps,
