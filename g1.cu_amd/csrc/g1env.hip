@@ -78,7 +78,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
     const int t = a.t0 + k * a.astep;
     const float act = L.hinge ? a.act[((long)t * a.N + wc) * kAct + ai] : 0.f;
     // PD target = clamp(stand + 0.5 a) (reference: src/g1_env.cu:123-130)
-    float target = L.qstand + 0.5f * act;
+    float target = fmaf_(0.5f, act, L.qstand);
     if (target < L.clo) target = L.clo;
     if (target > L.chi) target = L.chi;
     float vx_sum = 0.f, energy = 0.f;
@@ -86,7 +86,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
     for (int sub = 0; sub < a.S; ++sub) {
       float jtau = 0.f;
       if (L.hinge) {
-        float pdt = L.kp * (target - st.jq) - L.kd * st.jqd;
+        float pdt = fmaf_(-L.kd, st.jqd, L.kp * (target - st.jq));
         if (pdt < L.flo) pdt = L.flo;
         else if (pdt > L.fhi) pdt = L.fhi;
         jtau = pdt;
@@ -108,7 +108,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
       const float vx = vx_sum / (float)a.S;
       const float height = st.bq[2];
       const float qw = st.bq[3], qx = st.bq[4], qy = st.bq[5];
-      const float up = 1.f - 2.f * (qx * qx + qy * qy);
+      const float up = fmaf_(-2.f, fmaf_(qy, qy, qx * qx), 1.f);   // quat2mat(q)[2][2]
       const int alive = !(height < 0.45f || up < 0.5f);
       (void)qw;
       const float upc = up < 0.f ? 0.f : (up > 1.f ? 1.f : up);
@@ -202,7 +202,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_probe(ProbeArgs a) {
       if (a.mode == 0) jtau = a.tau[(long)wc * kNV + L.b + 4];
       else {
         const float tg = a.target[(long)wc * kAct + L.b - 2];
-        float pdt = L.kp * (tg - st.jq) - L.kd * st.jqd;
+        float pdt = fmaf_(-L.kd, st.jqd, L.kp * (tg - st.jq));
         if (pdt < L.flo) pdt = L.flo;
         else if (pdt > L.fhi) pdt = L.fhi;
         jtau = pdt;

@@ -38,21 +38,31 @@ constexpr int kPairs = kNFoot * (kNFoot + 1) / 2;
 struct V3 { float x, y, z; };
 struct Q4 { float w, x, y, z; };
 
+// Fused multiply-add is used only explicitly (the build passes -ffp-contract=off), with one
+// convention shared with the CPU restatement: a sum of products a0 b0 + a1 b1 + ... is evaluated
+// left to right as s = a0 b0, s = fma(a_i, b_i, s) (differences as fma(-a_i, b_i, s)); an
+// accumulation s = 0; s += a_i b_i as s = fma(a_i, b_i, s) from s = 0; x + a b as fma(a, b, x).
+__device__ __forceinline__ float fmaf_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+
 __device__ __forceinline__ V3 vadd(V3 a, V3 b) { return {a.x + b.x, a.y + b.y, a.z + b.z}; }
 __device__ __forceinline__ V3 vsub(V3 a, V3 b) { return {a.x - b.x, a.y - b.y, a.z - b.z}; }
 __device__ __forceinline__ V3 cross(V3 a, V3 b) {
-  return {a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+  return {fmaf_(-a.z, b.y, a.y * b.z), fmaf_(-a.x, b.z, a.z * b.x), fmaf_(-a.y, b.x, a.x * b.y)};
 }
-__device__ __forceinline__ float dot3(V3 a, V3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+__device__ __forceinline__ float dot3(V3 a, V3 b) { return fmaf_(a.z, b.z, fmaf_(a.y, b.y, a.x * b.x)); }
 __device__ __forceinline__ Q4 qmul(Q4 a, Q4 b) {
-  return {a.w * b.w - a.x * b.x - a.y * b.y - a.z * b.z, a.w * b.x + a.x * b.w + a.y * b.z - a.z * b.y,
-          a.w * b.y - a.x * b.z + a.y * b.w + a.z * b.x, a.w * b.z + a.x * b.y - a.y * b.x + a.z * b.w};
+  return {fmaf_(-a.z, b.z, fmaf_(-a.y, b.y, fmaf_(-a.x, b.x, a.w * b.w))),
+          fmaf_(-a.z, b.y, fmaf_(a.y, b.z, fmaf_(a.x, b.w, a.w * b.x))),
+          fmaf_(a.z, b.x, fmaf_(a.y, b.w, fmaf_(-a.x, b.z, a.w * b.y))),
+          fmaf_(a.z, b.w, fmaf_(-a.y, b.x, fmaf_(a.x, b.y, a.w * b.z)))};
 }
+// v' = v + w t + u x t, t = 2 u x v
 __device__ __forceinline__ V3 qrot(Q4 q, V3 v) {
-  V3 u{q.x, q.y, q.z};
-  V3 t{2.f * (u.y * v.z - u.z * v.y), 2.f * (u.z * v.x - u.x * v.z), 2.f * (u.x * v.y - u.y * v.x)};
-  return {v.x + q.w * t.x + (u.y * t.z - u.z * t.y), v.y + q.w * t.y + (u.z * t.x - u.x * t.z),
-          v.z + q.w * t.z + (u.x * t.y - u.y * t.x)};
+  const V3 u{q.x, q.y, q.z};
+  const V3 c = cross(u, v);
+  const V3 t{2.f * c.x, 2.f * c.y, 2.f * c.z};
+  const V3 ut = cross(u, t);
+  return {fmaf_(q.w, t.x, v.x) + ut.x, fmaf_(q.w, t.y, v.y) + ut.y, fmaf_(q.w, t.z, v.z) + ut.z};
 }
 // Correctly rounded fp32 transcendentals (evaluated in fp64, rounded once; fp64 VALU runs at the
 // fp32 rate on CDNA4 and these sit outside the inner loops). The contact force is stiff in the
@@ -79,16 +89,17 @@ __device__ __forceinline__ float div_rn(float a, float b, float yb) {
 __device__ __forceinline__ float rsqrt_rn(float x) { return rcp_rn(sqrtf(x)); }
 
 __device__ __forceinline__ Q4 qnorm(Q4 q) {
-  float n = rsqrt_rn(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+  float n = rsqrt_rn(fmaf_(q.z, q.z, fmaf_(q.y, q.y, fmaf_(q.x, q.x, q.w * q.w))));
   return {q.w * n, q.x * n, q.y * n, q.z * n};
 }
 struct M3 { float m[9]; };
 __device__ __forceinline__ M3 quat2mat(Q4 q) {
   float w = q.w, x = q.x, y = q.y, z = q.z;
   M3 r;
-  r.m[0] = 1 - 2 * (y * y + z * z); r.m[1] = 2 * (x * y - w * z);     r.m[2] = 2 * (x * z + w * y);
-  r.m[3] = 2 * (x * y + w * z);     r.m[4] = 1 - 2 * (x * x + z * z); r.m[5] = 2 * (y * z - w * x);
-  r.m[6] = 2 * (x * z - w * y);     r.m[7] = 2 * (y * z + w * x);     r.m[8] = 1 - 2 * (x * x + y * y);
+  // 1 - 2 s is fma(-2, s, 1) exactly (2 s is exact)
+  r.m[0] = fmaf_(-2.f, fmaf_(z, z, y * y), 1.f); r.m[1] = 2.f * fmaf_(-w, z, x * y); r.m[2] = 2.f * fmaf_(w, y, x * z);
+  r.m[3] = 2.f * fmaf_(w, z, x * y); r.m[4] = fmaf_(-2.f, fmaf_(z, z, x * x), 1.f); r.m[5] = 2.f * fmaf_(-w, x, y * z);
+  r.m[6] = 2.f * fmaf_(-w, y, x * z); r.m[7] = 2.f * fmaf_(w, x, y * z); r.m[8] = fmaf_(-2.f, fmaf_(y, y, x * x), 1.f);
   return r;
 }
 __device__ __forceinline__ void crossm(V3 w1, V3 v1, V3 w2, V3 v2, V3& ow, V3& ov) {
@@ -104,7 +115,7 @@ __device__ __forceinline__ int symidx(int i, int j) {
 __device__ __forceinline__ float dot6(const float* a, const float* b) {
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 6; ++i) s += a[i] * b[i];
+  for (int i = 0; i < 6; ++i) s = fmaf_(a[i], b[i], s);
   return s;
 }
 
@@ -128,9 +139,9 @@ __device__ __forceinline__ float foot_impedance(float pos) {
     static_assert(MF::foot_solimp[4] == 2.f, "impedance power 2 assumed");
     float a = 1.f / mid;
     float b = 1.f / (1.f - mid);
-    y = (x < mid) ? a * (x * x) : 1.f - b * ((1.f - x) * (1.f - x));
+    y = (x < mid) ? a * (x * x) : fmaf_(-b, (1.f - x) * (1.f - x), 1.f);
   }
-  return dmin + y * (dmax - dmin);
+  return fmaf_(y, dmax - dmin, dmin);
 }
 
 // ---------------------------------------------------------------- per-world LDS
@@ -293,8 +304,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int i = 0; i < 3; ++i)
 #pragma unroll
       for (int j = 0; j < 3; ++j)
-        Iw.m[3 * i + j] = Ri.m[3 * i + 0] * d[0] * Ri.m[3 * j + 0] + Ri.m[3 * i + 1] * d[1] * Ri.m[3 * j + 1] +
-                          Ri.m[3 * i + 2] * d[2] * Ri.m[3 * j + 2];
+        Iw.m[3 * i + j] = fmaf_(Ri.m[3 * i + 2] * d[2], Ri.m[3 * j + 2],
+                                fmaf_(Ri.m[3 * i + 1] * d[1], Ri.m[3 * j + 1], Ri.m[3 * i + 0] * d[0] * Ri.m[3 * j + 0]));
     cc = vsub(xip, p);
   }
   const float m = L.body ? L.mass : 0.f;
@@ -312,8 +323,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       V3 tw{0.f, 0.f, 0.f}, tv{k == 0 ? 1.f : 0.f, k == 1 ? 1.f : 0.f, k == 2 ? 1.f : 0.f};
       crossm(w, v, tw, tv, Sdw[k], Sdv[k]);
       const float qd = st.bqd[k];
-      w = {w.x + tw.x * qd, w.y + tw.y * qd, w.z + tw.z * qd};
-      v = {v.x + tv.x * qd, v.y + tv.y * qd, v.z + tv.z * qd};
+      w = {fmaf_(tw.x, qd, w.x), fmaf_(tw.y, qd, w.y), fmaf_(tw.z, qd, w.z)};
+      v = {fmaf_(tv.x, qd, v.x), fmaf_(tv.y, qd, v.y), fmaf_(tv.z, qd, v.z)};
     }
     const V3 wr = w, vr = v;
 #pragma unroll
@@ -324,16 +335,16 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
       const float qd = st.bqd[3 + k];
-      w = {w.x + R1.m[k] * qd, w.y + R1.m[3 + k] * qd, w.z + R1.m[6 + k] * qd};
-      v = {v.x + 0.f * qd, v.y + 0.f * qd, v.z + 0.f * qd};
+      w = {fmaf_(R1.m[k], qd, w.x), fmaf_(R1.m[3 + k], qd, w.y), fmaf_(R1.m[6 + k], qd, w.z)};
+      v = {fmaf_(0.f, qd, v.x), fmaf_(0.f, qd, v.y), fmaf_(0.f, qd, v.z)};
     }
     vw = w; vv = v;
     V3 a_w{0.f, 0.f, 0.f}, a_v{-MF::gravity[0], -MF::gravity[1], -MF::gravity[2]};
 #pragma unroll
     for (int k = 0; k < 6; ++k) {
       const float qd = st.bqd[k];
-      a_w = {a_w.x + Sdw[k].x * qd, a_w.y + Sdw[k].y * qd, a_w.z + Sdw[k].z * qd};
-      a_v = {a_v.x + Sdv[k].x * qd, a_v.y + Sdv[k].y * qd, a_v.z + Sdv[k].z * qd};
+      a_w = {fmaf_(Sdw[k].x, qd, a_w.x), fmaf_(Sdw[k].y, qd, a_w.y), fmaf_(Sdw[k].z, qd, a_w.z)};
+      a_v = {fmaf_(Sdv[k].x, qd, a_v.x), fmaf_(Sdv[k].y, qd, a_v.y), fmaf_(Sdv[k].z, qd, a_v.z)};
     }
     aw = a_w; av = a_v;
   }
@@ -347,25 +358,26 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       V3 Sdw, Sdv;
       crossm(pw, pv, sw, sv, Sdw, Sdv);
       const float qd = st.jqd;
-      vw = {pw.x + sw.x * qd, pw.y + sw.y * qd, pw.z + sw.z * qd};
-      vv = {pv.x + sv.x * qd, pv.y + sv.y * qd, pv.z + sv.z * qd};
-      aw = {paw.x + Sdw.x * qd, paw.y + Sdw.y * qd, paw.z + Sdw.z * qd};
-      av = {pav.x + Sdv.x * qd, pav.y + Sdv.y * qd, pav.z + Sdv.z * qd};
+      vw = {fmaf_(sw.x, qd, pw.x), fmaf_(sw.y, qd, pw.y), fmaf_(sw.z, qd, pw.z)};
+      vv = {fmaf_(sv.x, qd, pv.x), fmaf_(sv.y, qd, pv.y), fmaf_(sv.z, qd, pv.z)};
+      aw = {fmaf_(Sdw.x, qd, paw.x), fmaf_(Sdw.y, qd, paw.y), fmaf_(Sdw.z, qd, paw.z)};
+      av = {fmaf_(Sdv.x, qd, pav.x), fmaf_(Sdv.y, qd, pav.y), fmaf_(Sdv.z, qd, pav.z)};
     }
   }
 
   // ---------------- body forces f = I a + v x* (I v) (reference: src/aba_bias.cuh:103-111,
   // inertia application src/dynamics.cuh:126-139)
   auto apply_I = [&](V3 xw, V3 xv, V3& fw, V3& fv) {
-    V3 Asw{Iw.m[0] * xw.x + Iw.m[1] * xw.y + Iw.m[2] * xw.z, Iw.m[3] * xw.x + Iw.m[4] * xw.y + Iw.m[5] * xw.z,
-           Iw.m[6] * xw.x + Iw.m[7] * xw.y + Iw.m[8] * xw.z};
+    V3 Asw{fmaf_(Iw.m[2], xw.z, fmaf_(Iw.m[1], xw.y, Iw.m[0] * xw.x)),
+           fmaf_(Iw.m[5], xw.z, fmaf_(Iw.m[4], xw.y, Iw.m[3] * xw.x)),
+           fmaf_(Iw.m[8], xw.z, fmaf_(Iw.m[7], xw.y, Iw.m[6] * xw.x))};
     const float c2 = dot3(cc, cc), csw = dot3(cc, xw);
-    Asw = {Asw.x + m * (c2 * xw.x - csw * cc.x), Asw.y + m * (c2 * xw.y - csw * cc.y),
-           Asw.z + m * (c2 * xw.z - csw * cc.z)};
+    Asw = {fmaf_(m, fmaf_(-csw, cc.x, c2 * xw.x), Asw.x), fmaf_(m, fmaf_(-csw, cc.y, c2 * xw.y), Asw.y),
+           fmaf_(m, fmaf_(-csw, cc.z, c2 * xw.z), Asw.z)};
     V3 mc = cross(cc, xv);
-    fw = {Asw.x + m * mc.x, Asw.y + m * mc.y, Asw.z + m * mc.z};
+    fw = {fmaf_(m, mc.x, Asw.x), fmaf_(m, mc.y, Asw.y), fmaf_(m, mc.z, Asw.z)};
     V3 cs = cross(cc, xw);
-    fv = {-m * cs.x + m * xv.x, -m * cs.y + m * xv.y, -m * cs.z + m * xv.z};
+    fv = {fmaf_(m, xv.x, -m * cs.x), fmaf_(m, xv.y, -m * cs.y), fmaf_(m, xv.z, -m * cs.z)};
   };
   V3 Fw{0.f, 0.f, 0.f}, Fv{0.f, 0.f, 0.f};
   if (L.body) {
@@ -399,16 +411,17 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // smooth right-hand side tau - bias of the lane's dofs (lane 1: the six base dofs, tau = 0)
   float xr = 0.f, xb[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (L.hinge) {
-    const float bias = sw.x * Fw.x + sw.y * Fw.y + sw.z * Fw.z + sv.x * Fv.x + sv.y * Fv.y + sv.z * Fv.z;
+    const float bias = fmaf_(sv.z, Fv.z, fmaf_(sv.y, Fv.y, fmaf_(sv.x, Fv.x, fmaf_(sw.z, Fw.z, fmaf_(sw.y, Fw.y, sw.x * Fw.x)))));
     xr = -bias + jtau;
   }
   if (base) {
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
       // translation axis e_k: S = (0,0,0, e_k); rotation axis R1 col k: S = (R1 col, 0,0,0)
-      const float bt = 0.f * Fw.x + 0.f * Fw.y + 0.f * Fw.z + (k == 0 ? 1.f : 0.f) * Fv.x +
-                       (k == 1 ? 1.f : 0.f) * Fv.y + (k == 2 ? 1.f : 0.f) * Fv.z;
-      const float br = R1.m[k] * Fw.x + R1.m[3 + k] * Fw.y + R1.m[6 + k] * Fw.z + 0.f * Fv.x + 0.f * Fv.y + 0.f * Fv.z;
+      const float e0 = k == 0 ? 1.f : 0.f, e1 = k == 1 ? 1.f : 0.f, e2 = k == 2 ? 1.f : 0.f;
+      const float bt = fmaf_(e2, Fv.z, fmaf_(e1, Fv.y, fmaf_(e0, Fv.x, fmaf_(0.f, Fw.z, fmaf_(0.f, Fw.y, 0.f * Fw.x)))));
+      const float br = fmaf_(0.f, Fv.z, fmaf_(0.f, Fv.y, fmaf_(0.f, Fv.x,
+                       fmaf_(R1.m[6 + k], Fw.z, fmaf_(R1.m[3 + k], Fw.y, R1.m[k] * Fw.x)))));
       xb[k] = -bt + 0.f;
       xb[3 + k] = -br + 0.f;
     }
@@ -424,9 +437,9 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     float A[9];
 #pragma unroll
     for (int i = 0; i < 9; ++i) A[i] = Iw.m[i];
-    A[0] += m * (c2 - cc.x * cc.x); A[1] += m * (-cc.x * cc.y); A[2] += m * (-cc.x * cc.z);
-    A[3] += m * (-cc.y * cc.x);     A[4] += m * (c2 - cc.y * cc.y); A[5] += m * (-cc.y * cc.z);
-    A[6] += m * (-cc.z * cc.x);     A[7] += m * (-cc.z * cc.y); A[8] += m * (c2 - cc.z * cc.z);
+    A[0] = fmaf_(m, fmaf_(-cc.x, cc.x, c2), A[0]); A[1] = fmaf_(m, -cc.x * cc.y, A[1]); A[2] = fmaf_(m, -cc.x * cc.z, A[2]);
+    A[3] = fmaf_(m, -cc.y * cc.x, A[3]); A[4] = fmaf_(m, fmaf_(-cc.y, cc.y, c2), A[4]); A[5] = fmaf_(m, -cc.y * cc.z, A[5]);
+    A[6] = fmaf_(m, -cc.z * cc.x, A[6]); A[7] = fmaf_(m, -cc.z * cc.y, A[7]); A[8] = fmaf_(m, fmaf_(-cc.z, cc.z, c2), A[8]);
     const float Bx[9] = {0.f, -cc.z, cc.y, cc.z, 0.f, -cc.x, -cc.y, cc.x, 0.f};
     float M6[36];
 #pragma unroll
@@ -465,12 +478,15 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   float cs[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};    // last body's pA + U u / D (all six components)
   // this round's body inputs (motion axis, I6 row, right-hand side), loaded one round ahead
   auto chain_body = [&](int cd) { return (cd >= c_lo && cd <= c_hi) ? cd + c_off : 2; };
-  float Sn[6], In[6], xn;
+  // body b's armature and dt kd live on lane b; the chain lanes fetch them with the rhs
+  float Sn[6], In[6], xn, an, kn;
   {
     const int b = chain_body(kMaxDepth);
 #pragma unroll
     for (int j = 0; j < 6; ++j) { Sn[j] = s.u.fac.S[b + 4][j]; In[j] = I6[b * 21 + symidx(rowc, j)]; }
     xn = gshfl(xr, b);
+    an = gshfl(L.arm, b);
+    kn = gshfl(L.bdt, b);
   }
 #pragma unroll 1
   for (int cd = kMaxDepth; cd >= 2; --cd) {
@@ -478,7 +494,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const int b = chain_body(cd);
     const bool leaf = cd == c_hi;
     float Sd[6], IAr[6], pA[6];
-    const float xb_ = xn;
+    const float xb_ = xn, arm = an, bdt = kn;
 #pragma unroll
     for (int j = 0; j < 6; ++j) { Sd[j] = Sn[j]; IAr[j] = In[j]; pA[j] = 0.f; }
     if (cd > 2) {
@@ -486,6 +502,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
       for (int j = 0; j < 6; ++j) { Sn[j] = s.u.fac.S[bn + 4][j]; In[j] = I6[bn * 21 + symidx(rowc, j)]; }
       xn = gshfl(xr, bn);
+      an = gshfl(L.arm, bn);
+      kn = gshfl(L.bdt, bn);
     }
     if (cd == body_depth[16]) {
       // the right arm's last downdate and bias force join the torso first (lanes 24.. hold
@@ -503,19 +521,19 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
     float ur = 0.f;
 #pragma unroll
-    for (int j = 0; j < 6; ++j) ur += IAr[j] * Sd[j];
+    for (int j = 0; j < 6; ++j) ur = fmaf_(IAr[j], Sd[j], ur);
     const float Ub[6] = {chain_bcast<0>(ur), chain_bcast<1>(ur), chain_bcast<2>(ur),
                          chain_bcast<3>(ur), chain_bcast<4>(ur), chain_bcast<5>(ur)};
-    float D = dot6(Sd, Ub) + MF::dof_armature[b + 4];
-    if (P.damped) D += MF::dt * MF::act_kd[b - 2];
+    float D = dot6(Sd, Ub) + arm;
+    if (P.damped) D += bdt;
     const float invD = rcp_rn(D);
     const float u = xb_ - dot6(Sd, pA);
     const float ud = u * invD;
     if (act) {
 #pragma unroll
       for (int j = 0; j < 6; ++j) {
-        Dlr[j] = IAr[j] - Ub[rowc] * Ub[j] * invD;
-        cs[j] = pA[j] + Ub[j] * ud;
+        Dlr[j] = fmaf_(-(ur * Ub[j]), invD, IAr[j]);   // ur == Ub[crow] on rows 0..5
+        cs[j] = fmaf_(Ub[j], ud, pA[j]);
       }
       if (crow < 6) s.u.fac.U[b][crow] = ur;
       if (crow == 0) { s.u.fac.invD[b] = invD; s.u.fac.us[b] = u; }
@@ -551,14 +569,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int i = 0; i < 6; ++i) {
       float a = 0.f;
 #pragma unroll
-      for (int j = 0; j < 6; ++j) a += s.u.fac.IA1[symidx(i, j)] * Sc[j];
+      for (int j = 0; j < 6; ++j) a = fmaf_(s.u.fac.IA1[symidx(i, j)], Sc[j], a);
       U6c[i] = a;
     }
 #pragma unroll
     for (int k = 0; k < 6; ++k) {
       float a = 0.f;
 #pragma unroll
-      for (int i = 0; i < 6; ++i) a += s.u.fac.S[k][i] * U6c[i];
+      for (int i = 0; i < 6; ++i) a = fmaf_(s.u.fac.S[k][i], U6c[i], a);
       s.u.fac.Dm[k * 6 + l] = a + 0.f;   // + armature (0) + dt*damping (0) on the free joint
     }
   }
@@ -574,7 +592,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       for (int j = 0; j <= i; ++j) {
         float a = Dm[i * 6 + j];
 #pragma unroll
-        for (int k = 0; k < j; ++k) a -= Dm[i * 6 + k] * Dm[j * 6 + k];
+        for (int k = 0; k < j; ++k) a = fmaf_(-Dm[i * 6 + k], Dm[j * 6 + k], a);
         if (i == j) {
           Dm[i * 6 + i] = sqrtf(a);
           Dinv[i] = rcp_rn(Dm[i * 6 + i]);
@@ -599,14 +617,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int i = 0; i < 6; ++i) {
       float a = qdd[i];
 #pragma unroll
-      for (int k = 0; k < i; ++k) a -= Dm[i * 6 + k] * qdd[k];
+      for (int k = 0; k < i; ++k) a = fmaf_(-Dm[i * 6 + k], qdd[k], a);
       qdd[i] = div_rn(a, Dm[i * 6 + i], Dinv[i]);
     }
 #pragma unroll
     for (int i = 5; i >= 0; --i) {
       float a = qdd[i];
 #pragma unroll
-      for (int k = i + 1; k < 6; ++k) a -= Dm[k * 6 + i] * qdd[k];
+      for (int k = i + 1; k < 6; ++k) a = fmaf_(-Dm[k * 6 + i], qdd[k], a);
       qdd[i] = div_rn(a, Dm[i * 6 + i], Dinv[i]);
     }
 #pragma unroll
@@ -615,7 +633,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int i = 0; i < 6; ++i) {
       float a = 0.f;
 #pragma unroll
-      for (int k = 0; k < 6; ++k) a += s.u.fac.S[k][i] * qdd[k];
+      for (int k = 0; k < 6; ++k) a = fmaf_(s.u.fac.S[k][i], qdd[k], a);
       a6[i] = 0.f + a;
     }
   }
@@ -632,7 +650,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     if (L.depth == r) {
       const float q = (usk - dot6(Uk, ap)) * iDk;
 #pragma unroll
-      for (int k = 0; k < 6; ++k) a6[k] = ap[k] + S6[k] * q;
+      for (int k = 0; k < 6; ++k) a6[k] = fmaf_(S6[k], q, ap[k]);
       s.Mm[0][L.b + 4] = q;
     }
   }
@@ -677,7 +695,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const float e0 = jc.z, e1 = mu * jc.y, e2 = -mu * jc.x;
       s.Eb[c][0][k] = e0; s.Eb[c][1][k] = e1; s.Eb[c][2][k] = e2;
       const float qd = s.qvel[a];
-      v0 += e0 * qd; v1 += e1 * qd; v2 += e2 * qd;
+      v0 = fmaf_(e0, qd, v0); v1 = fmaf_(e1, qd, v1); v2 = fmaf_(e2, qd, v2);
     }
     const float dmax = MF::foot_solimp[1], tc = MF::foot_solref[0], dr = MF::foot_solref[1];
     const float bcoef = 2.f / (dmax * tc);
@@ -737,7 +755,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const float ud = ub * s.u.fac.invD[b];
 #pragma unroll
       for (int k = 0; k < 6; ++k) {
-        const float c = pb[k] + Ub[k] * ud;
+        const float c = fmaf_(Ub[k], ud, pb[k]);
         if (par == 16) p16[k] += c;
         else if (par == 1) p1[k] += c;
         else car[k] = 0.f + c;
@@ -758,14 +776,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       for (int i = 0; i < 6; ++i) {
         float a = rhs6[i];
 #pragma unroll
-        for (int k = 0; k < i; ++k) a -= Lf[i * 6 + k] * qdd[k];
+        for (int k = 0; k < i; ++k) a = fmaf_(-Lf[i * 6 + k], qdd[k], a);
         qdd[i] = div_rn(a, Lf[i * 6 + i], s.u.fac.Dinv[i]);
       }
 #pragma unroll
       for (int i = 5; i >= 0; --i) {
         float a = qdd[i];
 #pragma unroll
-        for (int k = i + 1; k < 6; ++k) a -= Lf[k * 6 + i] * qdd[k];
+        for (int k = i + 1; k < 6; ++k) a = fmaf_(-Lf[k * 6 + i], qdd[k], a);
         qdd[i] = div_rn(a, Lf[i * 6 + i], s.u.fac.Dinv[i]);
       }
     }
@@ -776,7 +794,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int i = 0; i < 6; ++i) {
       float a = 0.f;
 #pragma unroll
-      for (int k = 0; k < 6; ++k) a += s.u.fac.S[k][i] * qdd[k];
+      for (int k = 0; k < 6; ++k) a = fmaf_(s.u.fac.S[k][i], qdd[k], a);
       a1[i] = 0.f + a;
       a16[i] = 0.f;
       ac[i] = 0.f;
@@ -798,7 +816,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       if (wr) ycol[d] = q;
 #pragma unroll
       for (int k = 0; k < 6; ++k) {
-        ac[k] = ap[k] + Sd[k] * q;
+        ac[k] = fmaf_(Sd[k], q, ap[k]);
         if (b == 16) a16[k] = ac[k];
       }
       G1_PIN6(ac);
@@ -824,7 +842,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int k = 0; k < kContactDofs; ++k) {
       const int a = (k < 6) ? legbase + 5 - k : k - 6;
       const float qa = s.Mm[0][a];
-      bb0 += s.Eb[l][0][k] * qa; bb1 += s.Eb[l][1][k] * qa; bb2 += s.Eb[l][2][k] * qa;
+      bb0 = fmaf_(s.Eb[l][0][k], qa, bb0); bb1 = fmaf_(s.Eb[l][1][k], qa, bb1); bb2 = fmaf_(s.Eb[l][2][k], qa, bb2);
     }
   }
   __syncthreads();   // factor region is dead from here on: the Gram blocks overwrite it
@@ -841,7 +859,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         for (int k = 0; k < kContactDofs; ++k) {
           const int a = (k < 6) ? legbase + 5 - k : k - 6;
           const float mv = s.Mm[j][a];
-          g0 += s.Eb[c][0][k] * mv; g1 += s.Eb[c][1][k] * mv; g2 += s.Eb[c][2][k] * mv;
+          g0 = fmaf_(s.Eb[c][0][k], mv, g0); g1 = fmaf_(s.Eb[c][1][k], mv, g1); g2 = fmaf_(s.Eb[c][2][k], mv, g2);
         }
         const int pr = cp * (cp + 1) / 2 + c;
         s.u.G[pr][0 * 3 + bcol] = g0; s.u.G[pr][1 * 3 + bcol] = g1; s.u.G[pr][2 * 3 + bcol] = g2;
@@ -849,10 +867,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
   }
   if (l < ncon) {
-    s.bvec[4 * l + 0] = 1.f * bb0 + 1.f * bb1 + 0.f * bb2 - s.aref[4 * l + 0];
-    s.bvec[4 * l + 1] = 1.f * bb0 + -1.f * bb1 + 0.f * bb2 - s.aref[4 * l + 1];
-    s.bvec[4 * l + 2] = 1.f * bb0 + 0.f * bb1 + 1.f * bb2 - s.aref[4 * l + 2];
-    s.bvec[4 * l + 3] = 1.f * bb0 + 0.f * bb1 + -1.f * bb2 - s.aref[4 * l + 3];
+    s.bvec[4 * l + 0] = fmaf_(0.f, bb2, fmaf_(1.f, bb1, 1.f * bb0)) - s.aref[4 * l + 0];
+    s.bvec[4 * l + 1] = fmaf_(0.f, bb2, fmaf_(-1.f, bb1, 1.f * bb0)) - s.aref[4 * l + 1];
+    s.bvec[4 * l + 2] = fmaf_(1.f, bb2, fmaf_(0.f, bb1, 1.f * bb0)) - s.aref[4 * l + 2];
+    s.bvec[4 * l + 3] = fmaf_(-1.f, bb2, fmaf_(0.f, bb1, 1.f * bb0)) - s.aref[4 * l + 3];
   }
   __syncthreads();
 
@@ -878,10 +896,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       else { lo = ci; hi = ci; klo = ki > k2 ? ki : k2; khi = ki > k2 ? k2 : ki; }
       const float* G = s.u.G[hi * (hi + 1) / 2 + lo];
       const float d0 = dcoef(klo, 0), d1 = dcoef(klo, 1), d2 = dcoef(klo, 2);
-      const float t0 = d0 * G[0] + d1 * G[3] + d2 * G[6];
-      const float t1 = d0 * G[1] + d1 * G[4] + d2 * G[7];
-      const float t2 = d0 * G[2] + d1 * G[5] + d2 * G[8];
-      val = t0 * dcoef(khi, 0) + t1 * dcoef(khi, 1) + t2 * dcoef(khi, 2);
+      const float t0 = fmaf_(d2, G[6], fmaf_(d1, G[3], d0 * G[0]));
+      const float t1 = fmaf_(d2, G[7], fmaf_(d1, G[4], d0 * G[1]));
+      const float t2 = fmaf_(d2, G[8], fmaf_(d1, G[5], d0 * G[2]));
+      val = fmaf_(t2, dcoef(khi, 2), fmaf_(t1, dcoef(khi, 1), t0 * dcoef(khi, 0)));
       if (ii == l) val += s.Rc[ci];
     }
     Acol[ii] = val;
@@ -905,7 +923,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int ii = 0; ii < kMaxEfc; ++ii) {
       if (ii < nefc_max) {
         const float sum = gsum(Acol[ii] * fi);   // sum_j A[ii][j] f_j (lane j holds column j)
-        const float ri = (bi + sum) - Aii * fi;
+        const float ri = fmaf_(-Aii, fi, bi + sum);
         const float x = -ri;
         const float q0 = x * yi;
         const float fn = __builtin_fmaf(__builtin_fmaf(-q0, Aii, x), yi, q0);
@@ -927,7 +945,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       for (int c = 0; c < ncon; ++c) {
         const float f0 = s.f[4 * c], f1 = s.f[4 * c + 1], f2 = s.f[4 * c + 2], f3 = s.f[4 * c + 3];
         const float fb0 = f0 + f1 + f2 + f3, fb1 = f0 - f1, fb2 = f2 - f3;
-        dq += fb0 * s.Mm[1 + 3 * c][d] + fb1 * s.Mm[2 + 3 * c][d] + fb2 * s.Mm[3 + 3 * c][d];
+        dq += fmaf_(fb2, s.Mm[3 + 3 * c][d], fmaf_(fb1, s.Mm[2 + 3 * c][d], fb0 * s.Mm[1 + 3 * c][d]));
       }
       s.qacc[d] = s.Mm[0][d] + dq;
     }
@@ -949,7 +967,7 @@ __device__ __forceinline__ void integrate_lane(const LaneModel& L, LaneState& st
                                                bool guard) {
   const float dt = MF::dt;
   auto upd = [&](float v, float a) {
-    float n = v + dt * a;
+    float n = fmaf_(dt, a, v);
     if (guard) {
       if (!isfinite(n)) n = 0.f;
       if (n > 50.f) n = 50.f; else if (n < -50.f) n = -50.f;
@@ -958,14 +976,15 @@ __device__ __forceinline__ void integrate_lane(const LaneModel& L, LaneState& st
   };
   if (L.hinge) {
     st.jqd = upd(st.jqd, jqacc);
-    st.jq += dt * st.jqd;
+    st.jq = fmaf_(dt, st.jqd, st.jq);
   }
   if (L.l == 1) {
 #pragma unroll
     for (int k = 0; k < 6; ++k) st.bqd[k] = upd(st.bqd[k], bqacc[k]);
-    st.bq[0] += dt * st.bqd[0]; st.bq[1] += dt * st.bqd[1]; st.bq[2] += dt * st.bqd[2];
+    st.bq[0] = fmaf_(dt, st.bqd[0], st.bq[0]); st.bq[1] = fmaf_(dt, st.bqd[1], st.bq[1]);
+    st.bq[2] = fmaf_(dt, st.bqd[2], st.bq[2]);
     V3 v{st.bqd[3] * dt, st.bqd[4] * dt, st.bqd[5] * dt};
-    const float ang = sqrtf(v.x * v.x + v.y * v.y + v.z * v.z);
+    const float ang = sqrtf(fmaf_(v.z, v.z, fmaf_(v.y, v.y, v.x * v.x)));
     Q4 dq;
     if (ang < 1e-9f) dq = {1.f, 0.5f * v.x, 0.5f * v.y, 0.5f * v.z};
     else {

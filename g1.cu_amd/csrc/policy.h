@@ -52,7 +52,9 @@ __device__ __forceinline__ float obs_value(const float* qp, const float* qv, con
   if (i < 9) {
     const float w = qp[3], x = qp[4], y = qp[5], z = qp[6];
     // third row of quat2mat(q), negated: R^T (0,0,-1)
-    const float r = (i == 6) ? 2 * (x * z - w * y) : (i == 7) ? 2 * (y * z + w * x) : 1 - 2 * (x * x + y * y);
+    const float r = (i == 6)   ? 2.f * __builtin_fmaf(-w, y, x * z)
+                    : (i == 7) ? 2.f * __builtin_fmaf(w, x, y * z)
+                               : __builtin_fmaf(-2.f, __builtin_fmaf(y, y, x * x), 1.f);
     return -r;
   }
   if (i < 38) return qp[7 + (i - 9)];

@@ -7,8 +7,9 @@
 // Every function restates the reference's arithmetic in the reference's operation order (fp32
 // parity is order-sensitive), templated on the scalar type so the same code yields the fp32
 // oracle (parity vs the GPU) and the fp64 oracle (parity vs the MuJoCo fixtures). Citations are
-// file:line into the reference tree (Infatoshi/g1.cu). Build: oracle/Makefile (-ffp-contract=off,
-// no -march: results are identical on every x86-64 host).
+// file:line into the reference tree (Infatoshi/g1.cu). Build: oracle/Makefile (-ffp-contract=off:
+// the only fused operations are the explicit fma_ calls; -mfma: hardware fma, which returns the
+// same correctly rounded results as the library fma on every x86-64 host that has it).
 //
 // Pinning (tests/test_oracle_*.py): FK/bias/qacc/M against bench/ref_traj.npz (MuJoCo fp64);
 // fp32 bias/qacc against bench/cuda_fk.bin and aba_qacc.bin; 300-step smooth trajectories against
@@ -36,27 +37,33 @@ template <class R> using M = ModelT<R>;
 template <class R> struct V3 { R x, y, z; };
 template <class R> struct Q4 { R w, x, y, z; };
 
+// Fused multiply-add, the one contraction this restatement uses, always explicit: a sum of
+// products a0 b0 + a1 b1 + ... is evaluated left to right as s = a0 b0, s = fma(a_i, b_i, s)
+// (a difference as fma(-a_i, b_i, s)); an accumulation s = 0; s += a_i b_i as s = fma(a_i, b_i, s)
+// from s = 0; x + a b as fma(a, b, x). Everything else rounds every operation (-ffp-contract=off).
+template <class R> static inline R fma_(R a, R b, R c) { return std::fma(a, b, c); }
+
 template <class R> static inline V3<R> vadd(V3<R> a, V3<R> b) { return {a.x + b.x, a.y + b.y, a.z + b.z}; }
 template <class R> static inline V3<R> vsub(V3<R> a, V3<R> b) { return {a.x - b.x, a.y - b.y, a.z - b.z}; }
 template <class R> static inline V3<R> cross(V3<R> a, V3<R> b) {
-  return {a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+  return {fma_(-a.z, b.y, a.y * b.z), fma_(-a.x, b.z, a.z * b.x), fma_(-a.y, b.x, a.x * b.y)};
 }
-template <class R> static inline R dot3(V3<R> a, V3<R> b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+template <class R> static inline R dot3(V3<R> a, V3<R> b) { return fma_(a.z, b.z, fma_(a.y, b.y, a.x * b.x)); }
 
 // Hamilton product (reference: src/dynamics.cuh:17-24)
 template <class R> static inline Q4<R> qmul(Q4<R> a, Q4<R> b) {
-  return {a.w * b.w - a.x * b.x - a.y * b.y - a.z * b.z,
-          a.w * b.x + a.x * b.w + a.y * b.z - a.z * b.y,
-          a.w * b.y - a.x * b.z + a.y * b.w + a.z * b.x,
-          a.w * b.z + a.x * b.y - a.y * b.x + a.z * b.w};
+  return {fma_(-a.z, b.z, fma_(-a.y, b.y, fma_(-a.x, b.x, a.w * b.w))),
+          fma_(-a.z, b.y, fma_(a.y, b.z, fma_(a.x, b.w, a.w * b.x))),
+          fma_(a.z, b.x, fma_(a.y, b.w, fma_(-a.x, b.z, a.w * b.y))),
+          fma_(a.z, b.w, fma_(-a.y, b.x, fma_(a.x, b.y, a.w * b.z)))};
 }
 // v' = v + w t + u x t, t = 2 u x v (reference: src/dynamics.cuh:26-35)
 template <class R> static inline V3<R> qrot(Q4<R> q, V3<R> v) {
   V3<R> u{q.x, q.y, q.z};
-  V3<R> t{R(2) * (u.y * v.z - u.z * v.y), R(2) * (u.z * v.x - u.x * v.z), R(2) * (u.x * v.y - u.y * v.x)};
-  return {v.x + q.w * t.x + (u.y * t.z - u.z * t.y),
-          v.y + q.w * t.y + (u.z * t.x - u.x * t.z),
-          v.z + q.w * t.z + (u.x * t.y - u.y * t.x)};
+  V3<R> c = cross(u, v);
+  V3<R> t{R(2) * c.x, R(2) * c.y, R(2) * c.z};
+  V3<R> ut = cross(u, t);
+  return {fma_(q.w, t.x, v.x) + ut.x, fma_(q.w, t.y, v.y) + ut.y, fma_(q.w, t.z, v.z) + ut.z};
 }
 // fp32 transcendentals are correctly rounded (evaluated in fp64, rounded once), so every
 // implementation of the algorithm that does the same yields bit-identical values: the contact
@@ -67,7 +74,7 @@ template <class R> static inline R pow_(R x, R y) { return R(std::pow(double(x),
 template <class R> static inline R rsqrt_(R x) { return R(1) / std::sqrt(x); }
 // (reference: src/dynamics.cuh:36-39)
 template <class R> static inline Q4<R> qnorm(Q4<R> q) {
-  R n = rsqrt_(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+  R n = rsqrt_(fma_(q.z, q.z, fma_(q.y, q.y, fma_(q.x, q.x, q.w * q.w))));
   return {q.w * n, q.x * n, q.y * n, q.z * n};
 }
 // (reference: src/dynamics.cuh:40-43)
@@ -81,9 +88,10 @@ template <class R> struct M3 { R m[9]; };
 template <class R> static inline M3<R> quat2mat(Q4<R> q) {
   R w = q.w, x = q.x, y = q.y, z = q.z;
   M3<R> r;
-  r.m[0] = 1 - 2 * (y * y + z * z); r.m[1] = 2 * (x * y - w * z);     r.m[2] = 2 * (x * z + w * y);
-  r.m[3] = 2 * (x * y + w * z);     r.m[4] = 1 - 2 * (x * x + z * z); r.m[5] = 2 * (y * z - w * x);
-  r.m[6] = 2 * (x * z - w * y);     r.m[7] = 2 * (y * z + w * x);     r.m[8] = 1 - 2 * (x * x + y * y);
+  // 1 - 2 s is fma(-2, s, 1) exactly (2 s is exact)
+  r.m[0] = fma_(R(-2), fma_(z, z, y * y), R(1)); r.m[1] = 2 * fma_(-w, z, x * y); r.m[2] = 2 * fma_(w, y, x * z);
+  r.m[3] = 2 * fma_(w, z, x * y); r.m[4] = fma_(R(-2), fma_(z, z, x * x), R(1)); r.m[5] = 2 * fma_(-w, x, y * z);
+  r.m[6] = 2 * fma_(-w, y, x * z); r.m[7] = 2 * fma_(w, x, y * z); r.m[8] = fma_(R(-2), fma_(y, y, x * x), R(1));
   return r;
 }
 // R diag(d) R^T (reference: src/dynamics.cuh:109-115)
@@ -91,13 +99,13 @@ template <class R> static inline M3<R> world_inertia(const M3<R>& Rm, V3<R> d) {
   M3<R> o;
   for (int i = 0; i < 3; ++i)
     for (int j = 0; j < 3; ++j)
-      o.m[3 * i + j] = Rm.m[3 * i + 0] * d.x * Rm.m[3 * j + 0] + Rm.m[3 * i + 1] * d.y * Rm.m[3 * j + 1] +
-                       Rm.m[3 * i + 2] * d.z * Rm.m[3 * j + 2];
+      o.m[3 * i + j] = fma_(Rm.m[3 * i + 2] * d.z, Rm.m[3 * j + 2],
+                            fma_(Rm.m[3 * i + 1] * d.y, Rm.m[3 * j + 1], Rm.m[3 * i + 0] * d.x * Rm.m[3 * j + 0]));
   return o;
 }
 template <class R> static inline V3<R> mat3vec(const M3<R>& A, V3<R> v) {
-  return {A.m[0] * v.x + A.m[1] * v.y + A.m[2] * v.z, A.m[3] * v.x + A.m[4] * v.y + A.m[5] * v.z,
-          A.m[6] * v.x + A.m[7] * v.y + A.m[8] * v.z};
+  return {fma_(A.m[2], v.z, fma_(A.m[1], v.y, A.m[0] * v.x)), fma_(A.m[5], v.z, fma_(A.m[4], v.y, A.m[3] * v.x)),
+          fma_(A.m[8], v.z, fma_(A.m[7], v.y, A.m[6] * v.x))};
 }
 
 // rigid-body inertia about the common reference point (Iw about com, com offset c, mass m)
@@ -109,11 +117,12 @@ template <class R> static inline void apply_inertia(const SpatInert<R>& I, V3<R>
   V3<R> Asw = mat3vec(I.Iw, sw);
   R cc = dot3(c, c);
   R csw = dot3(c, sw);
-  Asw = {Asw.x + m * (cc * sw.x - csw * c.x), Asw.y + m * (cc * sw.y - csw * c.y), Asw.z + m * (cc * sw.z - csw * c.z)};
+  Asw = {fma_(m, fma_(-csw, c.x, cc * sw.x), Asw.x), fma_(m, fma_(-csw, c.y, cc * sw.y), Asw.y),
+         fma_(m, fma_(-csw, c.z, cc * sw.z), Asw.z)};
   V3<R> mc_sv = cross(c, sv);
-  fw = {Asw.x + m * mc_sv.x, Asw.y + m * mc_sv.y, Asw.z + m * mc_sv.z};
+  fw = {fma_(m, mc_sv.x, Asw.x), fma_(m, mc_sv.y, Asw.y), fma_(m, mc_sv.z, Asw.z)};
   V3<R> c_sw = cross(c, sw);
-  fv = {-m * c_sw.x + m * sv.x, -m * c_sw.y + m * sv.y, -m * c_sw.z + m * sv.z};
+  fv = {fma_(m, sv.x, -m * c_sw.x), fma_(m, sv.y, -m * c_sw.y), fma_(m, sv.z, -m * c_sw.z)};
 }
 // motion x motion (reference: src/dynamics.cuh:142-146)
 template <class R> static inline void crossm(V3<R> w1, V3<R> v1, V3<R> w2, V3<R> v2, V3<R>& ow, V3<R>& ov) {
@@ -222,31 +231,31 @@ template <class R> void compute_bias(const R* qvel, const Frames<R>& F, R* S, R*
         R qd = qvel[a];
         col(a, sw, sv);
         crossm(w, v, sw, sv, Sdw[a], Sdv[a]);
-        w = {w.x + sw.x * qd, w.y + sw.y * qd, w.z + sw.z * qd};
-        v = {v.x + sv.x * qd, v.y + sv.y * qd, v.z + sv.z * qd};
+        w = {fma_(sw.x, qd, w.x), fma_(sw.y, qd, w.y), fma_(sw.z, qd, w.z)};
+        v = {fma_(sv.x, qd, v.x), fma_(sv.y, qd, v.y), fma_(sv.z, qd, v.z)};
       }
       V3<R> wr = w, vr = v;
       for (int a = da + 3; a < da + 6; ++a) { col(a, sw, sv); crossm(wr, vr, sw, sv, Sdw[a], Sdv[a]); }
       for (int a = da + 3; a < da + 6; ++a) {
         R qd = qvel[a];
-        w = {w.x + S[a * 6 + 0] * qd, w.y + S[a * 6 + 1] * qd, w.z + S[a * 6 + 2] * qd};
-        v = {v.x + S[a * 6 + 3] * qd, v.y + S[a * 6 + 4] * qd, v.z + S[a * 6 + 5] * qd};
+        w = {fma_(S[a * 6 + 0], qd, w.x), fma_(S[a * 6 + 1], qd, w.y), fma_(S[a * 6 + 2], qd, w.z)};
+        v = {fma_(S[a * 6 + 3], qd, v.x), fma_(S[a * 6 + 4], qd, v.y), fma_(S[a * 6 + 5], qd, v.z)};
       }
     } else {
       for (int a = da; a < da + dn; ++a) {
         R qd = qvel[a];
         col(a, sw, sv);
         crossm(w, v, sw, sv, Sdw[a], Sdv[a]);
-        w = {w.x + sw.x * qd, w.y + sw.y * qd, w.z + sw.z * qd};
-        v = {v.x + sv.x * qd, v.y + sv.y * qd, v.z + sv.z * qd};
+        w = {fma_(sw.x, qd, w.x), fma_(sw.y, qd, w.y), fma_(sw.z, qd, w.z)};
+        v = {fma_(sv.x, qd, v.x), fma_(sv.y, qd, v.y), fma_(sv.z, qd, v.z)};
       }
     }
     vw[b] = w; vv[b] = v;
     V3<R> aaw = aw[par], aav = av[par];
     for (int a = da; a < da + dn; ++a) {
       R qd = qvel[a];
-      aaw = {aaw.x + Sdw[a].x * qd, aaw.y + Sdw[a].y * qd, aaw.z + Sdw[a].z * qd};
-      aav = {aav.x + Sdv[a].x * qd, aav.y + Sdv[a].y * qd, aav.z + Sdv[a].z * qd};
+      aaw = {fma_(Sdw[a].x, qd, aaw.x), fma_(Sdw[a].y, qd, aaw.y), fma_(Sdw[a].z, qd, aaw.z)};
+      aav = {fma_(Sdv[a].x, qd, aav.x), fma_(Sdv[a].y, qd, aav.y), fma_(Sdv[a].z, qd, aav.z)};
     }
     aw[b] = aaw; av[b] = aav;
   }
@@ -263,8 +272,8 @@ template <class R> void compute_bias(const R* qvel, const Frames<R>& F, R* S, R*
   for (int b = kNBody - 1; b >= 1; --b) {
     int da = body_dofadr[b], dn = body_dofnum[b];
     for (int a = da; a < da + dn; ++a)
-      bias[a] = S[a * 6 + 0] * fw[b].x + S[a * 6 + 1] * fw[b].y + S[a * 6 + 2] * fw[b].z +
-                S[a * 6 + 3] * fv[b].x + S[a * 6 + 4] * fv[b].y + S[a * 6 + 5] * fv[b].z;
+      bias[a] = fma_(S[a * 6 + 5], fv[b].z, fma_(S[a * 6 + 4], fv[b].y, fma_(S[a * 6 + 3], fv[b].x,
+                fma_(S[a * 6 + 2], fw[b].z, fma_(S[a * 6 + 1], fw[b].y, S[a * 6 + 0] * fw[b].x)))));
     int par = body_parent[b];
     if (par >= 1) { fw[par] = vadd(fw[par], fw[b]); fv[par] = vadd(fv[par], fv[b]); }
   }
@@ -278,13 +287,13 @@ static inline int symidx(int i, int j) {
 }
 template <class R> static inline R dot6(const R* a, const R* b) {
   R s = 0;
-  for (int i = 0; i < 6; ++i) s += a[i] * b[i];
+  for (int i = 0; i < 6; ++i) s = fma_(a[i], b[i], s);
   return s;
 }
 template <class R> static inline void symmv6(const R* P, const R* x, R* o) {
   for (int i = 0; i < 6; ++i) {
     R s = 0;
-    for (int j = 0; j < 6; ++j) s += P[symidx(i, j)] * x[j];
+    for (int j = 0; j < 6; ++j) s = fma_(P[symidx(i, j)], x[j], s);
     o[i] = s;
   }
 }
@@ -299,9 +308,9 @@ template <class R> void spatial_inertia6(const Frames<R>& F, int b, R* X) {
   R cc = dot3(c, c);
   R A[9];
   for (int i = 0; i < 9; ++i) A[i] = Iw.m[i];
-  A[0] += m * (cc - c.x * c.x); A[1] += m * (-c.x * c.y); A[2] += m * (-c.x * c.z);
-  A[3] += m * (-c.y * c.x);     A[4] += m * (cc - c.y * c.y); A[5] += m * (-c.y * c.z);
-  A[6] += m * (-c.z * c.x);     A[7] += m * (-c.z * c.y); A[8] += m * (cc - c.z * c.z);
+  A[0] = fma_(m, fma_(-c.x, c.x, cc), A[0]); A[1] = fma_(m, -c.x * c.y, A[1]); A[2] = fma_(m, -c.x * c.z, A[2]);
+  A[3] = fma_(m, -c.y * c.x, A[3]); A[4] = fma_(m, fma_(-c.y, c.y, cc), A[4]); A[5] = fma_(m, -c.y * c.z, A[5]);
+  A[6] = fma_(m, -c.z * c.x, A[6]); A[7] = fma_(m, -c.z * c.y, A[7]); A[8] = fma_(m, fma_(-c.z, c.z, cc), A[8]);
   R Bx[9] = {0, -c.z, c.y, c.z, 0, -c.x, -c.y, c.x, 0};
   R M6[36];
   for (int i = 0; i < 3; ++i)
@@ -333,7 +342,7 @@ template <class R> void factorize(const Frames<R>& F, const R* S, const R* Bdiag
     for (int k = 0; k < 6; ++k) fac.U[b * 6 + k] = U[k];
     fac.invD[b] = invD;
     for (int i = 0; i < 6; ++i)
-      for (int j = i; j < 6; ++j) IA[par * 21 + symidx(i, j)] += IA[b * 21 + symidx(i, j)] - U[i] * U[j] * invD;
+      for (int j = i; j < 6; ++j) IA[par * 21 + symidx(i, j)] += fma_(-(U[i] * U[j]), invD, IA[b * 21 + symidx(i, j)]);
   }
   int d = body_dofadr[1];
   R Dm[36];
@@ -345,13 +354,13 @@ template <class R> void factorize(const Frames<R>& F, const R* S, const R* Bdiag
   for (int k = 0; k < 6; ++k)
     for (int l = 0; l < 6; ++l) {
       R s = 0;
-      for (int i = 0; i < 6; ++i) s += S[(d + k) * 6 + i] * fac.U6[i * 6 + l];
+      for (int i = 0; i < 6; ++i) s = fma_(S[(d + k) * 6 + i], fac.U6[i * 6 + l], s);
       Dm[k * 6 + l] = s + (k == l ? (M<R>::dof_armature[d + k] + (Bdiag ? Bdiag[d + k] : R(0))) : R(0));
     }
   for (int i = 0; i < 6; ++i)
     for (int j = 0; j <= i; ++j) {
       R s = Dm[i * 6 + j];
-      for (int kk = 0; kk < j; ++kk) s -= Dm[i * 6 + kk] * Dm[j * 6 + kk];
+      for (int kk = 0; kk < j; ++kk) s = fma_(-Dm[i * 6 + kk], Dm[j * 6 + kk], s);
       if (i == j) Dm[i * 6 + i] = std::sqrt(s); else Dm[i * 6 + j] = s / Dm[j * 6 + j];
     }
   for (int i = 0; i < 36; ++i) fac.Dfac6[i] = Dm[i];
@@ -366,7 +375,7 @@ template <class R> void solveM(const Factor<R>& fac, const R* S, const R* x, R* 
     const R* U = &fac.U[b * 6];
     R u = x[d] - dot6(&S[d * 6], &pA[b * 6]);
     R ud = u * fac.invD[b];
-    for (int k = 0; k < 6; ++k) pA[par * 6 + k] += pA[b * 6 + k] + U[k] * ud;
+    for (int k = 0; k < 6; ++k) pA[par * 6 + k] += fma_(U[k], ud, pA[b * 6 + k]);
   }
   {
     int d = body_dofadr[1];
@@ -375,25 +384,25 @@ template <class R> void solveM(const Factor<R>& fac, const R* S, const R* x, R* 
     for (int k = 0; k < 6; ++k) {
       R uk = x[d + k] - dot6(&S[(d + k) * 6], &pA[6]);
       R UTa = 0;
-      for (int i = 0; i < 6; ++i) UTa += fac.U6[i * 6 + k] * ap[i];
+      for (int i = 0; i < 6; ++i) UTa = fma_(fac.U6[i * 6 + k], ap[i], UTa);
       rhs[k] = uk - UTa;
     }
     R qdd[6];
     const R* L = fac.Dfac6;
     for (int i = 0; i < 6; ++i) {
       R s = rhs[i];
-      for (int k = 0; k < i; ++k) s -= L[i * 6 + k] * qdd[k];
+      for (int k = 0; k < i; ++k) s = fma_(-L[i * 6 + k], qdd[k], s);
       qdd[i] = s / L[i * 6 + i];
     }
     for (int i = 5; i >= 0; --i) {
       R s = qdd[i];
-      for (int k = i + 1; k < 6; ++k) s -= L[k * 6 + i] * qdd[k];
+      for (int k = i + 1; k < 6; ++k) s = fma_(-L[k * 6 + i], qdd[k], s);
       qdd[i] = s / L[i * 6 + i];
     }
     for (int k = 0; k < 6; ++k) y[d + k] = qdd[k];
     for (int i = 0; i < 6; ++i) {
       R Sq = 0;
-      for (int k = 0; k < 6; ++k) Sq += S[(d + k) * 6 + i] * qdd[k];
+      for (int k = 0; k < 6; ++k) Sq = fma_(S[(d + k) * 6 + i], qdd[k], Sq);
       a6[6 + i] = ap[i] + Sq;
     }
   }
@@ -405,7 +414,7 @@ template <class R> void solveM(const Factor<R>& fac, const R* S, const R* x, R* 
     R u = x[d] - dot6(&S[d * 6], &pA[b * 6]);
     R qdd = (u - dot6(U, ap)) * fac.invD[b];
     y[d] = qdd;
-    for (int i = 0; i < 6; ++i) a6[b * 6 + i] = ap[i] + S[d * 6 + i] * qdd;
+    for (int i = 0; i < 6; ++i) a6[b * 6 + i] = fma_(S[d * 6 + i], qdd, ap[i]);
   }
 }
 
@@ -419,33 +428,33 @@ template <class R> void solveM_multi1(const Factor<R>& fac, const R* S, const R*
     const R* U = &fac.U[b * 6];
     const R* Sd = &S[d * 6];
     R ud = x[d];
-    for (int i = 0; i < 6; ++i) ud -= Sd[i] * pA[b * 6 + i];
+    for (int i = 0; i < 6; ++i) ud = fma_(-Sd[i], pA[b * 6 + i], ud);
     ud *= fac.invD[b];
-    for (int i = 0; i < 6; ++i) pA[par * 6 + i] += pA[b * 6 + i] + U[i] * ud;
+    for (int i = 0; i < 6; ++i) pA[par * 6 + i] += fma_(U[i], ud, pA[b * 6 + i]);
   }
   {
     int d = body_dofadr[1];
     R qdd[6];
     for (int i = 0; i < 6; ++i) {
       R s = 0;
-      for (int j = 0; j < 6; ++j) s += S[(d + i) * 6 + j] * pA[6 + j];
+      for (int j = 0; j < 6; ++j) s = fma_(S[(d + i) * 6 + j], pA[6 + j], s);
       qdd[i] = x[d + i] - s;
     }
     const R* L = fac.Dfac6;
     for (int i = 0; i < 6; ++i) {
       R s = qdd[i];
-      for (int k = 0; k < i; ++k) s -= L[i * 6 + k] * qdd[k];
+      for (int k = 0; k < i; ++k) s = fma_(-L[i * 6 + k], qdd[k], s);
       qdd[i] = s / L[i * 6 + i];
     }
     for (int i = 5; i >= 0; --i) {
       R s = qdd[i];
-      for (int k = i + 1; k < 6; ++k) s -= L[k * 6 + i] * qdd[k];
+      for (int k = i + 1; k < 6; ++k) s = fma_(-L[k * 6 + i], qdd[k], s);
       qdd[i] = s / L[i * 6 + i];
     }
     for (int k = 0; k < 6; ++k) y[d + k] = qdd[k];
     for (int i = 0; i < 6; ++i) {
       R Sq = 0;
-      for (int k = 0; k < 6; ++k) Sq += S[(d + k) * 6 + i] * qdd[k];
+      for (int k = 0; k < 6; ++k) Sq = fma_(S[(d + k) * 6 + i], qdd[k], Sq);
       a6[6 + i] = Sq;
     }
   }
@@ -454,10 +463,10 @@ template <class R> void solveM_multi1(const Factor<R>& fac, const R* S, const R*
     const R* U = &fac.U[b * 6];
     const R* Sd = &S[d * 6];
     R qdd = x[d];
-    for (int i = 0; i < 6; ++i) qdd -= Sd[i] * pA[b * 6 + i] + U[i] * a6[par * 6 + i];
+    for (int i = 0; i < 6; ++i) qdd -= fma_(U[i], a6[par * 6 + i], Sd[i] * pA[b * 6 + i]);
     qdd *= fac.invD[b];
     y[d] = qdd;
-    for (int i = 0; i < 6; ++i) a6[b * 6 + i] = a6[par * 6 + i] + Sd[i] * qdd;
+    for (int i = 0; i < 6; ++i) a6[b * 6 + i] = fma_(Sd[i], qdd, a6[par * 6 + i]);
   }
 }
 
@@ -511,9 +520,9 @@ template <class R> R foot_impedance(R pos) {
   else {
     R a = R(1) / pow_(mid, power - R(1));
     R b = R(1) / pow_(R(1) - mid, power - R(1));
-    y = (x < mid) ? a * pow_(x, power) : R(1) - b * pow_(R(1) - x, power);
+    y = (x < mid) ? a * pow_(x, power) : fma_(-b, pow_(R(1) - x, power), R(1));
   }
-  return dmin + y * (dmax - dmin);
+  return fma_(y, dmax - dmin, dmin);
 }
 
 // Projected Gauss-Seidel on min 0.5 f'Af + f'b, f >= 0 (reference: src/contact.cuh:159-171)
@@ -523,8 +532,8 @@ template <class R> void solve_pgs(const R* A, const R* b, R* f, int n, int iters
     for (int i = 0; i < n; ++i) {
       R Aii = A[i * n + i];
       R ri = b[i];
-      for (int j = 0; j < n; ++j) ri += A[i * n + j] * f[j];
-      ri -= Aii * f[i];
+      for (int j = 0; j < n; ++j) ri = fma_(A[i * n + j], f[j], ri);
+      ri = fma_(-Aii, f[i], ri);
       R fi = -ri / Aii;
       f[i] = fi > R(0) ? fi : R(0);
     }
@@ -607,9 +616,9 @@ int env_qacc(const R* qp, const R* qv, const Frames<R>& F, const R* tau, const R
       R e0 = jc.z, e1 = mu * jc.y, e2 = -mu * jc.x;
       Eb[c][0][k] = e0; Eb[c][1][k] = e1; Eb[c][2][k] = e2;
       R qa = qacc_s[a];
-      b0 += e0 * qa; b1 += e1 * qa; b2 += e2 * qa;
+      b0 = fma_(e0, qa, b0); b1 = fma_(e1, qa, b1); b2 = fma_(e2, qa, b2);
       R qd = qv[a];
-      v0 += e0 * qd; v1 += e1 * qd; v2 += e2 * qd;
+      v0 = fma_(e0, qd, v0); v1 = fma_(e1, qd, v1); v2 = fma_(e2, qd, v2);
     }
     bb[c][0] = b0; bb[c][1] = b1; bb[c][2] = b2;
     R pen = cpen[c], imp = foot_impedance(pen);
@@ -643,19 +652,19 @@ int env_qacc(const R* qp, const R* qv, const Frames<R>& F, const R* tau, const R
         for (int k = 0; k < cnd[c]; ++k) {
           R v = Eb[c][a][k];
           int dd = cdof[c][k];
-          g0 += v * Mm[cp][0][dd]; g1 += v * Mm[cp][1][dd]; g2 += v * Mm[cp][2][dd];
+          g0 = fma_(v, Mm[cp][0][dd], g0); g1 = fma_(v, Mm[cp][1][dd], g1); g2 = fma_(v, Mm[cp][2][dd], g2);
         }
         G[a][0] = g0; G[a][1] = g1; G[a][2] = g2;
       }
       for (int k = 0; k < 4; ++k) {
         const R* dk = DC[k];
-        R t0 = dk[0] * G[0][0] + dk[1] * G[1][0] + dk[2] * G[2][0];
-        R t1 = dk[0] * G[0][1] + dk[1] * G[1][1] + dk[2] * G[2][1];
-        R t2 = dk[0] * G[0][2] + dk[1] * G[1][2] + dk[2] * G[2][2];
+        R t0 = fma_(dk[2], G[2][0], fma_(dk[1], G[1][0], dk[0] * G[0][0]));
+        R t1 = fma_(dk[2], G[2][1], fma_(dk[1], G[1][1], dk[0] * G[0][1]));
+        R t2 = fma_(dk[2], G[2][2], fma_(dk[1], G[1][2], dk[0] * G[0][2]));
         int i = 4 * c + k;
         for (int kp = 0; kp < 4; ++kp) {
           const R* dq4 = DC[kp];
-          R aij = t0 * dq4[0] + t1 * dq4[1] + t2 * dq4[2];
+          R aij = fma_(t2, dq4[2], fma_(t1, dq4[1], t0 * dq4[0]));
           int j = 4 * cp + kp;
           if (i == j) aij += Rr[i];
           A[i * nefc + j] = aij;
@@ -666,7 +675,7 @@ int env_qacc(const R* qp, const R* qv, const Frames<R>& F, const R* tau, const R
     for (int k = 0; k < 4; ++k) {
       const R* dk = DC[k];
       int i = 4 * c + k;
-      bvec[i] = dk[0] * bb[c][0] + dk[1] * bb[c][1] + dk[2] * bb[c][2] - aref[i];
+      bvec[i] = fma_(dk[2], bb[c][2], fma_(dk[1], bb[c][1], dk[0] * bb[c][0])) - aref[i];
     }
   }
   R f[kMaxEfc];
@@ -677,7 +686,7 @@ int env_qacc(const R* qp, const R* qv, const Frames<R>& F, const R* tau, const R
   for (int c = 0; c < ncon; ++c) {
     R f0 = f[4 * c], f1 = f[4 * c + 1], f2 = f[4 * c + 2], f3 = f[4 * c + 3];
     R fb0 = f0 + f1 + f2 + f3, fb1 = f0 - f1, fb2 = f2 - f3;
-    for (int a = 0; a < kNV; ++a) dq[a] += fb0 * Mm[c][0][a] + fb1 * Mm[c][1][a] + fb2 * Mm[c][2][a];
+    for (int a = 0; a < kNV; ++a) dq[a] += fma_(fb2, Mm[c][2][a], fma_(fb1, Mm[c][1][a], fb0 * Mm[c][0][a]));
   }
   for (int i = 0; i < kNV; ++i) qacc[i] = qacc_s[i] + dq[i];
   if (dbg) {
@@ -692,7 +701,7 @@ int env_qacc(const R* qp, const R* qv, const Frames<R>& F, const R* tau, const R
 // q <- normalize(q (x) exp(w dt)), w body-local (reference: src/dynamics.cuh:333-342)
 template <class R> void quat_integrate(R* q, V3<R> w, R dt) {
   V3<R> v{w.x * dt, w.y * dt, w.z * dt};
-  R ang = std::sqrt(v.x * v.x + v.y * v.y + v.z * v.z);
+  R ang = std::sqrt(fma_(v.z, v.z, fma_(v.y, v.y, v.x * v.x)));
   Q4<R> dq;
   if (ang < R(1e-9)) dq = {R(1), R(0.5) * v.x, R(0.5) * v.y, R(0.5) * v.z};
   else {
@@ -707,10 +716,11 @@ template <class R> void integrate_pos(R* qpos, const R* qvel, R dt) {
   for (int j = 0; j < kNJnt; ++j) {
     int qa = jnt_qposadr[j], da = jnt_dofadr[j];
     if (jnt_type[j] == 0) {
-      qpos[qa] += dt * qvel[da]; qpos[qa + 1] += dt * qvel[da + 1]; qpos[qa + 2] += dt * qvel[da + 2];
+      qpos[qa] = fma_(dt, qvel[da], qpos[qa]); qpos[qa + 1] = fma_(dt, qvel[da + 1], qpos[qa + 1]);
+      qpos[qa + 2] = fma_(dt, qvel[da + 2], qpos[qa + 2]);
       quat_integrate(&qpos[qa + 3], V3<R>{qvel[da + 3], qvel[da + 4], qvel[da + 5]}, dt);
     } else {
-      qpos[qa] += dt * qvel[da];
+      qpos[qa] = fma_(dt, qvel[da], qpos[qa]);
     }
   }
 }
@@ -739,7 +749,7 @@ void env_advance(R* lp, R* lv, R* pa, int* pstep, const R* a, const R* reset_noi
   R target[kAct];
   const R ACT_SCALE = R(0.5);
   for (int i = 0; i < kAct; ++i) {
-    R t = M<R>::qpos_stand[act_qadr[i]] + ACT_SCALE * a[i];
+    R t = fma_(ACT_SCALE, a[i], M<R>::qpos_stand[act_qadr[i]]);
     if (t < M<R>::act_ctrl_lo[i]) t = M<R>::act_ctrl_lo[i];
     if (t > M<R>::act_ctrl_hi[i]) t = M<R>::act_ctrl_hi[i];
     target[i] = t;
@@ -757,7 +767,7 @@ void env_advance(R* lp, R* lv, R* pa, int* pstep, const R* a, const R* reset_noi
     for (int i = 0; i < kNV; ++i) tau[i] = 0;
     for (int i = 0; i < kAct; ++i) {
       int d = act_dof[i];
-      R pdt = M<R>::act_kp[i] * (target[i] - lp[act_qadr[i]]) - M<R>::act_kd[i] * lv[d];
+      R pdt = fma_(-M<R>::act_kd[i], lv[d], M<R>::act_kp[i] * (target[i] - lp[act_qadr[i]]));
       if (pdt < M<R>::act_frc_lo[i]) pdt = M<R>::act_frc_lo[i];
       else if (pdt > M<R>::act_frc_hi[i]) pdt = M<R>::act_frc_hi[i];
       tau[d] = pdt;
@@ -766,7 +776,7 @@ void env_advance(R* lp, R* lv, R* pa, int* pstep, const R* a, const R* reset_noi
     int nc = env_qacc(lp, lv, F, tau, Bdt, Sm, qacc, pgs, mu);
     if (ncon_hist) ncon_hist[nc] += 1;
     for (int i = 0; i < kNV; ++i) {
-      R v = lv[i] + dt * qacc[i];
+      R v = fma_(dt, qacc[i], lv[i]);
       if (!std::isfinite(v)) v = 0;
       if (v > R(50)) v = R(50); else if (v < R(-50)) v = R(-50);
       lv[i] = v;
@@ -960,7 +970,7 @@ static void substep_batch(int n, R* qpos, R* qvel, const R* target, int pgs, R m
     for (int i = 0; i < kNV; ++i) tau[i] = 0;
     for (int i = 0; i < kAct; ++i) {
       int d = act_dof[i];
-      R pdt = M<R>::act_kp[i] * (tg[i] - lp[act_qadr[i]]) - M<R>::act_kd[i] * lv[d];
+      R pdt = fma_(-M<R>::act_kd[i], lv[d], M<R>::act_kp[i] * (tg[i] - lp[act_qadr[i]]));
       if (pdt < M<R>::act_frc_lo[i]) pdt = M<R>::act_frc_lo[i];
       else if (pdt > M<R>::act_frc_hi[i]) pdt = M<R>::act_frc_hi[i];
       tau[d] = pdt;
@@ -968,7 +978,7 @@ static void substep_batch(int n, R* qpos, R* qvel, const R* target, int pgs, R m
     int nc = env_qacc(lp, lv, F, tau, Bdt, S, qacc, pgs, mu);
     if (ncon) ncon[w] = nc;
     for (int i = 0; i < kNV; ++i) {
-      R v = lv[i] + dt * qacc[i];
+      R v = fma_(dt, qacc[i], lv[i]);
       if (!std::isfinite(v)) v = 0;
       if (v > R(50)) v = R(50); else if (v < R(-50)) v = R(-50);
       lv[i] = v;
@@ -991,7 +1001,7 @@ template <class R> static void smooth_traj(const R* q0, const R* v0, int nsteps,
     factorize(F, S, (const R*)nullptr, fac);
     for (int i = 0; i < kNV; ++i) rhs[i] = -bias[i];
     solveM(fac, S, rhs, qacc);
-    for (int i = 0; i < kNV; ++i) lv[i] += M<R>::dt * qacc[i];
+    for (int i = 0; i < kNV; ++i) lv[i] = fma_(M<R>::dt, qacc[i], lv[i]);
     integrate_pos(lp, lv, M<R>::dt);
     std::memcpy(qout + (long)(t + 1) * kNQ, lp, sizeof(lp));
     if (vout) std::memcpy(vout + (long)(t + 1) * kNV, lv, sizeof(lv));
@@ -1012,7 +1022,7 @@ template <class R> static void implicit_traj(const R* q0, const R* v0, const R* 
     for (int i = 0; i < kNV; ++i) tau[i] = 0;
     for (int i = 0; i < kAct; ++i) {
       int d = act_dof[i];
-      R pdt = M<R>::act_kp[i] * (tg[i] - lp[act_qadr[i]]) - M<R>::act_kd[i] * lv[d];
+      R pdt = fma_(-M<R>::act_kd[i], lv[d], M<R>::act_kp[i] * (tg[i] - lp[act_qadr[i]]));
       if (pdt < M<R>::act_frc_lo[i]) pdt = M<R>::act_frc_lo[i];
       else if (pdt > M<R>::act_frc_hi[i]) pdt = M<R>::act_frc_hi[i];
       tau[d] = pdt;
@@ -1021,7 +1031,7 @@ template <class R> static void implicit_traj(const R* q0, const R* v0, const R* 
     factorize(F, S, Bdt, fac);
     for (int i = 0; i < kNV; ++i) rhs[i] = -bias[i] + tau[i];
     solveM(fac, S, rhs, qacc);
-    for (int i = 0; i < kNV; ++i) lv[i] += M<R>::dt * qacc[i];
+    for (int i = 0; i < kNV; ++i) lv[i] = fma_(M<R>::dt, qacc[i], lv[i]);
     integrate_pos(lp, lv, M<R>::dt);
     std::memcpy(qout + (long)(t + 1) * kNQ, lp, sizeof(lp));
     std::memcpy(vout + (long)(t + 1) * kNV, lv, sizeof(lv));
