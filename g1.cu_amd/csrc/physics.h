@@ -476,69 +476,71 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   const int c_lo = grp == 3 ? 5 : 2, c_hi = grp >= 2 ? kMaxDepth : 7;
   float Dlr[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // row `crow` of the last body's downdate
   float cs[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};    // last body's pA + U u / D (all six components)
-  // this round's body inputs (motion axis, I6 row, right-hand side), loaded one round ahead
+  // the next level's body inputs (motion axis, I6 row, right-hand side, armature, dt kd; the
+  // last three live on lane b and come by shuffle), loaded while the current level computes
   auto chain_body = [&](int cd) { return (cd >= c_lo && cd <= c_hi) ? cd + c_off : 2; };
-  // body b's armature and dt kd live on lane b; the chain lanes fetch them with the rhs
   float Sn[6], In[6], xn, an, kn;
-  {
-    const int b = chain_body(kMaxDepth);
+  auto prefetch = [&](int cd) {
+    const int b = chain_body(cd);
 #pragma unroll
     for (int j = 0; j < 6; ++j) { Sn[j] = s.u.fac.S[b + 4][j]; In[j] = I6[b * 21 + symidx(rowc, j)]; }
     xn = gshfl(xr, b);
     an = gshfl(L.arm, b);
     kn = gshfl(L.bdt, b);
-  }
-#pragma unroll 1
-  for (int cd = kMaxDepth; cd >= 2; --cd) {
+  };
+  // one level of the chains; `junction` adds the right arm's downdate and bias force (gD, gc)
+  // to the torso before its own child's
+  auto level = [&](int cd, bool junction, const float* gD, const float* gc) {
     const bool act = cd >= c_lo && cd <= c_hi;
-    const int b = chain_body(cd);
     const bool leaf = cd == c_hi;
+    const int b = chain_body(cd);
     float Sd[6], IAr[6], pA[6];
     const float xb_ = xn, arm = an, bdt = kn;
 #pragma unroll
-    for (int j = 0; j < 6; ++j) { Sd[j] = Sn[j]; IAr[j] = In[j]; pA[j] = 0.f; }
-    if (cd > 2) {
-      const int bn = chain_body(cd - 1);
-#pragma unroll
-      for (int j = 0; j < 6; ++j) { Sn[j] = s.u.fac.S[bn + 4][j]; In[j] = I6[bn * 21 + symidx(rowc, j)]; }
-      xn = gshfl(xr, bn);
-      an = gshfl(L.arm, bn);
-      kn = gshfl(L.bdt, bn);
-    }
-    if (cd == body_depth[16]) {
-      // the right arm's last downdate and bias force join the torso first (lanes 24.. hold
-      // chain 3; the torso's own child 17 follows below)
-      const bool torso = grp == 2;
-#pragma unroll
-      for (int j = 0; j < 6; ++j) {
-        const float gD = gshfl(Dlr[j], 24 + rowc), gc = gshfl(cs[j], 24 + rowc);
-        if (torso) { IAr[j] = IAr[j] + gD; pA[j] = pA[j] + gc; }
-      }
-    }
-#pragma unroll
     for (int j = 0; j < 6; ++j) {
-      if (!leaf) { IAr[j] = IAr[j] + Dlr[j]; pA[j] = pA[j] + cs[j]; }
+      Sd[j] = Sn[j];
+      float v = In[j], q = 0.f;
+      if (junction) { v = v + gD[j]; q = q + gc[j]; }
+      IAr[j] = leaf ? v : v + Dlr[j];
+      pA[j] = leaf ? q : q + cs[j];
     }
     float ur = 0.f;
 #pragma unroll
     for (int j = 0; j < 6; ++j) ur = fmaf_(IAr[j], Sd[j], ur);
     const float Ub[6] = {chain_bcast<0>(ur), chain_bcast<1>(ur), chain_bcast<2>(ur),
                          chain_bcast<3>(ur), chain_bcast<4>(ur), chain_bcast<5>(ur)};
+    prefetch(cd - 1);   // (cd - 1 == 1 loads body 2 again; unused)
     float D = dot6(Sd, Ub) + arm;
     if (P.damped) D += bdt;
     const float invD = rcp_rn(D);
     const float u = xb_ - dot6(Sd, pA);
     const float ud = u * invD;
-    if (act) {
 #pragma unroll
-      for (int j = 0; j < 6; ++j) {
-        Dlr[j] = fmaf_(-(ur * Ub[j]), invD, IAr[j]);   // ur == Ub[crow] on rows 0..5
-        cs[j] = fmaf_(Ub[j], ud, pA[j]);
-      }
-      if (crow < 6) s.u.fac.U[b][crow] = ur;
-      if (crow == 0) { s.u.fac.invD[b] = invD; s.u.fac.us[b] = u; }
+    for (int j = 0; j < 6; ++j) {
+      const float dl = fmaf_(-(ur * Ub[j]), invD, IAr[j]);   // ur == Ub[crow] on rows 0..5
+      const float c = fmaf_(Ub[j], ud, pA[j]);
+      Dlr[j] = act ? dl : Dlr[j];
+      cs[j] = act ? c : cs[j];
     }
+    if (act && crow < 6) s.u.fac.U[b][crow] = ur;
+    if (act && crow == 0) { s.u.fac.invD[b] = invD; s.u.fac.us[b] = u; }
+  };
+  prefetch(kMaxDepth);
+  const float none[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  constexpr int kTorsoDepth = body_depth[16];
+#pragma unroll 1
+  for (int cd = kMaxDepth; cd > kTorsoDepth; --cd) level(cd, false, none, none);
+  {
+    // the right arm (chain 3, lanes 24..) ends at depth 5; its downdate and bias force join the
+    // torso (chain 2) at depth 4
+    static_assert(body_parent[24] == 16 && body_parent[17] == 16 && body_depth[24] == kTorsoDepth + 1, "torso");
+    float gD[6], gc[6];
+#pragma unroll
+    for (int j = 0; j < 6; ++j) { gD[j] = gshfl(Dlr[j], 24 + rowc); gc[j] = gshfl(cs[j], 24 + rowc); }
+    level(kTorsoDepth, grp == 2, gD, gc);
   }
+#pragma unroll 1
+  for (int cd = kTorsoDepth - 1; cd >= 2; --cd) level(cd, false, none, none);
   // pelvis: I^A_1 = I6_1 + D_14 + D_8 + D_2 and pA_1 = cs_14 + cs_8 + cs_2 (descending children),
   // row r on lane r of chain 0; lane 1 keeps pA_1 for the base solve
   float pAs[6];
