@@ -166,9 +166,10 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
 
 // ---- probes: the same world_qacc device code on caller-given states (parity harnesses)
 struct ProbeArgs {
-  int n, mode;            // mode 0: qacc only; 1: one env substep (PD from targets, guard, integrate)
-  float* qp; float* qv;   // [n][36], [n][35]; updated in place by mode 1
-  const float* tau;       // mode 0: [n][35] generalized force on the hinge dofs (base entries ignored)
+  int n, mode;            // mode 0: qacc only; 1: env substeps (PD from targets, integrate);
+                          // 2: substeps driven by tau (integrate)
+  float* qp; float* qv;   // [n][36], [n][35]; updated in place by modes 1 and 2
+  const float* tau;       // modes 0, 2: [n][35] generalized force on the hinge dofs (base entries ignored)
   const float* target;    // mode 1: [n][29] PD joint targets
   float* qacc; int* ncon; // [n][35], [n]
   int pgs, damped, contact, guard, nsub;
@@ -199,7 +200,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_probe(ProbeArgs a) {
   for (int sub = 0; sub < a.nsub; ++sub) {
     float jtau = 0.f;
     if (L.hinge) {
-      if (a.mode == 0) jtau = a.tau[(long)wc * kNV + L.b + 4];
+      if (a.mode != 1) jtau = a.tau[(long)wc * kNV + L.b + 4];
       else {
         const float tg = a.target[(long)wc * kAct + L.b - 2];
         float pdt = fmaf_(-L.kd, st.jqd, L.kp * (tg - st.jq));
@@ -209,7 +210,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_probe(ProbeArgs a) {
       }
     }
     nc = world_qacc(l, s, st, jtau, P, bqacc, jqacc);
-    if (a.mode == 1) integrate_lane(L, st, bqacc, jqacc, a.guard != 0);
+    if (a.mode != 0) integrate_lane(L, st, bqacc, jqacc, a.guard != 0);
   }
   if (!wvalid) return;
   float* oa = a.qacc + (long)w * kNV;
@@ -219,7 +220,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_probe(ProbeArgs a) {
     a.ncon[w] = nc;
   }
   if (L.hinge) oa[L.b + 4] = jqacc;
-  if (a.mode == 1) {
+  if (a.mode != 0) {
     float* oq = a.qp + (long)w * kNQ;
     float* ov = a.qv + (long)w * kNV;
     if (l == 1) {
@@ -755,6 +756,16 @@ void g1_probe_substep(int n, float* qpos, float* qvel, const float* target, int 
   ProbeArgs a{};
   a.n = n; a.mode = 1; a.qp = qpos; a.qv = qvel; a.target = target; a.qacc = qacc; a.ncon = ncon;
   a.pgs = pgs; a.damped = 1; a.contact = 1; a.guard = 1; a.nsub = nsub; a.mu = mu;
+  hipLaunchKernelGGL(k_probe, dim3((n + 1) / 2), dim3(kPhysThreads), 0, 0, a);
+  HIPCHECK(hipGetLastError());
+}
+
+void g1_dynamics_bench(int n, float* qpos, float* qvel, const float* tau, int nsub, int contact, int damped, int guard,
+                       int pgs, float mu, float* qacc, int* ncon) {
+  if (n <= 0 || nsub <= 0) return;
+  ProbeArgs a{};
+  a.n = n; a.mode = 2; a.qp = qpos; a.qv = qvel; a.tau = tau; a.qacc = qacc; a.ncon = ncon;
+  a.pgs = pgs; a.damped = damped; a.contact = contact; a.guard = guard; a.nsub = nsub; a.mu = mu;
   hipLaunchKernelGGL(k_probe, dim3((n + 1) / 2), dim3(kPhysThreads), 0, 0, a);
   HIPCHECK(hipGetLastError());
 }

@@ -102,6 +102,17 @@ void g1_probe_substep(int n, float* qpos, float* qvel, const float* target, int 
 int g1_probe_policy(int n, int nlayers, const int* hidden, int activation, const float* W, const float* obs_norm,
                     float* mu_out, float* v_out);
 
+/* nsub semi-implicit Euler substeps of n worlds (DEVICE qpos [n][36], qvel [n][35], updated in
+ * place) driven by a generalized force on the hinge dofs (DEVICE tau [n][35], base entries
+ * ignored); contact on/off, damped (M + dt kd) or plain factor, the env's velocity guard (NaN -> 0,
+ * clamp +-50) on/off, pgs sweeps, friction mu. qacc [n][35] and ncon [n] (DEVICE) receive the last
+ * substep's values. Asynchronous
+ * on the null stream. Additive (no reference symbol): the batched smooth-dynamics benchmark (no
+ * contact, plain factor, tau held over substeps; reference standalone bench src/sim_aba.cu:19-58)
+ * and the contact-solve benchmark on fixed contact states run on it. */
+void g1_dynamics_bench(int n, float* qpos, float* qvel, const float* tau, int nsub, int contact, int damped, int guard,
+                       int pgs, float mu, float* qacc, int* ncon);
+
 /* The physics kernel's reciprocal and quotient helpers on n DEVICE operand pairs: rcp[i] = 1/b[i],
  * quot[i] = a[i]/b[i] (both correctly rounded for positive normal b). */
 void g1_probe_divide(int n, const float* a, const float* b, float* rcp, float* quot);

@@ -952,6 +952,40 @@ static void qacc_batch(int n, const R* qpos, const R* qvel, const R* tau, const 
     if (ncon) ncon[w] = nc;
   }
 }
+// nsub substeps for a batch driven by a generalized force tau on the hinge dofs (FK -> env_qacc ->
+// v += dt qacc, optionally with the env's NaN/clamp guard -> integrate), damped or plain factor,
+// contact on or off: the
+// counterpart of the library's dynamics benchmark (smooth dynamics: reference src/sim_aba.cu:19-38).
+template <class R>
+static void dyn_batch(int n, R* qpos, R* qvel, const R* tau, int nsub, int contact, int damped, int guard, int pgs,
+                      R mu, R* qacc_out, int* ncon, int nthreads) {
+#pragma omp parallel for num_threads(nthreads) schedule(dynamic, 16)
+  for (int w = 0; w < n; ++w) {
+    R* lp = qpos + (long)w * kNQ; R* lv = qvel + (long)w * kNV;
+    const R* tw = tau + (long)w * kNV;
+    Frames<R> F; R S[kNV * 6], t[kNV], qacc[kNV], Bdt[kNV];
+    const R dt = M<R>::dt;
+    for (int i = 0; i < kNV; ++i) { Bdt[i] = 0; t[i] = i < 6 ? R(0) : tw[i]; }
+    for (int i = 0; i < kAct; ++i) Bdt[act_dof[i]] = dt * M<R>::act_kd[i];
+    int nc = 0;
+    for (int s = 0; s < nsub; ++s) {
+      fk(lp, F.xpos, F.xquat, F.xipos);
+      nc = env_qacc(lp, lv, F, t, damped ? Bdt : nullptr, S, qacc, pgs, mu, (ContactDebug<R>*)nullptr, contact != 0);
+      for (int i = 0; i < kNV; ++i) {
+        R v = fma_(dt, qacc[i], lv[i]);
+        if (guard) {   // (reference: src/g1_env.cu:154-160)
+          if (!std::isfinite(v)) v = 0;
+          if (v > R(50)) v = R(50); else if (v < R(-50)) v = R(-50);
+        }
+        lv[i] = v;
+      }
+      integrate_pos(lp, lv, dt);
+    }
+    if (ncon) ncon[w] = nc;
+    if (qacc_out) for (int i = 0; i < kNV; ++i) qacc_out[(long)w * kNV + i] = qacc[i];
+  }
+}
+
 // One substep for a batch (FK -> PD torque with clamp -> env_qacc -> Euler with NaN/clamp ->
 // integrate), the teacher-forced unit of the per-substep parity gate (reference:
 // src/g1_env.cu:141-163). target[n][29] are PD joint targets.
@@ -1064,6 +1098,14 @@ void orc_qacc_f(int n, const float* q, const float* v, const float* tau, const f
 void orc_qacc_d(int n, const double* q, const double* v, const double* tau, const double* Bdt, int pgs, double mu,
                 double* qacc, int* ncon, int nthreads, int contact) {
   qacc_batch(n, q, v, tau, Bdt, pgs, mu, qacc, ncon, nthreads, contact);
+}
+void orc_dyn_f(int n, float* q, float* v, const float* tau, int nsub, int contact, int damped, int guard, int pgs,
+               float mu, float* qacc, int* ncon, int nthreads) {
+  dyn_batch(n, q, v, tau, nsub, contact, damped, guard, pgs, mu, qacc, ncon, nthreads);
+}
+void orc_dyn_d(int n, double* q, double* v, const double* tau, int nsub, int contact, int damped, int guard, int pgs,
+               double mu, double* qacc, int* ncon, int nthreads) {
+  dyn_batch(n, q, v, tau, nsub, contact, damped, guard, pgs, mu, qacc, ncon, nthreads);
 }
 void orc_substep_f(int n, float* q, float* v, const float* target, int pgs, float mu, float* qacc, int* ncon,
                    int nthreads) { substep_batch(n, q, v, target, pgs, mu, qacc, ncon, nthreads); }

@@ -38,6 +38,8 @@ def _load():
                                                     _c.c_void_p, _c.c_int, _c.c_int]
         getattr(lib, f"orc_substep_{suf}").argtypes = [_c.c_int, fp, fp, fp, _c.c_int, real, _c.c_void_p,
                                                        _c.c_void_p, _c.c_int]
+        getattr(lib, f"orc_dyn_{suf}").argtypes = [_c.c_int, fp, fp, fp] + [_c.c_int] * 5 + [real, _c.c_void_p,
+                                                    _c.c_void_p, _c.c_int]
         getattr(lib, f"orc_pgs_{suf}").argtypes = [_c.c_int, fp, fp, fp, _c.c_int]
         getattr(lib, f"orc_impedance_{suf}").argtypes = [real]
         getattr(lib, f"orc_impedance_{suf}").restype = real
@@ -133,6 +135,18 @@ def substep(qpos, qvel, target, pgs=8, mu=MU_MODEL, dtype=np.float32, threads=1)
     n = q.shape[0]
     qa = np.zeros((n, NV), dtype); nc = np.zeros(n, np.int32)
     getattr(lib(), f"orc_substep_{_dt(dtype)}")(n, q, v, tg, pgs, mu, qa.ctypes.data, nc.ctypes.data, threads)
+    return q, v, qa, nc
+
+
+def dynamics(qpos, qvel, tau, nsub=1, contact=False, damped=False, guard=False, pgs=8, mu=MU_MODEL, dtype=np.float32,
+             threads=1):
+    """nsub tau-driven substeps on copies; returns (qpos', qvel', qacc of the last substep, ncon)."""
+    q = _arr(np.atleast_2d(qpos), dtype).copy(); v = _arr(np.atleast_2d(qvel), dtype).copy()
+    t = _arr(np.atleast_2d(tau), dtype)
+    n = q.shape[0]
+    qa = np.zeros((n, NV), dtype); nc = np.zeros(n, np.int32)
+    getattr(lib(), f"orc_dyn_{_dt(dtype)}")(n, q, v, t, nsub, int(contact), int(damped), int(guard), pgs, mu, qa.ctypes.data,
+                                            nc.ctypes.data, threads)
     return q, v, qa, nc
 
 

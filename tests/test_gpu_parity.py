@@ -97,6 +97,36 @@ def test_smooth_qacc_config0(g1, orc):
     assert r64.max() <= 1e-4
 
 
+def test_config1_dynamics_teacher_forced_and_drift(g1, orc):
+    """Config 1 (no contact, plain factor, tau held, semi-implicit Euler) through g1_dynamics_bench:
+    one substep from the oracle's own state is bit-identical in qpos, qvel and qacc; a 100-substep
+    free run (tau held, 0.2 s) stays within fp32 drift of the oracle's free run. Full-range random
+    torques on the unconstrained floating robot make explicit Euler diverge within ~50 substeps
+    (fp32 and fp64 alike), so the runs use the env's velocity guard (NaN -> 0, clamp +-50)."""
+    import torch
+    import configs
+    qp, qv, tau = configs.config0(seed=7, n=512)
+    qp, qv, tau = (x.astype(np.float32) for x in (qp, qv, tau))
+
+    def gpu(nsub):
+        dq, dv, dt_ = _dev(qp), _dev(qv), _dev(tau)
+        qa = torch.zeros(qp.shape[0], 35, device="cuda")
+        nc = torch.zeros(qp.shape[0], dtype=torch.int32, device="cuda")
+        g1._lib.g1_dynamics_bench(qp.shape[0], g1._dp(dq), g1._dp(dv), g1._dp(dt_), nsub, 0, 0, 1, 8, 0.6,
+                                  g1._dp(qa), g1._dp(nc))
+        torch.cuda.synchronize()
+        return dq.cpu().numpy(), dv.cpu().numpy(), qa.cpu().numpy()
+
+    gq, gv, ga = gpu(1)
+    oq, ov, oa, _ = orc.dynamics(qp, qv, tau, nsub=1, guard=True, threads=8)
+    assert np.array_equal(ga, oa) and np.array_equal(gv, ov) and np.array_equal(gq, oq)
+    gq, gv, ga = gpu(100)
+    oq, ov, oa, _ = orc.dynamics(qp, qv, tau, nsub=100, guard=True, threads=8)
+    dq_, dv_ = relerr_rows(gq, oq), relerr_rows(gv, ov)
+    print(f"config1: 1 substep bit-identical; 100-substep free-run drift qpos {dq_.max():.2e}, qvel {dv_.max():.2e}")
+    assert np.isfinite(gq).all() and dq_.max() <= 1e-4
+
+
 def test_smooth_qacc_vs_mujoco(g1, ref_traj):
     sel = ref_traj["sel"]
     prev = np.maximum(sel - 1, 0)
