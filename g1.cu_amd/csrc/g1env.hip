@@ -280,15 +280,23 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
     __syncthreads();
     float* t = in; in = out; out = t;
   }
-  // ---- fused head [mu(29) | v | pad]
-  mfma_layer(in, kLdx, out, kLdx, a.pp.Wp + a.pp.woff[a.shape.nl], a.pp.Wp + a.pp.boff[a.shape.nl],
-             a.pp.K[a.shape.nl], 32, 0, false);
+  // ---- fused head [mu(29) | v | pad]: its K range is split over the 4 waves when the free buffer
+  // holds the 4 partial tiles; the summed head then overwrites the (consumed) input tile
+  float* head = out;
+  if (kTileWorlds * kLdx >= 4 * 32 * 32) {
+    mfma_head_splitk(in, kLdx, in, kLdx, out, a.pp.Wp + a.pp.woff[a.shape.nl], a.pp.Wp + a.pp.boff[a.shape.nl],
+                     a.pp.K[a.shape.nl]);
+    head = in;
+  } else {
+    mfma_layer(in, kLdx, out, kLdx, a.pp.Wp + a.pp.woff[a.shape.nl], a.pp.Wp + a.pp.boff[a.shape.nl],
+               a.pp.K[a.shape.nl], 32, 0, false);
+  }
   __syncthreads();
   // ---- sampling + log-prob, one thread per world, actions in order (reference: src/g1_env.cu:308-318)
   if (tid < kTileWorlds) {
     const int w = w0 + tid;
     if (w < a.N) {
-      const float* h = out + tid * kLdx;
+      const float* h = head + tid * kLdx;
       const float val = h[kAct];
       if (a.mu_out) {
         for (int i = 0; i < kAct; ++i) a.mu_out[(long)w * kAct + i] = h[i];

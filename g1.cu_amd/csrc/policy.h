@@ -110,18 +110,73 @@ __device__ __forceinline__ void mfma_layer(const float* __restrict__ in, int ldi
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = bv;
     const float* wcol = Wp + (long)(n0 + mrow) * 2 + khalf;
-#pragma unroll 4
-    for (int kk = 0; kk < K / 2; ++kk) {
-      const float a = in[mrow * ldi + 2 * kk + khalf];
-      const float b = wcol[(long)kk * Np * 2];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+    const float* arow = in + mrow * ldi + khalf;
+    // k-pairs in batches of kB: all kB weight loads (L2 latency) are in flight before the first
+    // MFMA of the batch waits on them
+    constexpr int kB = 16;
+    const int K2 = K / 2;
+    int kk = 0;
+    for (; kk + kB <= K2; kk += kB) {
+      float a[kB], b[kB];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        b[u] = wcol[(long)(kk + u) * Np * 2];
+        a[u] = arow[2 * (kk + u)];
+      }
+#pragma unroll
+      for (int u = 0; u < kB; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u], b[u], acc, 0, 0, 0);
     }
+    for (; kk < K2; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(arow[2 * kk], wcol[(long)kk * Np * 2], acc, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int m = (i & 3) + 4 * khalf + 8 * (i >> 2);
       const float v = acc[i];
       out[m * ldo + n0 + mrow] = apply_act ? act_fn(v, act) : v;
     }
+  }
+}
+
+// The fused 32-wide head has a single output tile: its K range is split over the 4 waves and the
+// partial tiles are summed through LDS (scratch: 4 x 32 x 32 floats, not aliasing `in`; `out` may
+// alias `in`: every wave has finished reading `in` at the barrier before the sum is written).
+__device__ __forceinline__ void mfma_head_splitk(const float* in, int ldi, float* out, int ldo,
+                                                 float* __restrict__ scratch, const float* __restrict__ Wp,
+                                                 const float* __restrict__ bias, int K) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int mrow = lane & 31, khalf = lane >> 5;
+  constexpr int Np = 32;
+  const int K2 = K / 2;
+  const int q = (K2 + 3) / 4;
+  const int k0 = wv * q, k1 = min(K2, k0 + q);
+  f32x16 acc;
+  const float bv = wv == 0 ? bias[mrow] : 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = bv;
+  const float* wcol = Wp + (long)mrow * 2 + khalf;
+  const float* arow = in + mrow * ldi + khalf;
+  constexpr int kB = 16;
+  int kk = k0;
+  for (; kk + kB <= k1; kk += kB) {
+    float a[kB], b[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      b[u] = wcol[(long)(kk + u) * Np * 2];
+      a[u] = arow[2 * (kk + u)];
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u], b[u], acc, 0, 0, 0);
+  }
+  for (; kk < k1; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(arow[2 * kk], wcol[(long)kk * Np * 2], acc, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = (i & 3) + 4 * khalf + 8 * (i >> 2);
+    scratch[(wv * 32 + m) * 32 + mrow] = acc[i];
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 32 * 32; idx += 256) {
+    const int m = idx >> 5, n = idx & 31;
+    out[m * ldo + n] = ((scratch[m * 32 + n] + scratch[(32 + m) * 32 + n]) + scratch[(64 + m) * 32 + n]) +
+                       scratch[(96 + m) * 32 + n];
   }
 }
 
