@@ -732,24 +732,23 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       if (d < 18) return (basis && right) ? eb[17 - d] : 0.f;
       return 0.f;
     };
+    // leaf -> root. The basis right-hand sides live on the base and leg dofs (the feet hang off
+    // bodies 7 and 13, legs 2..13), so the waist/arm subtree (bodies 14..30) carries zero
+    // articulated bias: u = 0 - S.0 = +0 and its contribution to the pelvis is +0; skipping it
+    // changes no bit. The two legs are independent chains and are walked interleaved (right leg
+    // 13..8 with left leg 7..2) so their dependency chains overlap; the pelvis then adds the
+    // right leg's root (8) before the left leg's (2), the reference's descending order.
+    static_assert(foot_body[0] < 14 && foot_body[kNFoot - 1] < 14 && body_parent[14] == 1, "leg layout");
+    static_assert(body_parent[2] == 1 && body_parent[8] == 1 && body_nchild[7] == 0 && body_nchild[13] == 0, "legs");
     float u[kNBody];
-    float car[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float p16[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float p1[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int b = kNBody - 1; b >= 2; --b) {
-      const int par = body_parent[b], d = b + 4;
-      // The basis right-hand sides live on the base and leg dofs (the feet hang off bodies 7 and
-      // 13, legs 2..13), so the waist/arm subtree (bodies 14..30) carries zero articulated bias:
-      // u = 0 - S.0 = +0 and its contribution to the pelvis is +0. Skipping it changes no bit.
-      static_assert(foot_body[0] < 14 && foot_body[kNFoot - 1] < 14 && body_parent[14] == 1, "leg layout");
-      if (b >= 14) {
-        u[b] = 0.f;
-        continue;
-      }
+    for (int b = 14; b < kNBody; ++b) u[b] = 0.f;
+    float carR[6], carL[6], c8[6], c2[6];
+    auto up = [&](int b, float (&car)[6], float (&croot)[6]) {
+      const int d = b + 4;
       float pb[6];
 #pragma unroll
-      for (int k = 0; k < 6; ++k) pb[k] = (b == 16) ? p16[k] : (body_nchild[b] == 0 ? 0.f : car[k]);
+      for (int k = 0; k < 6; ++k) pb[k] = body_nchild[b] == 0 ? 0.f : car[k];
       const float* Sd = s.u.fac.S[d];
       const float* Ub = s.u.fac.U[b];
       const float ub = xrhs(d) - dot6(Sd, pb);
@@ -758,15 +757,20 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
       for (int k = 0; k < 6; ++k) {
         const float c = fmaf_(Ub[k], ud, pb[k]);
-        if (par == 16) p16[k] += c;
-        else if (par == 1) p1[k] += c;
+        if (body_parent[b] == 1) croot[k] = c;
         else car[k] = 0.f + c;
       }
-      if (par == 16) G1_PIN6(p16);
-      else if (par == 1) G1_PIN6(p1);
-      else G1_PIN6(car);
+      G1_PIN6(car);
       __asm__ volatile("" : "+v"(u[b]));
+    };
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      up(13 - i, carR, c8);
+      up(7 - i, carL, c2);
     }
+    float p1[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) p1[k] = (0.f + c8[k]) + c2[k];
     // free joint: D qdd = x_base - S_base.pA_1 with D = L L'
     float qdd[6];
     {
@@ -791,37 +795,58 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
     float* ycol = s.Mm[(j >= 1 && j < kCols) ? j : kCols - 1];
     const bool wr = j >= 1 && j < kCols;
-    float a1[6], a16[6], ac[6];
+    float a1[6];
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
       float a = 0.f;
 #pragma unroll
       for (int k = 0; k < 6; ++k) a = fmaf_(s.u.fac.S[k][i], qdd[k], a);
       a1[i] = 0.f + a;
-      a16[i] = 0.f;
-      ac[i] = 0.f;
     }
     if (wr) {
 #pragma unroll
       for (int k = 0; k < 6; ++k) ycol[k] = qdd[k];
     }
     G1_PIN6(a1);
-#pragma unroll
-    for (int b = 2; b < kNBody; ++b) {
-      const int par = body_parent[b], d = b + 4;
-      float ap[6];
-#pragma unroll
-      for (int k = 0; k < 6; ++k) ap[k] = (par == 1) ? a1[k] : (par == 16 ? a16[k] : ac[k]);
+    // root -> leaf over five independent chains, walked interleaved: legs and waist from the
+    // pelvis (2.., 8.., 14..16), then both arms from the torso (17.., 24..)
+    static_assert(body_parent[14] == 1 && body_parent[17] == 16 && body_parent[24] == 16, "chains");
+    auto down = [&](int b, const float (&ap)[6], float (&ac)[6]) {
+      const int d = b + 4;
       const float* Ub = s.u.fac.U[b];
       const float* Sd = s.u.fac.S[d];
       const float q = (u[b] - dot6(Ub, ap)) * s.u.fac.invD[b];
       if (wr) ycol[d] = q;
 #pragma unroll
-      for (int k = 0; k < 6; ++k) {
-        ac[k] = fmaf_(Sd[k], q, ap[k]);
-        if (b == 16) a16[k] = ac[k];
-      }
+      for (int k = 0; k < 6; ++k) ac[k] = fmaf_(Sd[k], q, ap[k]);
       G1_PIN6(ac);
+    };
+    float aL[6], aR[6], aW[6], tmp[6];
+    down(2, a1, aL); down(8, a1, aR); down(14, a1, aW);
+#pragma unroll
+    for (int i = 1; i < 6; ++i) {
+#pragma unroll
+      for (int k = 0; k < 6; ++k) tmp[k] = aL[k];
+      down(2 + i, tmp, aL);
+#pragma unroll
+      for (int k = 0; k < 6; ++k) tmp[k] = aR[k];
+      down(8 + i, tmp, aR);
+      if (i < 3) {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) tmp[k] = aW[k];
+        down(14 + i, tmp, aW);
+      }
+    }
+    float aLA[6], aRA[6];
+    down(17, aW, aLA); down(24, aW, aRA);   // aW is the torso (16) now
+#pragma unroll
+    for (int i = 1; i < 7; ++i) {
+#pragma unroll
+      for (int k = 0; k < 6; ++k) tmp[k] = aLA[k];
+      down(17 + i, tmp, aLA);
+#pragma unroll
+      for (int k = 0; k < 6; ++k) tmp[k] = aRA[k];
+      down(24 + i, tmp, aRA);
     }
   }
   __syncthreads();
