@@ -62,6 +62,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=3, choices=[3, 4])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--policy", choices=["random", "trained"], default="random",
+                    help="random-init weights (the configuration's definition) or the reference's trained "
+                         "checkpoint (g1.cu_amd/data/trained_policy_finish_best.npz: walking contact mix)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the rollout shards worlds across GPUs with no exchange, "
@@ -77,8 +80,15 @@ def main():
     env = ppo.G1Env(N, substeps=S, pgs_iters=pgs, seed=1)
     env.set_policy(cfg["hidden"], cfg["act"])
     env.reset()
-    W = torch.from_numpy(configs.policy_init(rng, hidden=cfg["hidden"])).cuda()
-    mean = torch.zeros(100, device="cuda"); var = torch.ones(100, device="cuda")
+    if args.policy == "trained":
+        if args.config != 3:
+            sys.exit("the trained checkpoint has the config-3 policy shape (100-256-256 tanh)")
+        tp = np.load(os.path.join(ROOT, "g1.cu_amd", "data", "trained_policy_finish_best.npz"))
+        W = torch.from_numpy(tp["W"]).cuda()
+        mean = torch.from_numpy(tp["obs_mean"]).cuda(); var = torch.from_numpy(tp["obs_var"]).cuda()
+    else:
+        W = torch.from_numpy(configs.policy_init(rng, hidden=cfg["hidden"])).cuda()
+        mean = torch.zeros(100, device="cuda"); var = torch.ones(100, device="cuda")
     O = torch.zeros(H, N, 100, device="cuda"); A = torch.zeros(H, N, 29, device="cuda")
     LP, V, R, D = (torch.zeros(H, N, device="cuda") for _ in range(4))
     Vlast = torch.zeros(N, device="cuda")
@@ -127,8 +137,12 @@ def main():
         "scaling": "weak",
         "vs_baseline": substeps_per_s / RTX3090_SUBSTEPS_PER_S if args.config == 3 else None,
         "dtype": "fp32",
-        "data": "synthetic (stand-pose resets, random-init policy N(0,1/fan_in), library Philox noise)",
-        "config": {"workload": f"config{args.config}: fused rollout N={N} H={H} S={S} pgs={pgs} "
+        "data": ("synthetic (stand-pose resets, random-init policy N(0,1/fan_in), library Philox noise)"
+                 if args.policy == "random" else
+                 "stand-pose resets, the reference's trained policy (models/ppo_ckpt/finish_best.pt, converted) "
+                 "with its frozen obs statistics, library Philox noise"),
+        "config": {"workload": f"config{args.config}{' (trained policy)' if args.policy == 'trained' else ''}: "
+                               f"fused rollout N={N} H={H} S={S} pgs={pgs} "
                                f"policy 100-{'-'.join(map(str, cfg['hidden']))} {'tanh' if cfg['act'] == 0 else 'ELU'}",
                    "N": N, "H": H, "substeps": S, "pgs": pgs, "ms_per_rollout": ms_rollout},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -228,3 +228,27 @@ def test_reciprocal_and_quotient_are_ieee(g1):
     with np.errstate(all="ignore"):
         assert np.array_equal(r.view(np.uint32), (np.float32(1) / bs).view(np.uint32))
         assert np.array_equal(q.view(np.uint32), (a / bs).view(np.uint32))
+
+
+def test_policy_mlp_trained_checkpoint(g1, orc):
+    """The reference's trained policy (converted checkpoint) through the MFMA policy kernel vs the
+    oracle's fp32 MLP on normalised observations of perturbed stand states."""
+    import os
+    import torch
+    from conftest import ROOT
+    tp = np.load(os.path.join(ROOT, "g1.cu_amd", "data", "trained_policy_finish_best.npz"))
+    W = tp["W"]
+    rng = np.random.default_rng(9)
+    n = 1000
+    x = np.clip(rng.normal(0, 1.0, (n, 100)), -10, 10).astype(np.float32)
+    mu_ref, _, v_ref = orc.mlp(W, x, hidden=(256, 256), act=0)
+    mu = torch.zeros(n, 29, device="cuda"); v = torch.zeros(n, device="cuda")
+    h = np.asarray((256, 256), np.int32)
+    dW, dx = _dev(W), _dev(x)
+    rc = g1._lib.g1_probe_policy(n, 2, h.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), 0, g1._dp(dW), g1._dp(dx),
+                                 g1._dp(mu), g1._dp(v))
+    assert rc == 0
+    rm = relerr_rows(mu.cpu().numpy(), mu_ref)
+    rv = np.linalg.norm(v.cpu().numpy() - v_ref) / np.linalg.norm(v_ref)
+    print(f"trained mlp: mu worst relerr {rm.max():.3e}, v batch relerr {rv:.3e}")
+    assert rm.max() <= 1e-5 and rv <= 1e-5
