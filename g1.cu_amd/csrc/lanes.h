@@ -43,7 +43,9 @@ __device__ __forceinline__ float gsum(float v) {
 // length depends on per-world data
 __device__ __forceinline__ int wave_max(int v) {
   int o = __shfl_xor(v, 32, 64);
-  return v > o ? v : o;
+  // wave-uniform by construction: hand it to the scalar unit so the loops and branches it bounds
+  // compile to scalar compares instead of exec-mask regions
+  return __builtin_amdgcn_readfirstlane(v > o ? v : o);
 }
 
 // Value of lane I of this lane's aligned 8-lane chain (ds_swizzle bit mode within 32 lanes:

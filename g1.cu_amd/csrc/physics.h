@@ -911,25 +911,28 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   auto dcoef = [](int k, int a) -> float {
     return a == 0 ? 1.f : (a == 1 ? (k == 0 ? 1.f : (k == 1 ? -1.f : 0.f)) : (k == 2 ? 1.f : (k == 3 ? -1.f : 0.f)));
   };
+  // Entries are formed by every lane (branch-free; the G block and R indices stay inside their
+  // arrays for every lane) and kept where (row, column) is a constraint pair; the row loop stops at
+  // the wave's largest row count.
   float Acol[kMaxEfc];
 #pragma unroll
+  for (int ii = 0; ii < kMaxEfc; ++ii) Acol[ii] = 0.f;
+#pragma unroll
   for (int ii = 0; ii < kMaxEfc; ++ii) {
+    if (ii >= nefc_max) break;
     const int c2 = ii >> 2, k2 = ii & 3;
-    float val = 0.f;
-    if (row && ii < nefc) {
-      int lo, hi, klo, khi;
-      if (c2 < ci) { lo = c2; hi = ci; klo = k2; khi = ki; }
-      else if (c2 > ci) { lo = ci; hi = c2; klo = ki; khi = k2; }
-      else { lo = ci; hi = ci; klo = ki > k2 ? ki : k2; khi = ki > k2 ? k2 : ki; }
-      const float* G = s.u.G[hi * (hi + 1) / 2 + lo];
-      const float d0 = dcoef(klo, 0), d1 = dcoef(klo, 1), d2 = dcoef(klo, 2);
-      const float t0 = fmaf_(d2, G[6], fmaf_(d1, G[3], d0 * G[0]));
-      const float t1 = fmaf_(d2, G[7], fmaf_(d1, G[4], d0 * G[1]));
-      const float t2 = fmaf_(d2, G[8], fmaf_(d1, G[5], d0 * G[2]));
-      val = fmaf_(t2, dcoef(khi, 2), fmaf_(t1, dcoef(khi, 1), t0 * dcoef(khi, 0)));
-      if (ii == l) val += s.Rc[ci];
-    }
-    Acol[ii] = val;
+    int lo, hi, klo, khi;
+    if (c2 < ci) { lo = c2; hi = ci; klo = k2; khi = ki; }
+    else if (c2 > ci) { lo = ci; hi = c2; klo = ki; khi = k2; }
+    else { lo = ci; hi = ci; klo = ki > k2 ? ki : k2; khi = ki > k2 ? k2 : ki; }
+    const float* G = s.u.G[hi * (hi + 1) / 2 + lo];
+    const float d0 = dcoef(klo, 0), d1 = dcoef(klo, 1), d2 = dcoef(klo, 2);
+    const float t0 = fmaf_(d2, G[6], fmaf_(d1, G[3], d0 * G[0]));
+    const float t1 = fmaf_(d2, G[7], fmaf_(d1, G[4], d0 * G[1]));
+    const float t2 = fmaf_(d2, G[8], fmaf_(d1, G[5], d0 * G[2]));
+    float val = fmaf_(t2, dcoef(khi, 2), fmaf_(t1, dcoef(khi, 1), t0 * dcoef(khi, 0)));
+    val = (ii == l) ? val + s.Rc[ci] : val;
+    Acol[ii] = (row && ii < nefc) ? val : 0.f;
   }
   const float bi = row ? s.bvec[l] : 0.f;
   float Aii = 1.f;
@@ -948,15 +951,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   for (int it = 0; it < P.pgs; ++it) {
 #pragma unroll
     for (int ii = 0; ii < kMaxEfc; ++ii) {
-      if (ii < nefc_max) {
-        const float sum = gsum(Acol[ii] * fi);   // sum_j A[ii][j] f_j (lane j holds column j)
-        const float ri = fmaf_(-Aii, fi, bi + sum);
-        const float x = -ri;
-        const float q0 = x * yi;
-        const float fn = __builtin_fmaf(__builtin_fmaf(-q0, Aii, x), yi, q0);
-        const float fnew = fn > 0.f ? fn : 0.f;
-        fi = (row && l == ii) ? fnew : fi;
-      }
+      if (ii >= nefc_max) break;
+      const float sum = gsum(Acol[ii] * fi);   // sum_j A[ii][j] f_j (lane j holds column j)
+      const float ri = fmaf_(-Aii, fi, bi + sum);
+      const float x = -ri;
+      const float q0 = x * yi;
+      const float fn = __builtin_fmaf(__builtin_fmaf(-q0, Aii, x), yi, q0);
+      const float fnew = fn > 0.f ? fn : 0.f;
+      fi = (row && l == ii) ? fnew : fi;
     }
   }
   if (row) s.f[l] = fi;
