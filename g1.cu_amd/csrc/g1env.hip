@@ -42,6 +42,7 @@ struct PhysArgs {
   const float* act; int t0, astep; // actions [*, N, 29]; row t = t0 + k * astep
   const float* reset_noise;        // [*, N, 29] injected U(-1,1) or null (Philox)
   float* R; float* D; int rstep;   // outputs [*, N], row t0 + k * rstep
+  float* obs;                      // [N][100] observation after the last control step, or null
   unsigned long long seed;
   unsigned long long* ncon_hist;   // [9] or null
 };
@@ -161,6 +162,20 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
       a.pa[(long)w * kAct + ai] = pa;
     }
     if (a.ncon_hist && l < 9 && hcnt) atomicAdd(&a.ncon_hist[l], (unsigned long long)hcnt);
+    if (a.obs) {
+      // observation of the final state, each lane writing its own entries (same values as k_obs)
+      float* o = a.obs + (long)w * kObs;
+      if (l == 1) {
+#pragma unroll
+        for (int q = 0; q < 6; ++q) o[q] = st.bqd[q];
+        const float qw = st.bq[3], qx = st.bq[4], qy = st.bq[5], qz = st.bq[6];
+        o[6] = -(2.f * fmaf_(-qw, qy, qx * qz));
+        o[7] = -(2.f * fmaf_(qw, qx, qy * qz));
+        o[8] = -fmaf_(-2.f, fmaf_(qy, qy, qx * qx), 1.f);
+      }
+      if (L.hinge) { o[9 + ai] = st.jq; o[38 + ai] = st.jqd; o[67 + ai] = pa; }
+      if (l == 0) { o[96] = 0.8f; o[97] = 0.f; o[98] = 0.f; o[99] = 0.f; }
+    }
   }
 }
 
@@ -413,7 +428,9 @@ struct EnvState {
   float *qp, *qv, *pa;
   int* steps;
   unsigned* rng;
-  float *dact, *dobs, *drew, *ddone, *zero_act, *bench_r, *bench_d;
+  float *dact, *zero_act, *bench_r, *bench_d;
+  float* dout;            // host-step outputs on the device: [obs N x 100 | reward N | done N]
+  float *h_act, *h_out;   // pinned host staging of the host-step path (actions in, outputs out)
   float* Wp;
   long Wp_cap;
   unsigned long long* ncon_hist;
@@ -564,13 +581,13 @@ void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
   HIPCHECK(hipMalloc(&E->steps, (size_t)N * 4));
   HIPCHECK(hipMalloc(&E->rng, (size_t)N * 4));
   HIPCHECK(hipMalloc(&E->dact, (size_t)N * kAct * 4));
-  HIPCHECK(hipMalloc(&E->dobs, (size_t)N * kObs * 4));
-  HIPCHECK(hipMalloc(&E->drew, (size_t)N * 4));
-  HIPCHECK(hipMalloc(&E->ddone, (size_t)N * 4));
   HIPCHECK(hipMalloc(&E->zero_act, (size_t)N * kAct * 4));
   HIPCHECK(hipMalloc(&E->bench_r, (size_t)N * 4));
   HIPCHECK(hipMalloc(&E->bench_d, (size_t)N * 4));
   HIPCHECK(hipMalloc(&E->ncon_hist, 9 * sizeof(unsigned long long)));
+  HIPCHECK(hipMalloc(&E->dout, (size_t)N * (kObs + 2) * 4));
+  HIPCHECK(hipHostMalloc((void**)&E->h_act, (size_t)N * kAct * 4, hipHostMallocDefault));
+  HIPCHECK(hipHostMalloc((void**)&E->h_out, (size_t)N * (kObs + 2) * 4, hipHostMallocDefault));
   HIPCHECK(hipMemset(E->zero_act, 0, (size_t)N * kAct * 4));
   HIPCHECK(hipMemset(E->rng, 0, (size_t)N * 4));
   HIPCHECK(hipMemset(E->ncon_hist, 0, 9 * sizeof(unsigned long long)));
@@ -587,10 +604,12 @@ void g1_env_destroy(void* h) {
   EnvState* E = (EnvState*)h;
   if (!E) return;
   HIPCHECK(hipDeviceSynchronize());
-  void* bufs[] = {E->qp, E->qv, E->pa, E->steps, E->rng, E->dact, E->dobs, E->drew, E->ddone,
-                  E->zero_act, E->bench_r, E->bench_d, E->ncon_hist, E->Wp};
+  void* bufs[] = {E->qp, E->qv, E->pa, E->steps, E->rng, E->dact,
+                  E->zero_act, E->bench_r, E->bench_d, E->ncon_hist, E->Wp, E->dout};
   for (void* b : bufs)
     if (b) HIPCHECK(hipFree(b));
+  if (E->h_act) HIPCHECK(hipHostFree(E->h_act));
+  if (E->h_out) HIPCHECK(hipHostFree(E->h_out));
   for (auto e : E->ev_phys) (void)hipEventDestroy(e);
   for (auto e : E->ev_pol) (void)hipEventDestroy(e);
   delete E;
@@ -603,24 +622,29 @@ void g1_env_reset(void* h, float* obs_out) {
                      (const float*)nullptr, E->seed);
   HIPCHECK(hipGetLastError());
   hipLaunchKernelGGL(k_obs, dim3((unsigned)(((long)N * kObs + 255) / 256)), dim3(256), 0, 0, E->qp, E->qv, E->pa, N,
-                     E->dobs);
+                     E->dout);
   HIPCHECK(hipGetLastError());
-  HIPCHECK(hipMemcpy(obs_out, E->dobs, (size_t)N * kObs * 4, hipMemcpyDeviceToHost));
+  HIPCHECK(hipMemcpyAsync(E->h_out, E->dout, (size_t)N * kObs * 4, hipMemcpyDeviceToHost, 0));
+  HIPCHECK(hipStreamSynchronize(0));
+  std::memcpy(obs_out, E->h_out, (size_t)N * kObs * 4);
 }
 
+// Host-step path (reference: src/g1_env.cu:245-268,431-441): actions staged through pinned memory,
+// one launch that also writes the observation, one device-to-host copy of [obs | reward | done].
 void g1_env_step(void* h, const float* act, float* obs, float* rew, float* done) {
   EnvState* E = (EnvState*)h;
   const int N = E->N;
-  HIPCHECK(hipMemcpy(E->dact, act, (size_t)N * kAct * 4, hipMemcpyHostToDevice));
+  std::memcpy(E->h_act, act, (size_t)N * kAct * 4);
+  HIPCHECK(hipMemcpyAsync(E->dact, E->h_act, (size_t)N * kAct * 4, hipMemcpyHostToDevice, 0));
   PhysArgs pa = phys_args(E);
-  pa.act = E->dact; pa.t0 = 0; pa.astep = 0; pa.rstep = 0; pa.R = E->drew; pa.D = E->ddone;
+  pa.act = E->dact; pa.t0 = 0; pa.astep = 0; pa.rstep = 0;
+  pa.obs = E->dout; pa.R = E->dout + (size_t)N * kObs; pa.D = E->dout + (size_t)N * (kObs + 1);
   launch_physics(pa);
-  hipLaunchKernelGGL(k_obs, dim3((unsigned)(((long)N * kObs + 255) / 256)), dim3(256), 0, 0, E->qp, E->qv, E->pa, N,
-                     E->dobs);
-  HIPCHECK(hipGetLastError());
-  HIPCHECK(hipMemcpy(obs, E->dobs, (size_t)N * kObs * 4, hipMemcpyDeviceToHost));
-  HIPCHECK(hipMemcpy(rew, E->drew, (size_t)N * 4, hipMemcpyDeviceToHost));
-  HIPCHECK(hipMemcpy(done, E->ddone, (size_t)N * 4, hipMemcpyDeviceToHost));
+  HIPCHECK(hipMemcpyAsync(E->h_out, E->dout, (size_t)N * (kObs + 2) * 4, hipMemcpyDeviceToHost, 0));
+  HIPCHECK(hipStreamSynchronize(0));
+  std::memcpy(obs, E->h_out, (size_t)N * kObs * 4);
+  std::memcpy(rew, E->h_out + (size_t)N * kObs, (size_t)N * 4);
+  std::memcpy(done, E->h_out + (size_t)N * (kObs + 1), (size_t)N * 4);
 }
 
 void g1_rollout(void* h, int H, const float* W, const float* mean, const float* var, float* O, float* A, float* LP,

@@ -130,6 +130,22 @@ def main():
             rec[f"cpu_{thr}thr_solves_per_s"] = n / dt2
     out(rec)
 
+    # ---------------- config 3 through the host-step path: H control steps of g1_env_step with host
+    # numpy buffers (the reference's non-fused loop, scripts/ppo.py evaluate / DEVLOG's host-loop rollout)
+    N3, H3 = 8192, 32
+    env = ppo.G1Env(N3, substeps=10, pgs_iters=8, seed=1)
+    env.reset()
+    acts = np.random.default_rng(2).normal(0, 0.5, (H3, N3, 29)).astype(np.float32)
+    for t in range(4):
+        env.step(acts[t])
+    t0 = time.perf_counter()
+    for t in range(H3):
+        env.step(acts[t])
+    dt_h = time.perf_counter() - t0
+    env.close()
+    out(dict(config="3-host-step", N=N3, H=H3, ms_per_rollout=dt_h * 1e3, ms_per_step=dt_h * 1e3 / H3,
+             substeps_per_s=N3 * H3 * 10 / dt_h))
+
     # ---------------- configs 3 and 4: CPU oracle rollout rate (GPU: bench.py)
     if not args.skip_cpu:
         for cfgid in (3, 4):
