@@ -877,15 +877,20 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const int j = l;
     const int cp = (j >= 1) ? (j - 1) / 3 : 0, bcol = (j >= 1) ? (j - 1) % 3 : 0;
     const bool active = (j >= 1) && (cp < ncon);
+    // the lane's solve column on the base and both legs' dofs (0..17), read once for all c
+    float mj[18];
+    const float* mcol = s.Mm[active ? j : 0];
+#pragma unroll
+    for (int a = 0; a < 18; ++a) mj[a] = mcol[a];
 #pragma unroll 1
     for (int c = 0; c < ncon_max; ++c) {
       if (active && c <= cp) {
-        const int legbase = s.con_leg[c] ? 12 : 6;
+        const bool rightleg = s.con_leg[c] != 0;
         float g0 = 0.f, g1 = 0.f, g2 = 0.f;
 #pragma unroll
         for (int k = 0; k < kContactDofs; ++k) {
-          const int a = (k < 6) ? legbase + 5 - k : k - 6;
-          const float mv = s.Mm[j][a];
+          // dof a = legbase + 5 - k on the leg (legbase 6 left, 12 right), k - 6 on the base
+          const float mv = (k < 6) ? (rightleg ? mj[17 - k] : mj[11 - k]) : mj[k - 6];
           g0 = fmaf_(s.Eb[c][0][k], mv, g0); g1 = fmaf_(s.Eb[c][1][k], mv, g1); g2 = fmaf_(s.Eb[c][2][k], mv, g2);
         }
         const int pr = cp * (cp + 1) / 2 + c;
@@ -917,21 +922,28 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   float Acol[kMaxEfc];
 #pragma unroll
   for (int ii = 0; ii < kMaxEfc; ++ii) Acol[ii] = 0.f;
+  const float Rci = s.Rc[ci];
+  float G[9];
 #pragma unroll
   for (int ii = 0; ii < kMaxEfc; ++ii) {
     if (ii >= nefc_max) break;
     const int c2 = ii >> 2, k2 = ii & 3;
-    int lo, hi, klo, khi;
-    if (c2 < ci) { lo = c2; hi = ci; klo = k2; khi = ki; }
-    else if (c2 > ci) { lo = ci; hi = c2; klo = ki; khi = k2; }
-    else { lo = ci; hi = ci; klo = ki > k2 ? ki : k2; khi = ki > k2 ? k2 : ki; }
-    const float* G = s.u.G[hi * (hi + 1) / 2 + lo];
+    if (k2 == 0) {   // the lane's G block of the pair (ci, c2), read once for the c2's four rows
+      const int lo = c2 < ci ? c2 : ci, hi = c2 < ci ? ci : c2;
+      const float* Gp = s.u.G[hi * (hi + 1) / 2 + lo];
+#pragma unroll
+      for (int e = 0; e < 9; ++e) G[e] = Gp[e];
+    }
+    int klo, khi;
+    if (c2 < ci) { klo = k2; khi = ki; }
+    else if (c2 > ci) { klo = ki; khi = k2; }
+    else { klo = ki > k2 ? ki : k2; khi = ki > k2 ? k2 : ki; }
     const float d0 = dcoef(klo, 0), d1 = dcoef(klo, 1), d2 = dcoef(klo, 2);
     const float t0 = fmaf_(d2, G[6], fmaf_(d1, G[3], d0 * G[0]));
     const float t1 = fmaf_(d2, G[7], fmaf_(d1, G[4], d0 * G[1]));
     const float t2 = fmaf_(d2, G[8], fmaf_(d1, G[5], d0 * G[2]));
     float val = fmaf_(t2, dcoef(khi, 2), fmaf_(t1, dcoef(khi, 1), t0 * dcoef(khi, 0)));
-    val = (ii == l) ? val + s.Rc[ci] : val;
+    val = (ii == l) ? val + Rci : val;
     Acol[ii] = (row && ii < nefc) ? val : 0.f;
   }
   const float bi = row ? s.bvec[l] : 0.f;
