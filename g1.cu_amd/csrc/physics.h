@@ -923,28 +923,31 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
   for (int ii = 0; ii < kMaxEfc; ++ii) Acol[ii] = 0.f;
   const float Rci = s.Rc[ci];
-  float G[9];
+  // pyramid coefficients of the lane's own row (d0 = 1 for every direction)
+  const float dki1 = dcoef(ki, 1), dki2 = dcoef(ki, 2);
 #pragma unroll
-  for (int ii = 0; ii < kMaxEfc; ++ii) {
-    if (ii >= nefc_max) break;
-    const int c2 = ii >> 2, k2 = ii & 3;
-    if (k2 == 0) {   // the lane's G block of the pair (ci, c2), read once for the c2's four rows
-      const int lo = c2 < ci ? c2 : ci, hi = c2 < ci ? ci : c2;
-      const float* Gp = s.u.G[hi * (hi + 1) / 2 + lo];
+  for (int c2 = 0; c2 < kNFoot; ++c2) {
+    if (c2 >= ncon_max) break;
+    const int lo = c2 < ci ? c2 : ci, hi = c2 < ci ? ci : c2;
+    const float* Gp = s.u.G[hi * (hi + 1) / 2 + lo];
+    float G[9];
 #pragma unroll
-      for (int e = 0; e < 9; ++e) G[e] = Gp[e];
+    for (int e = 0; e < 9; ++e) G[e] = Gp[e];
+    const bool lt = c2 < ci, eq = c2 == ci, keep = row && c2 < ncon;
+#pragma unroll
+    for (int k2 = 0; k2 < 4; ++k2) {
+      // (klo, khi) = (k2, ki) if c2 < ci, (ki, k2) if c2 > ci, (max, min) within one contact
+      const bool k2lo = lt || (eq && k2 >= ki);
+      const float dk1 = dcoef(k2, 1), dk2 = dcoef(k2, 2);
+      const float dl1 = k2lo ? dk1 : dki1, dl2 = k2lo ? dk2 : dki2;
+      const float dh1 = k2lo ? dki1 : dk1, dh2 = k2lo ? dki2 : dk2;
+      const float t0 = fmaf_(dl2, G[6], fmaf_(dl1, G[3], 1.f * G[0]));
+      const float t1 = fmaf_(dl2, G[7], fmaf_(dl1, G[4], 1.f * G[1]));
+      const float t2 = fmaf_(dl2, G[8], fmaf_(dl1, G[5], 1.f * G[2]));
+      float val = fmaf_(t2, dh2, fmaf_(t1, dh1, t0 * 1.f));
+      val = (eq && k2 == ki) ? val + Rci : val;
+      Acol[4 * c2 + k2] = keep ? val : 0.f;
     }
-    int klo, khi;
-    if (c2 < ci) { klo = k2; khi = ki; }
-    else if (c2 > ci) { klo = ki; khi = k2; }
-    else { klo = ki > k2 ? ki : k2; khi = ki > k2 ? k2 : ki; }
-    const float d0 = dcoef(klo, 0), d1 = dcoef(klo, 1), d2 = dcoef(klo, 2);
-    const float t0 = fmaf_(d2, G[6], fmaf_(d1, G[3], d0 * G[0]));
-    const float t1 = fmaf_(d2, G[7], fmaf_(d1, G[4], d0 * G[1]));
-    const float t2 = fmaf_(d2, G[8], fmaf_(d1, G[5], d0 * G[2]));
-    float val = fmaf_(t2, dcoef(khi, 2), fmaf_(t1, dcoef(khi, 1), t0 * dcoef(khi, 0)));
-    val = (ii == l) ? val + Rci : val;
-    Acol[ii] = (row && ii < nefc) ? val : 0.f;
   }
   const float bi = row ? s.bvec[l] : 0.f;
   float Aii = 1.f;
