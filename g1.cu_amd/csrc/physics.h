@@ -230,6 +230,31 @@ struct SolveParams {
   bool contact;  // foot-ground contact on/off
 };
 
+// One projected Gauss-Seidel sweep over rows II.. of the lane-held columns, fully unrolled with the
+// rows nested: the first row at or past the wave's largest row count nefc_max branches once to the
+// end of the sweep. Row ii's update f_ii = max(0, -(b_ii + A_ii.f - A_ii,ii f_ii) / A_ii,ii)
+// (reference: src/contact.cuh:159-171) is evaluated by every lane and kept by lane ii; a lane without
+// a row (ii >= its world's count) may take it: its column entries are +0, so its f enters no row
+// sum. The quotient x / A_ii uses the correctly rounded reciprocal y = RN(1/A_ii) and one
+// exact-residual correction: q0 = RN(x y), r = x - A_ii q0 (exact with fma), q = RN(q0 + r y) equals
+// RN(x / A_ii) (Markstein's theorem), the IEEE quotient, on a 3-op dependency chain.
+template <int II>
+__device__ __forceinline__ void pgs_sweep(const float (&Acol)[kMaxEfc], float Aii, float yi, float bi, int l,
+                                          int nefc_max, float& fi) {
+  if constexpr (II < kMaxEfc) {
+    if (II < nefc_max) {
+      const float sum = gsum(Acol[II] * fi);   // sum_j A[II][j] f_j (lane j holds column j)
+      const float ri = fmaf_(-Aii, fi, bi + sum);
+      const float x = -ri;
+      const float q0 = x * yi;
+      const float fn = __builtin_fmaf(__builtin_fmaf(-q0, Aii, x), yi, q0);
+      const float fnew = fn > 0.f ? fn : 0.f;
+      fi = (l == II) ? fnew : fi;
+      pgs_sweep<II + 1>(Acol, Aii, yi, bi, l, nefc_max, fi);
+    }
+  }
+}
+
 // ================================================================ substep: qacc of one world
 // Inputs: lane state, PD torque of the lane's hinge dof (jtau). Output: qacc of the lane's dofs
 // (lane 1: 6 base dofs into bqacc[], hinge lanes: jqacc). Returns this world's contact count.
@@ -954,28 +979,11 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
   for (int ii = 0; ii < kMaxEfc; ++ii) Aii = (ii == l && row) ? Acol[ii] : Aii;
 
-  // ---------------- projected Gauss-Seidel (reference: src/contact.cuh:159-171)
-  // Row ii's update f_ii = max(0, -(b_ii + A_ii.f - A_ii,ii f_ii) / A_ii,ii) is evaluated by every
-  // lane and kept by lane ii only (branch-free). The quotient x / A_ii uses the correctly rounded
-  // reciprocal y = RN(1/A_ii) once per solve and one exact-residual correction per row:
-  // q0 = RN(x y), r = x - A_ii q0 (exact with fma), q = RN(q0 + r y) equals RN(x / A_ii)
-  // (Markstein's theorem), i.e. the IEEE quotient, on a 3-op dependency chain.
+  // ---------------- projected Gauss-Seidel (reference: src/contact.cuh:159-171), P.pgs sweeps
   float fi = 0.f;
   const float yi = rcp_rn(Aii);
 #pragma unroll 1
-  for (int it = 0; it < P.pgs; ++it) {
-#pragma unroll
-    for (int ii = 0; ii < kMaxEfc; ++ii) {
-      if (ii >= nefc_max) break;
-      const float sum = gsum(Acol[ii] * fi);   // sum_j A[ii][j] f_j (lane j holds column j)
-      const float ri = fmaf_(-Aii, fi, bi + sum);
-      const float x = -ri;
-      const float q0 = x * yi;
-      const float fn = __builtin_fmaf(__builtin_fmaf(-q0, Aii, x), yi, q0);
-      const float fnew = fn > 0.f ? fn : 0.f;
-      fi = (row && l == ii) ? fnew : fi;
-    }
-  }
+  for (int it = 0; it < P.pgs; ++it) pgs_sweep<0>(Acol, Aii, yi, bi, l, nefc_max, fi);
   if (row) s.f[l] = fi;
   __syncthreads();
 
