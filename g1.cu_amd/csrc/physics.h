@@ -283,7 +283,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     float h = 0.5f * st.jq, sn = sin_rn(h);
     aa = {cos_rn(h), L.axis.x * sn, L.axis.y * sn, L.axis.z * sn};
   }
-#pragma unroll 1
+#pragma unroll
   for (int r = 2; r <= kMaxDepth; ++r) {
     Q4 qp{gshfl(xq.w, L.par), gshfl(xq.x, L.par), gshfl(xq.y, L.par), gshfl(xq.z, L.par)};
     V3 pp{gshfl(xp.x, L.par), gshfl(xp.y, L.par), gshfl(xp.z, L.par)};
@@ -373,7 +373,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
     aw = a_w; av = a_v;
   }
-#pragma unroll 1
+#pragma unroll
   for (int r = 2; r <= kMaxDepth; ++r) {
     V3 pw{gshfl(vw.x, L.par), gshfl(vw.y, L.par), gshfl(vw.z, L.par)};
     V3 pv{gshfl(vv.x, L.par), gshfl(vv.y, L.par), gshfl(vv.z, L.par)};
@@ -416,7 +416,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     Fv = {Iav.x + cv.x, Iav.y + cv.y, Iav.z + cv.z};
   }
   // ---------------- leaf->root force gather (reference: src/aba_bias.cuh:112-120)
-#pragma unroll 1
+#pragma unroll
   for (int cd = kMaxDepth; cd >= 2; --cd) {
     const bool gather = (L.depth == cd - 1);
     V3 gw{gshfl(Fw.x, L.c0), gshfl(Fw.y, L.c0), gshfl(Fw.z, L.c0)};
@@ -553,7 +553,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   prefetch(kMaxDepth);
   const float none[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   constexpr int kTorsoDepth = body_depth[16];
-#pragma unroll 1
+#pragma unroll
   for (int cd = kMaxDepth; cd > kTorsoDepth; --cd) level(cd, false, none, none);
   {
     // the right arm (chain 3, lanes 24..) ends at depth 5; its downdate and bias force join the
@@ -564,7 +564,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int j = 0; j < 6; ++j) { gD[j] = gshfl(Dlr[j], 24 + rowc); gc[j] = gshfl(cs[j], 24 + rowc); }
     level(kTorsoDepth, grp == 2, gD, gc);
   }
-#pragma unroll 1
+#pragma unroll
   for (int cd = kTorsoDepth - 1; cd >= 2; --cd) level(cd, false, none, none);
   // pelvis: I^A_1 = I6_1 + D_14 + D_8 + D_2 and pA_1 = cs_14 + cs_8 + cs_2 (descending children),
   // row r on lane r of chain 0; lane 1 keeps pA_1 for the base solve
@@ -669,7 +669,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
   for (int k = 0; k < 6; ++k) Uk[k] = s.u.fac.U[L.b][k];
   const float usk = s.u.fac.us[L.b], iDk = s.u.fac.invD[L.b];
-#pragma unroll 1
+#pragma unroll
   for (int r = 2; r <= kMaxDepth; ++r) {
     float ap[6];
 #pragma unroll
