@@ -907,8 +907,9 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const float* mcol = s.Mm[active ? j : 0];
 #pragma unroll
     for (int a = 0; a < 18; ++a) mj[a] = mcol[a];
-#pragma unroll 1
-    for (int c = 0; c < ncon_max; ++c) {
+#pragma unroll
+    for (int c = 0; c < kNFoot; ++c) {
+      if (c >= ncon_max) break;
       if (active && c <= cp) {
         const bool rightleg = s.con_leg[c] != 0;
         float g0 = 0.f, g1 = 0.f, g2 = 0.f;
@@ -988,19 +989,23 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   __syncthreads();
 
   // ---------------- qacc = qacc_smooth + sum_c sum_a fb_c[a] m_{c,a} (reference: src/env_qacc.cuh:196-211)
+  // lane l: dof l and (lanes 0..2) dof 32 + l, both accumulated in one pass over the contacts
+  {
+    static_assert(kNV <= 2 * kGroup, "two dofs per lane");
+    const int d1 = l, d2 = kGroup + l < kNV ? kGroup + l : l;
+    float dq1 = 0.f, dq2 = 0.f;
 #pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    const int d = pass == 0 ? l : kGroup + l;
-    if (d < kNV) {
-      float dq = 0.f;
-#pragma unroll 1
-      for (int c = 0; c < ncon; ++c) {
+    for (int c = 0; c < kNFoot; ++c) {
+      if (c >= ncon_max) break;
+      if (c < ncon) {
         const float f0 = s.f[4 * c], f1 = s.f[4 * c + 1], f2 = s.f[4 * c + 2], f3 = s.f[4 * c + 3];
         const float fb0 = f0 + f1 + f2 + f3, fb1 = f0 - f1, fb2 = f2 - f3;
-        dq += fmaf_(fb2, s.Mm[3 + 3 * c][d], fmaf_(fb1, s.Mm[2 + 3 * c][d], fb0 * s.Mm[1 + 3 * c][d]));
+        dq1 += fmaf_(fb2, s.Mm[3 + 3 * c][d1], fmaf_(fb1, s.Mm[2 + 3 * c][d1], fb0 * s.Mm[1 + 3 * c][d1]));
+        dq2 += fmaf_(fb2, s.Mm[3 + 3 * c][d2], fmaf_(fb1, s.Mm[2 + 3 * c][d2], fb0 * s.Mm[1 + 3 * c][d2]));
       }
-      s.qacc[d] = s.Mm[0][d] + dq;
     }
+    s.qacc[d1] = s.Mm[0][d1] + dq1;
+    if (kGroup + l < kNV) s.qacc[d2] = s.Mm[0][d2] + dq2;
   }
   __syncthreads();
   if (base) {
