@@ -373,21 +373,70 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
     aw = a_w; av = a_v;
   }
+  // Hinge bodies, chain-parallel: the hinges form four chains (left leg 2..7, right leg 8..13,
+  // waist 14..16 continued by the left arm 17..23, right arm 24..30 off the torso 16), walked
+  // root -> leaf in lock-step over tree depth. Chain g runs on lanes 8g..8g+5 and lane 8g+c holds
+  // spatial component c (w0 w1 w2 v0 v1 v2) of the current body's velocity and acceleration; the
+  // cross products take the parent's other components from the chain's lanes. Each component is
+  // the lane-per-body formula term for term: v = vp + S qd, a = ap + (vp x S) qd with
+  // (vp x S)_w = w_p x s_w, (vp x S)_v = w_p x s_v + v_p x s_w. The results go to LDS (the
+  // solve-output region is idle until the factor) and each body lane reads its own back.
+  const int grp = l >> 3, crow = l & 7, rowc = crow < 6 ? crow : 5;
+  const int c_off = grp == 0 ? 0 : (grp == 1 ? 6 : (grp == 2 ? 12 : 19));
+  const int c_lo = grp == 3 ? 5 : 2, c_hi = grp >= 2 ? kMaxDepth : 7;
+  auto chain_body = [&](int cd) { return (cd >= c_lo && cd <= c_hi) ? cd + c_off : 2; };
+  static_assert(body_parent[2] == 1 && body_parent[8] == 1 && body_parent[14] == 1 && body_parent[24] == 16 &&
+                body_depth[24] == 5 && body_depth[2] == 2, "chain roots");
+  float* const V6 = &s.Mm[0][0];          // [kNBody][6] body velocities about the pelvis origin
+  float* const A6 = V6 + kNBody * 6;      // [kNBody][6] body accelerations
+  static_assert(kCols * kMmStride >= 2 * kNBody * 6, "RNE staging fits the solve-output region");
+  if (base) {
+    V6[6 + 0] = vw.x; V6[6 + 1] = vw.y; V6[6 + 2] = vw.z; V6[6 + 3] = vv.x; V6[6 + 4] = vv.y; V6[6 + 5] = vv.z;
+    A6[6 + 0] = aw.x; A6[6 + 1] = aw.y; A6[6 + 2] = aw.z; A6[6 + 3] = av.x; A6[6 + 4] = av.y; A6[6 + 5] = av.z;
+  }
+  __syncthreads();   // pelvis velocity / acceleration and every motion axis and hinge qvel in LDS
+  {
+    const int k = rowc < 3 ? rowc : rowc - 3, k1 = k == 2 ? 0 : k + 1, k2 = k == 0 ? 2 : k - 1;
+    const bool isv = rowc >= 3;
+    const int so = isv ? 3 : 0;
+    const int base8 = 8 * grp;
+    float pc = 0.f, pac = 0.f;   // component rowc of the current body's v and a
 #pragma unroll
-  for (int r = 2; r <= kMaxDepth; ++r) {
-    V3 pw{gshfl(vw.x, L.par), gshfl(vw.y, L.par), gshfl(vw.z, L.par)};
-    V3 pv{gshfl(vv.x, L.par), gshfl(vv.y, L.par), gshfl(vv.z, L.par)};
-    V3 paw{gshfl(aw.x, L.par), gshfl(aw.y, L.par), gshfl(aw.z, L.par)};
-    V3 pav{gshfl(av.x, L.par), gshfl(av.y, L.par), gshfl(av.z, L.par)};
-    if (L.depth == r) {
-      V3 Sdw, Sdv;
-      crossm(pw, pv, sw, sv, Sdw, Sdv);
-      const float qd = st.jqd;
-      vw = {fmaf_(sw.x, qd, pw.x), fmaf_(sw.y, qd, pw.y), fmaf_(sw.z, qd, pw.z)};
-      vv = {fmaf_(sv.x, qd, pv.x), fmaf_(sv.y, qd, pv.y), fmaf_(sv.z, qd, pv.z)};
-      aw = {fmaf_(Sdw.x, qd, paw.x), fmaf_(Sdw.y, qd, paw.y), fmaf_(Sdw.z, qd, paw.z)};
-      av = {fmaf_(Sdv.x, qd, pav.x), fmaf_(Sdv.y, qd, pav.y), fmaf_(Sdv.z, qd, pav.z)};
+    for (int r = 2; r <= kMaxDepth; ++r) {
+      const bool act = r >= c_lo && r <= c_hi;
+      const int b = chain_body(r);
+      // parent's components: the chain's previous level, or from LDS at a chain's first body
+      float X1 = gshfl(pc, base8 + k1), X2 = gshfl(pc, base8 + k2);            // w_p[k+1], w_p[k+2]
+      float Y1 = gshfl(pc, base8 + 3 + k1), Y2 = gshfl(pc, base8 + 3 + k2);    // v_p[k+1], v_p[k+2]
+      float P = pc, PA = pac;
+      if (r == 2 || r == 5) {
+        const bool start = (r == c_lo);
+        const int pb = grp == 3 ? 16 : 1;
+        const float* pv6 = V6 + 6 * pb;
+        if (start) {
+          X1 = pv6[k1]; X2 = pv6[k2]; Y1 = pv6[3 + k1]; Y2 = pv6[3 + k2];
+          P = pv6[rowc]; PA = A6[6 * pb + rowc];
+        }
+      }
+      const float* Sb = s.u.fac.S[b + 4];
+      const float qd = s.qvel[b + 4];
+      const float vn = fmaf_(Sb[rowc], qd, P);
+      const float t1 = fmaf_(-X2, Sb[so + k1], X1 * Sb[so + k2]);   // (w_p x s_w)_k, or (w_p x s_v)_k
+      const float t2 = fmaf_(-Y2, Sb[k1], Y1 * Sb[k2]);             // (v_p x s_w)_k
+      const float sd = isv ? t1 + t2 : t1;
+      const float an = fmaf_(sd, qd, PA);
+      pc = act ? vn : pc;
+      pac = act ? an : pac;
+      if (act && crow < 6) { V6[6 * b + crow] = pc; A6[6 * b + crow] = pac; }
+      if (r == 4) __syncthreads();   // the torso (depth 4) is in LDS before the right arm starts
     }
+  }
+  __syncthreads();
+  if (L.hinge) {
+    const float* v6 = V6 + 6 * L.b;
+    const float* a6 = A6 + 6 * L.b;
+    vw = {v6[0], v6[1], v6[2]}; vv = {v6[3], v6[4], v6[5]};
+    aw = {a6[0], a6[1], a6[2]}; av = {a6[3], a6[4], a6[5]};
   }
 
   // ---------------- body forces f = I a + v x* (I v) (reference: src/aba_bias.cuh:103-111,
@@ -496,14 +545,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // descending child order (torso: + D_24 then + D_17), U_i = sum_j I^A_ij S_j, D = S.U + arm
   // (+ dt kd), downdate I^A_ij - U_i U_j / D; the products U_i U_j commute, so row r of the
   // symmetric downdate equals the packed entries bit for bit.
-  const int grp = l >> 3, crow = l & 7, rowc = crow < 6 ? crow : 5;
-  const int c_off = grp == 0 ? 0 : (grp == 1 ? 6 : (grp == 2 ? 12 : 19));
-  const int c_lo = grp == 3 ? 5 : 2, c_hi = grp >= 2 ? kMaxDepth : 7;
   float Dlr[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // row `crow` of the last body's downdate
   float cs[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};    // last body's pA + U u / D (all six components)
   // the next level's body inputs (motion axis, I6 row, right-hand side, armature, dt kd; the
   // last three live on lane b and come by shuffle), loaded while the current level computes
-  auto chain_body = [&](int cd) { return (cd >= c_lo && cd <= c_hi) ? cd + c_off : 2; };
   float Sn[6], In[6], xn, an, kn;
   auto prefetch = [&](int cd) {
     const int b = chain_body(cd);
