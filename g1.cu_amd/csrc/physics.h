@@ -464,48 +464,16 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     Fw = {Iaw.x + cw.x, Iaw.y + cw.y, Iaw.z + cw.z};
     Fv = {Iav.x + cv.x, Iav.y + cv.y, Iav.z + cv.z};
   }
-  // ---------------- leaf->root force gather (reference: src/aba_bias.cuh:112-120)
-#pragma unroll
-  for (int cd = kMaxDepth; cd >= 2; --cd) {
-    const bool gather = (L.depth == cd - 1);
-    V3 gw{gshfl(Fw.x, L.c0), gshfl(Fw.y, L.c0), gshfl(Fw.z, L.c0)};
-    V3 gv{gshfl(Fv.x, L.c0), gshfl(Fv.y, L.c0), gshfl(Fv.z, L.c0)};
-    if (gather && L.nchild > 0) { Fw = vadd(Fw, gw); Fv = vadd(Fv, gv); }
-    if (cd == body_depth[17] || cd == 2) {   // multi-child parents: torso (depth 4), pelvis (depth 1)
-      gw = {gshfl(Fw.x, L.c1), gshfl(Fw.y, L.c1), gshfl(Fw.z, L.c1)};
-      gv = {gshfl(Fv.x, L.c1), gshfl(Fv.y, L.c1), gshfl(Fv.z, L.c1)};
-      if (gather && L.nchild > 1) { Fw = vadd(Fw, gw); Fv = vadd(Fv, gv); }
-      if (cd == 2) {
-        gw = {gshfl(Fw.x, L.c2), gshfl(Fw.y, L.c2), gshfl(Fw.z, L.c2)};
-        gv = {gshfl(Fv.x, L.c2), gshfl(Fv.y, L.c2), gshfl(Fv.z, L.c2)};
-        if (gather && L.nchild > 2) { Fw = vadd(Fw, gw); Fv = vadd(Fv, gv); }
-      }
-    }
-  }
-  // smooth right-hand side tau - bias of the lane's dofs (lane 1: the six base dofs, tau = 0)
-  float xr = 0.f, xb[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (L.hinge) {
-    const float bias = fmaf_(sv.z, Fv.z, fmaf_(sv.y, Fv.y, fmaf_(sv.x, Fv.x, fmaf_(sw.z, Fw.z, fmaf_(sw.y, Fw.y, sw.x * Fw.x)))));
-    xr = -bias + jtau;
-  }
-  if (base) {
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      // translation axis e_k: S = (0,0,0, e_k); rotation axis R1 col k: S = (R1 col, 0,0,0)
-      const float e0 = k == 0 ? 1.f : 0.f, e1 = k == 1 ? 1.f : 0.f, e2 = k == 2 ? 1.f : 0.f;
-      const float bt = fmaf_(e2, Fv.z, fmaf_(e1, Fv.y, fmaf_(e0, Fv.x, fmaf_(0.f, Fw.z, fmaf_(0.f, Fw.y, 0.f * Fw.x)))));
-      const float br = fmaf_(0.f, Fv.z, fmaf_(0.f, Fv.y, fmaf_(0.f, Fv.x,
-                       fmaf_(R1.m[6 + k], Fw.z, fmaf_(R1.m[3 + k], Fw.y, R1.m[k] * Fw.x)))));
-      xb[k] = -bt + 0.f;
-      xb[3 + k] = -br + 0.f;
-    }
-  }
-
   // ---------------- body spatial inertia about the pelvis origin, 21-packed (reference:
   // src/aba_factor.cuh:51-76), staged in LDS for the chain-parallel factor. The solve-output
   // region (Mm) is free until the factor is done and holds it.
-  static_assert(kCols * kMmStride >= kNBody * 21, "I6 staging fits the solve-output region");
+  static_assert(kCols * kMmStride >= kNBody * 27, "I6 and force staging fit the solve-output region");
   float* const I6 = &s.Mm[0][0];
+  float* const Fo = I6 + kNBody * 21;      // [kNBody][6] each body's own RNE force (w, v)
+  if (L.body) {
+    Fo[6 * L.b + 0] = Fw.x; Fo[6 * L.b + 1] = Fw.y; Fo[6 * L.b + 2] = Fw.z;
+    Fo[6 * L.b + 3] = Fv.x; Fo[6 * L.b + 4] = Fv.y; Fo[6 * L.b + 5] = Fv.z;
+  }
   if (L.body) {
     const float c2 = dot3(cc, cc);
     float A[9];
@@ -531,7 +499,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       for (int j = i; j < 6; ++j) I6[L.b * 21 + symidx(i, j)] = M6[i * 6 + j];
   }
   const float S6[6] = {sw.x, sw.y, sw.z, sv.x, sv.y, sv.z};
-  __syncthreads();   // S and I6 of every body in LDS
+  __syncthreads();   // S, I6 and the own forces of every body in LDS
 
   // ---------------- damped articulated-inertia factor, chain-parallel (reference:
   // src/aba_factor.cuh:77-88), fused with the leaf -> root sweep of the smooth solve
@@ -549,23 +517,32 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   float cs[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};    // last body's pA + U u / D (all six components)
   // the next level's body inputs (motion axis, I6 row, right-hand side, armature, dt kd; the
   // last three live on lane b and come by shuffle), loaded while the current level computes
-  float Sn[6], In[6], xn, an, kn;
+  // The RNE force gather rides on the same sweep (reference: src/aba_bias.cuh:112-120): lane r
+  // carries component r of the body's subtree force F_b = F_own_b + the children's F in
+  // descending child order (torso: + F_24 then + F_17), and the body's right-hand side is
+  // tau - S.F (the bias in the lane-per-body form's order).
+  float Fc = 0.f;                                  // component rowc of the last body's subtree force
+  float Sn[6], In[6], Fn, tn, an, kn;
   auto prefetch = [&](int cd) {
     const int b = chain_body(cd);
 #pragma unroll
     for (int j = 0; j < 6; ++j) { Sn[j] = s.u.fac.S[b + 4][j]; In[j] = I6[b * 21 + symidx(rowc, j)]; }
-    xn = gshfl(xr, b);
+    Fn = Fo[6 * b + rowc];
+    tn = gshfl(jtau, b);
     an = gshfl(L.arm, b);
     kn = gshfl(L.bdt, b);
   };
   // one level of the chains; `junction` adds the right arm's downdate and bias force (gD, gc)
   // to the torso before its own child's
-  auto level = [&](int cd, bool junction, const float* gD, const float* gc) {
+  auto level = [&](int cd, bool junction, const float* gD, const float* gc, float gF) {
     const bool act = cd >= c_lo && cd <= c_hi;
     const bool leaf = cd == c_hi;
     const int b = chain_body(cd);
     float Sd[6], IAr[6], pA[6];
-    const float xb_ = xn, arm = an, bdt = kn;
+    const float tb = tn, arm = an, bdt = kn;
+    float F = Fn;
+    if (junction) F = F + gF;
+    F = leaf ? F : F + Fc;
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
       Sd[j] = Sn[j];
@@ -574,6 +551,12 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       IAr[j] = leaf ? v : v + Dlr[j];
       pA[j] = leaf ? q : q + cs[j];
     }
+    const float Fb[6] = {chain_bcast<0>(F), chain_bcast<1>(F), chain_bcast<2>(F),
+                         chain_bcast<3>(F), chain_bcast<4>(F), chain_bcast<5>(F)};
+    float bias = Sd[0] * Fb[0];
+#pragma unroll
+    for (int j = 1; j < 6; ++j) bias = fmaf_(Sd[j], Fb[j], bias);
+    const float xb_ = -bias + tb;
     float ur = 0.f;
 #pragma unroll
     for (int j = 0; j < 6; ++j) ur = fmaf_(IAr[j], Sd[j], ur);
@@ -592,6 +575,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       Dlr[j] = act ? dl : Dlr[j];
       cs[j] = act ? c : cs[j];
     }
+    Fc = act ? F : Fc;
     if (act && crow < 6) s.u.fac.U[b][crow] = ur;
     if (act && crow == 0) { s.u.fac.invD[b] = invD; s.u.fac.us[b] = u; }
   };
@@ -599,7 +583,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   const float none[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   constexpr int kTorsoDepth = body_depth[16];
 #pragma unroll
-  for (int cd = kMaxDepth; cd > kTorsoDepth; --cd) level(cd, false, none, none);
+  for (int cd = kMaxDepth; cd > kTorsoDepth; --cd) level(cd, false, none, none, 0.f);
   {
     // the right arm (chain 3, lanes 24..) ends at depth 5; its downdate and bias force join the
     // torso (chain 2) at depth 4
@@ -607,14 +591,31 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     float gD[6], gc[6];
 #pragma unroll
     for (int j = 0; j < 6; ++j) { gD[j] = gshfl(Dlr[j], 24 + rowc); gc[j] = gshfl(cs[j], 24 + rowc); }
-    level(kTorsoDepth, grp == 2, gD, gc);
+    level(kTorsoDepth, grp == 2, gD, gc, gshfl(Fc, 24 + rowc));
   }
 #pragma unroll
-  for (int cd = kTorsoDepth - 1; cd >= 2; --cd) level(cd, false, none, none);
+  for (int cd = kTorsoDepth - 1; cd >= 2; --cd) level(cd, false, none, none, 0.f);
   // pelvis: I^A_1 = I6_1 + D_14 + D_8 + D_2 and pA_1 = cs_14 + cs_8 + cs_2 (descending children),
   // row r on lane r of chain 0; lane 1 keeps pA_1 for the base solve
   float pAs[6];
+  float xb[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   {
+    // pelvis subtree force F_1 = F_own_1 + F_14 + F_8 + F_2 (descending children), component r
+    // on lane r of chain 0, then the free joint's right-hand side -S_base.F_1 on lane 1
+    const float F1 = ((Fo[6 + rowc] + gshfl(Fc, 16 + rowc)) + gshfl(Fc, 8 + rowc)) + Fc;
+    const V3 Fw{gshfl(F1, 0), gshfl(F1, 1), gshfl(F1, 2)}, Fv{gshfl(F1, 3), gshfl(F1, 4), gshfl(F1, 5)};
+    if (base) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        // translation axis e_k: S = (0,0,0, e_k); rotation axis R1 col k: S = (R1 col, 0,0,0)
+        const float e0 = k == 0 ? 1.f : 0.f, e1 = k == 1 ? 1.f : 0.f, e2 = k == 2 ? 1.f : 0.f;
+        const float bt = fmaf_(e2, Fv.z, fmaf_(e1, Fv.y, fmaf_(e0, Fv.x, fmaf_(0.f, Fw.z, fmaf_(0.f, Fw.y, 0.f * Fw.x)))));
+        const float br = fmaf_(0.f, Fv.z, fmaf_(0.f, Fv.y, fmaf_(0.f, Fv.x,
+                         fmaf_(R1.m[6 + k], Fw.z, fmaf_(R1.m[3 + k], Fw.y, R1.m[k] * Fw.x)))));
+        xb[k] = -bt + 0.f;
+        xb[3 + k] = -br + 0.f;
+      }
+    }
     float I1[6];
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
