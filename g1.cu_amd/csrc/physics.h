@@ -425,8 +425,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const float t2 = fmaf_(-Y2, Sb[k1], Y1 * Sb[k2]);             // (v_p x s_w)_k
       const float sd = isv ? t1 + t2 : t1;
       const float an = fmaf_(sd, qd, PA);
-      pc = act ? vn : pc;
-      pac = act ? an : pac;
+      // a chain's values outside its depth range are never read (its first body takes the parent
+      // from LDS, its results are stored only while active), so no select keeps them
+      pc = vn;
+      pac = an;
       if (act && crow < 6) { V6[6 * b + crow] = pc; A6[6 * b + crow] = pac; }
       if (r == 4) __syncthreads();   // the torso (depth 4) is in LDS before the right arm starts
     }
@@ -572,10 +574,13 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int j = 0; j < 6; ++j) {
       const float dl = fmaf_(-(ur * Ub[j]), invD, IAr[j]);   // ur == Ub[crow] on rows 0..5
       const float c = fmaf_(Ub[j], ud, pA[j]);
-      Dlr[j] = act ? dl : Dlr[j];
-      cs[j] = act ? c : cs[j];
+      // Outside a chain's depth range its values are dead: before its leaf the leaf level starts
+      // afresh, after its root nothing reads them (the right arm's last body is read at the
+      // torso level before that level overwrites it); only the LDS stores below need `act`.
+      Dlr[j] = dl;
+      cs[j] = c;
     }
-    Fc = act ? F : Fc;
+    Fc = F;
     if (act && crow < 6) s.u.fac.U[b][crow] = ur;
     if (act && crow == 0) { s.u.fac.invD[b] = invD; s.u.fac.us[b] = u; }
   };
