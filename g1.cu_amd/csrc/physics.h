@@ -384,7 +384,12 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   const int grp = l >> 3, crow = l & 7, rowc = crow < 6 ? crow : 5;
   const int c_off = grp == 0 ? 0 : (grp == 1 ? 6 : (grp == 2 ? 12 : 19));
   const int c_lo = grp == 3 ? 5 : 2, c_hi = grp >= 2 ? kMaxDepth : 7;
-  auto chain_body = [&](int cd) { return (cd >= c_lo && cd <= c_hi) ? cd + c_off : 2; };
+  // Body of chain g at depth cd. Outside the chain's depth range this is another in-range body
+  // (cd + c_off lies in 1..30 for every cd in 1..11) whose data is read but never stored: keeping
+  // the index linear in cd lets every per-level LDS address be a loop-invariant register plus an
+  // immediate offset.
+  auto chain_body = [&](int cd) { return cd + c_off; };
+  static_assert(kMaxDepth + 19 < kNBody, "chain bodies in range");
   static_assert(body_parent[2] == 1 && body_parent[8] == 1 && body_parent[14] == 1 && body_parent[24] == 16 &&
                 body_depth[24] == 5 && body_depth[2] == 2, "chain roots");
   float* const V6 = &s.Mm[0][0];          // [kNBody][6] body velocities about the pelvis origin
