@@ -419,6 +419,16 @@ __global__ void k_divide(const float* a, const float* b, float* rcp, float* quot
   quot[i] = div_rn(a[i], b[i], y);
 }
 
+// sincos_small_rn of the physics kernel on caller-given arguments (parity probe)
+__global__ void k_sincos(const float* x, float* sn, float* cs, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s, c;
+  sincos_small_rn(x[i], s, c);
+  sn[i] = s;
+  cs[i] = c;
+}
+
 // ====================================================================== host side
 struct EnvState {
   int N, S, pgs;
@@ -822,6 +832,12 @@ int g1_probe_policy(int n, int nlayers, const int* hidden, int activation, const
 void g1_probe_divide(int n, const float* a, const float* b, float* rcp, float* quot) {
   if (n <= 0) return;
   hipLaunchKernelGGL(k_divide, dim3((n + 255) / 256), dim3(256), 0, 0, a, b, rcp, quot, n);
+  HIPCHECK(hipGetLastError());
+}
+
+void g1_probe_sincos(int n, const float* x, float* sn, float* cs) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_sincos, dim3((n + 255) / 256), dim3(256), 0, 0, x, sn, cs, n);
   HIPCHECK(hipGetLastError());
 }
 

@@ -71,6 +71,34 @@ __device__ __forceinline__ V3 qrot(Q4 q, V3 v) {
 __device__ __forceinline__ float sin_rn(float x) { return (float)sin((double)x); }
 __device__ __forceinline__ float cos_rn(float x) { return (float)cos((double)x); }
 
+// sin_rn and cos_rn of one argument on a short path for |x| <= 1/8 (the free joint's half rotation
+// per substep): the fp64 Taylor series by Horner, sin to x^11 and cos to x^12 (truncation below
+// 2^-68 relative), coefficients (-1)^k / n! rounded once, then one rounding to float. For every
+// float with |x| <= 1/8 this equals the fp64-libm value rounded to float (tests: the probe
+// g1_probe_sincos against the oracle over all of them); larger or non-finite x take the library.
+__device__ __forceinline__ void sincos_small_rn(float x, float& sn, float& cs) {
+  if (fabsf(x) <= 0.125f) {
+    const double xd = x, z = xd * xd;
+    double ps = -1.0 / 39916800.0;
+    ps = __builtin_fma(z, ps, 1.0 / 362880.0);
+    ps = __builtin_fma(z, ps, -1.0 / 5040.0);
+    ps = __builtin_fma(z, ps, 1.0 / 120.0);
+    ps = __builtin_fma(z, ps, -1.0 / 6.0);
+    double pc = 1.0 / 479001600.0;
+    pc = __builtin_fma(z, pc, -1.0 / 3628800.0);
+    pc = __builtin_fma(z, pc, 1.0 / 40320.0);
+    pc = __builtin_fma(z, pc, -1.0 / 720.0);
+    pc = __builtin_fma(z, pc, 1.0 / 24.0);
+    pc = __builtin_fma(z, pc, -0.5);
+    const float s_ = (float)__builtin_fma(xd * z, ps, xd);
+    sn = (x == 0.f) ? x : s_;   // sin(-0) = -0
+    cs = (float)__builtin_fma(z, pc, 1.0);
+  } else {
+    sn = sin_rn(x);
+    cs = cos_rn(x);
+  }
+}
+
 // Correctly rounded reciprocal and quotient on short dependency chains, for the positive normal
 // divisors of this path (pivots, D = S'I^A S + armature + dt kd, A_ii, impedances, angles).
 // rcp_rn: one Newton step y = y0 + y0 (1 - b y0) (fused) on the hardware estimate y0 returns
@@ -1101,8 +1129,10 @@ __device__ __forceinline__ void integrate_lane(const LaneModel& L, LaneState& st
     Q4 dq;
     if (ang < 1e-9f) dq = {1.f, 0.5f * v.x, 0.5f * v.y, 0.5f * v.z};
     else {
-      const float sn = div_rn(sin_rn(0.5f * ang), ang, rcp_rn(ang));
-      dq = {cos_rn(0.5f * ang), v.x * sn, v.y * sn, v.z * sn};
+      float sh, ch;
+      sincos_small_rn(0.5f * ang, sh, ch);
+      const float sn = div_rn(sh, ang, rcp_rn(ang));
+      dq = {ch, v.x * sn, v.y * sn, v.z * sn};
     }
     Q4 qn = qnorm(qmul(Q4{st.bq[3], st.bq[4], st.bq[5], st.bq[6]}, dq));
     st.bq[3] = qn.w; st.bq[4] = qn.x; st.bq[5] = qn.y; st.bq[6] = qn.z;

@@ -58,6 +58,7 @@ _lib.g1_probe_policy.restype = ctypes.c_int
 _lib.g1_probe_policy.argtypes = [ctypes.c_int, ctypes.c_int, _ip, ctypes.c_int] + [ctypes.c_void_p] * 4
 _lib.g1_probe_philox.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint, ctypes.c_uint]
 _lib.g1_probe_divide.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 4
+_lib.g1_probe_sincos.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 3
 _lib.g1_dynamics_bench.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 3 + [ctypes.c_int] * 5 + [ctypes.c_float] + \
     [ctypes.c_void_p] * 2
 

@@ -117,6 +117,10 @@ void g1_dynamics_bench(int n, float* qpos, float* qvel, const float* tau, int ns
  * quot[i] = a[i]/b[i] (both correctly rounded for positive normal b). */
 void g1_probe_divide(int n, const float* a, const float* b, float* rcp, float* quot);
 
+/* The physics kernel's sine/cosine of the free joint's half rotation angle on n DEVICE arguments:
+ * sn[i] = sin(x[i]), cs[i] = cos(x[i]) rounded to float. */
+void g1_probe_sincos(int n, const float* x, float* sn, float* cs);
+
 /* Philox4x32-10 of n DEVICE counters ctr [n*4] with key (k0, k1) into out [n*4]. */
 void g1_probe_philox(int n, const unsigned* ctr, unsigned* out, unsigned k0, unsigned k1);
 

@@ -1081,6 +1081,12 @@ void orc_implicit_traj_f(const float* q0, const float* v0, const float* Bdt, con
 void orc_implicit_traj_d(const double* q0, const double* v0, const double* Bdt, const double* tg, int n, double* qo,
                          double* vo) { implicit_traj(q0, v0, Bdt, tg, n, qo, vo); }
 
+// the oracle's sine and cosine of floats (fp64 libm, rounded once)
+void orc_sincos_f(long n, const float* x, float* sn, float* cs) {
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) { sn[i] = sin_(x[i]); cs[i] = cos_(x[i]); }
+}
+
 int orc_nbody() { return kNBody; }
 int orc_nq() { return kNQ; }
 int orc_nv() { return kNV; }

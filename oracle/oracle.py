@@ -49,6 +49,7 @@ def _load():
     lib.orc_qacc_debug_f.argtypes = [_f32p, _f32p, _f32p, _c.c_void_p, _c.c_int, _c.c_float] + [_f32p] * 7
     lib.orc_qacc_debug_f.restype = _c.c_int
     lib.orc_obs_f.argtypes = [_c.c_int, _f32p, _f32p, _f32p, _f32p]
+    lib.orc_sincos_f.argtypes = [_c.c_long, _f32p, _f32p, _f32p]
     lib.orc_policy_params.argtypes = [_c.c_int, _i32p, _c.c_int]
     lib.orc_policy_params.restype = _c.c_long
     lib.orc_mlp_f.argtypes = [_c.c_int, _c.c_int, _i32p, _c.c_int, _f32p, _f32p, _f32p, _f32p, _f32p]
@@ -189,6 +190,14 @@ def pgs(A, b, iters, dtype=np.float64):
 
 def impedance(pos, dtype=np.float64):
     return getattr(lib(), f"orc_impedance_{_dt(dtype)}")(pos)
+
+
+def sincos(x):
+    """sin and cos of float32 values as the oracle evaluates them: fp64 libm, rounded once."""
+    x = _arr(np.ravel(x), np.float32)
+    sn, cs = np.zeros_like(x), np.zeros_like(x)
+    lib().orc_sincos_f(x.size, x, sn, cs)
+    return sn, cs
 
 
 def obs(qp, qv, pa):

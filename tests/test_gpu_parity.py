@@ -230,6 +230,31 @@ def test_reciprocal_and_quotient_are_ieee(g1):
         assert np.array_equal(q.view(np.uint32), (a / bs).view(np.uint32))
 
 
+def test_small_angle_sincos_exhaustive(g1, orc):
+    """The free joint's quaternion update takes sin/cos of the half rotation per substep on a short
+    fp64 path for |x| <= 1/8: bit-identical to the oracle's fp64 libm rounded once for EVERY float
+    of that range (both signs, zeros and denormals), plus the library path just above it."""
+    import torch
+    lim = int(np.float32(0.125).view(np.uint32))          # bit patterns 0 .. lim are 0 .. 1/8
+    chunk = 1 << 25
+    for start in range(0, lim + 1, chunk):
+        bits = np.arange(start, min(start + chunk, lim + 1), dtype=np.uint32)
+        for sign in (np.uint32(0), np.uint32(0x80000000)):
+            x = (bits | sign).view(np.float32)
+            dx = torch.from_numpy(x).cuda()
+            ds, dc = torch.zeros_like(dx), torch.zeros_like(dx)
+            g1._lib.g1_probe_sincos(x.size, g1._dp(dx), g1._dp(ds), g1._dp(dc))
+            want_s, want_c = orc.sincos(x)
+            assert np.array_equal(ds.cpu().numpy().view(np.uint32), want_s.view(np.uint32)), start
+            assert np.array_equal(dc.cpu().numpy().view(np.uint32), want_c.view(np.uint32)), start
+    x = np.nextafter(np.float32(0.125), np.float32(1), dtype=np.float32) * np.arange(1, 1001, dtype=np.float32)
+    dx = torch.from_numpy(x).cuda()
+    ds, dc = torch.zeros_like(dx), torch.zeros_like(dx)
+    g1._lib.g1_probe_sincos(x.size, g1._dp(dx), g1._dp(ds), g1._dp(dc))
+    want_s, want_c = orc.sincos(x)
+    assert np.array_equal(ds.cpu().numpy(), want_s) and np.array_equal(dc.cpu().numpy(), want_c)
+
+
 def test_policy_mlp_trained_checkpoint(g1, orc):
     """The reference's trained policy (converted checkpoint) through the MFMA policy kernel vs the
     oracle's fp32 MLP on normalised observations of perturbed stand states."""
