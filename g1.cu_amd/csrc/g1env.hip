@@ -295,10 +295,10 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
     __syncthreads();
     float* t = in; in = out; out = t;
   }
-  // ---- fused head [mu(29) | v | pad]: its K range is split over the 4 waves when the free buffer
-  // holds the 4 partial tiles; the summed head then overwrites the (consumed) input tile
+  // ---- fused head [mu(29) | v | pad]: its K range is split over the waves when the free buffer
+  // holds their partial tiles; the summed head then overwrites the (consumed) input tile
   float* head = out;
-  if (kTileWorlds * kLdx >= 4 * 32 * 32) {
+  if (kTileWorlds * kLdx >= kPolicyWaves * 32 * 32) {
     mfma_head_splitk(in, kLdx, in, kLdx, out, a.pp.Wp + a.pp.woff[a.shape.nl], a.pp.Wp + a.pp.boff[a.shape.nl],
                      a.pp.K[a.shape.nl]);
     head = in;

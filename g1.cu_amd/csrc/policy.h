@@ -1,6 +1,6 @@
 // policy.h -- observation, frozen normalisation, policy MLP on fp32 MFMA, Gaussian sampling.
 //
-// One workgroup (4 waves) owns a tile of 32 worlds. Activations live in LDS ([32][K] row-major,
+// One workgroup (8 waves) owns a tile of 32 worlds. Activations live in LDS ([32][K] row-major,
 // padded); each dense layer is a [32 x K] . [K x N] contraction on v_mfma_f32_32x32x2f32 with the
 // weights pre-packed k-pair-major (Wp[k/2][n][k%2]) so every B-operand load is one contiguous
 // 256-byte line. Waves take 32-column output tiles round-robin. The mu (29) and value (1) heads are
@@ -18,7 +18,8 @@ namespace g1k {
 
 constexpr int kObs = 100, kAct = 29;
 constexpr int kTileWorlds = 32;
-constexpr int kPolicyThreads = 256;
+constexpr int kPolicyThreads = 512;
+constexpr int kPolicyWaves = kPolicyThreads / 64;
 constexpr int kMaxHidden = 512;
 constexpr int kMaxLayers = 4;
 
@@ -97,13 +98,13 @@ __device__ __forceinline__ float rng_pm1(unsigned long long seed, int w, unsigne
 
 // ---------------------------------------------------------------- one dense layer on MFMA
 // out[m][n] = act(sum_k in[m][k] W[n][k] + b[n]) for the 32 worlds of the tile.
-// in: LDS [32][ldi], out: LDS [32][ldo]; wave wv takes n-tiles wv, wv+4, ...
+// in: LDS [32][ldi], out: LDS [32][ldo]; wave wv takes n-tiles wv, wv + kPolicyWaves, ...
 __device__ __forceinline__ void mfma_layer(const float* __restrict__ in, int ldi, float* __restrict__ out, int ldo,
                                            const float* __restrict__ Wp, const float* __restrict__ bias, int K,
                                            int Np, int act, bool apply_act) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int mrow = lane & 31, khalf = lane >> 5;
-  for (int nt = wv; nt < Np / 32; nt += 4) {
+  for (int nt = wv; nt < Np / 32; nt += kPolicyWaves) {
     const int n0 = nt * 32;
     const float bv = bias[n0 + mrow];
     f32x16 acc;
@@ -136,9 +137,10 @@ __device__ __forceinline__ void mfma_layer(const float* __restrict__ in, int ldi
   }
 }
 
-// The fused 32-wide head has a single output tile: its K range is split over the 4 waves and the
-// partial tiles are summed through LDS (scratch: 4 x 32 x 32 floats, not aliasing `in`; `out` may
-// alias `in`: every wave has finished reading `in` at the barrier before the sum is written).
+// The fused 32-wide head has a single output tile: its K range is split over the waves and the
+// partial tiles are summed through LDS in wave order (scratch: kPolicyWaves x 32 x 32 floats, not
+// aliasing `in`; `out` may alias `in`: every wave has finished reading `in` at the barrier before
+// the sum is written).
 __device__ __forceinline__ void mfma_head_splitk(const float* in, int ldi, float* out, int ldo,
                                                  float* __restrict__ scratch, const float* __restrict__ Wp,
                                                  const float* __restrict__ bias, int K) {
@@ -146,7 +148,7 @@ __device__ __forceinline__ void mfma_head_splitk(const float* in, int ldi, float
   const int mrow = lane & 31, khalf = lane >> 5;
   constexpr int Np = 32;
   const int K2 = K / 2;
-  const int q = (K2 + 3) / 4;
+  const int q = (K2 + kPolicyWaves - 1) / kPolicyWaves;
   const int k0 = wv * q, k1 = min(K2, k0 + q);
   f32x16 acc;
   const float bv = wv == 0 ? bias[mrow] : 0.f;
@@ -173,10 +175,12 @@ __device__ __forceinline__ void mfma_head_splitk(const float* in, int ldi, float
     scratch[(wv * 32 + m) * 32 + mrow] = acc[i];
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 32 * 32; idx += 256) {
+  for (int idx = threadIdx.x; idx < 32 * 32; idx += kPolicyThreads) {
     const int m = idx >> 5, n = idx & 31;
-    out[m * ldo + n] = ((scratch[m * 32 + n] + scratch[(32 + m) * 32 + n]) + scratch[(64 + m) * 32 + n]) +
-                       scratch[(96 + m) * 32 + n];
+    float v = scratch[m * 32 + n];
+#pragma unroll
+    for (int w = 1; w < kPolicyWaves; ++w) v = v + scratch[(32 * w + m) * 32 + n];
+    out[m * ldo + n] = v;
   }
 }
 
