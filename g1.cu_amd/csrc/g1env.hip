@@ -307,7 +307,28 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
                a.pp.K[a.shape.nl], 32, 0, false);
   }
   __syncthreads();
-  // ---- sampling + log-prob, one thread per world, actions in order (reference: src/g1_env.cu:308-318)
+  // ---- sampling + log-prob (reference: src/g1_env.cu:308-318): one thread per (world, action)
+  // draws the noise and writes the action; each world's log-prob terms are then summed by one
+  // thread in action order (the terms go through the free activation buffer)
+  float* lpt = (head == in) ? out : in;   // [32][kAct] log-prob terms
+  const bool sample = !a.mu_out && a.t < a.H;
+  if (sample) {
+    const float LOG2PI = 1.8378770664093453f;
+    for (int idx = tid; idx < kTileWorlds * kAct; idx += kPolicyThreads) {
+      const int m = idx / kAct, i = idx - m * kAct;
+      const int w = w0 + m;
+      if (w < a.N) {
+        const float* h = head + m * kLdx;
+        const float ls = a.pp.log_std[i];
+        const float sd = expf(ls);
+        const long ab = ((long)a.t * a.N + w) * kAct;
+        const float nz = a.act_noise ? a.act_noise[ab + i] : rng_normal(a.seed, w, a.rng[w], kStreamAction, i);
+        a.A[ab + i] = h[i] + sd * nz;
+        lpt[m * kAct + i] = -0.5f * nz * nz - ls - 0.5f * LOG2PI;
+      }
+    }
+    __syncthreads();
+  }
   if (tid < kTileWorlds) {
     const int w = w0 + tid;
     if (w < a.N) {
@@ -319,16 +340,8 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
       } else if (a.t == a.H) {
         a.Vlast[w] = val;
       } else {
-        const float LOG2PI = 1.8378770664093453f;
         float lpsum = 0.f;
-        const long ab = ((long)a.t * a.N + w) * kAct;
-        for (int i = 0; i < kAct; ++i) {
-          const float ls = a.pp.log_std[i];
-          const float sd = expf(ls);
-          const float nz = a.act_noise ? a.act_noise[ab + i] : rng_normal(a.seed, w, a.rng[w], kStreamAction, i);
-          a.A[ab + i] = h[i] + sd * nz;
-          lpsum += -0.5f * nz * nz - ls - 0.5f * LOG2PI;
-        }
+        for (int i = 0; i < kAct; ++i) lpsum += lpt[tid * kAct + i];
         a.LP[(long)a.t * a.N + w] = lpsum;
         a.V[(long)a.t * a.N + w] = val;
       }
