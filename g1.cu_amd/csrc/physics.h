@@ -581,10 +581,12 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
       Sd[j] = Sn[j];
-      float v = In[j], q = 0.f;
-      if (junction) { v = v + gD[j]; q = q + gc[j]; }
+      // the bias force accumulates the children's terms from the first one (no 0 + x: a sum that
+      // starts at the first term differs from 0 + ... only in the sign of an exact zero)
+      float v = In[j];
+      if (junction) v = v + gD[j];
       IAr[j] = leaf ? v : v + Dlr[j];
-      pA[j] = leaf ? q : q + cs[j];
+      pA[j] = leaf ? 0.f : (junction ? gc[j] + cs[j] : cs[j]);
     }
     const float Fb[6] = {chain_bcast<0>(F), chain_bcast<1>(F), chain_bcast<2>(F),
                          chain_bcast<3>(F), chain_bcast<4>(F), chain_bcast<5>(F)};
@@ -660,7 +662,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const float d14 = gshfl(Dlr[j], 16 + rowc), d8 = gshfl(Dlr[j], 8 + rowc);
       const float c14 = gshfl(cs[j], 16 + rowc), c8 = gshfl(cs[j], 8 + rowc);
       I1[j] = ((I6[1 * 21 + symidx(rowc, j)] + d14) + d8) + Dlr[j];
-      pAs[j] = ((0.f + c14) + c8) + cs[j];
+      pAs[j] = (c14 + c8) + cs[j];
     }
     if (l < 6) {
 #pragma unroll
@@ -745,7 +747,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       float a = 0.f;
 #pragma unroll
       for (int k = 0; k < 6; ++k) a = fmaf_(s.u.fac.S[k][i], qdd[k], a);
-      a6[i] = 0.f + a;
+      a6[i] = a;
     }
   }
   // ---------------- smooth solve root -> leaf (reference: src/aba_factor.cuh:156-164)
@@ -867,7 +869,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       for (int k = 0; k < 6; ++k) {
         const float c = fmaf_(Ub[k], ud, pb[k]);
         if (body_parent[b] == 1) croot[k] = c;
-        else car[k] = 0.f + c;
+        else car[k] = c;
       }
       G1_PIN6(car);
       __asm__ volatile("" : "+v"(u[b]));
@@ -879,7 +881,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
     float p1[6];
 #pragma unroll
-    for (int k = 0; k < 6; ++k) p1[k] = (0.f + c8[k]) + c2[k];
+    for (int k = 0; k < 6; ++k) p1[k] = c8[k] + c2[k];
     // free joint: D qdd = x_base - S_base.pA_1 with D = L L'
     float qdd[6];
     {
@@ -910,7 +912,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       float a = 0.f;
 #pragma unroll
       for (int k = 0; k < 6; ++k) a = fmaf_(s.u.fac.S[k][i], qdd[k], a);
-      a1[i] = 0.f + a;
+      a1[i] = a;
     }
     if (wr) {
 #pragma unroll

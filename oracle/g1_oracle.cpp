@@ -367,15 +367,22 @@ template <class R> void factorize(const Frames<R>& F, const R* S, const R* Bdiag
 }
 
 // y = (M + dt B)^-1 x, single right-hand side (reference: src/aba_factor.cuh:121-165)
+// The parent's bias force pA starts at its first (highest-index) child's term instead of 0 + that
+// term: the two differ only in the sign of an exact zero, which nothing downstream observes.
 template <class R> void solveM(const Factor<R>& fac, const R* S, const R* x, R* y) {
   R pA[kNBody * 6], a6[kNBody * 6];
+  bool started[kNBody] = {};
   for (int i = 0; i < kNBody * 6; ++i) pA[i] = 0;
   for (int b = kNBody - 1; b >= 2; --b) {
     int par = body_parent[b], d = body_dofadr[b];
     const R* U = &fac.U[b * 6];
     R u = x[d] - dot6(&S[d * 6], &pA[b * 6]);
     R ud = u * fac.invD[b];
-    for (int k = 0; k < 6; ++k) pA[par * 6 + k] += fma_(U[k], ud, pA[b * 6 + k]);
+    for (int k = 0; k < 6; ++k) {
+      const R c = fma_(U[k], ud, pA[b * 6 + k]);
+      pA[par * 6 + k] = started[par] ? pA[par * 6 + k] + c : c;
+    }
+    started[par] = true;
   }
   {
     int d = body_dofadr[1];
@@ -403,7 +410,7 @@ template <class R> void solveM(const Factor<R>& fac, const R* S, const R* x, R* 
     for (int i = 0; i < 6; ++i) {
       R Sq = 0;
       for (int k = 0; k < 6; ++k) Sq = fma_(S[(d + k) * 6 + i], qdd[k], Sq);
-      a6[6 + i] = ap[i] + Sq;
+      a6[6 + i] = Sq;   // ap = 0 (no 0 + x)
     }
   }
   for (int b = 2; b < kNBody; ++b) {
