@@ -45,37 +45,114 @@ struct PhysArgs {
   float* obs;                      // [N][100] observation after the last control step, or null
   unsigned long long seed;
   unsigned long long* ncon_hist;   // [9] or null
+  // work queue (k_physics below)
+  unsigned* flags;                 // [pairs] chunks completed per world pair since the env was created
+  unsigned fbase;                  // value every flag holds when this launch starts
+  unsigned* qctr;                  // [2][kQueues] claim counters: this launch counts on row qpar and
+  int qpar;                        //   clears row qpar ^ 1 for the next launch
+  float* acc;                      // [N][32] per-lane energy sums of a control step split over items
+  float* vxs;                      // [N] base x-velocity sum of a control step split over items
+  int* qerr;                       // 1: a dependency wait exceeded kSpinLimit polls; 2: a wave of
+                                   //   queue q ran outside XCD q while xlocal is set
+  int xlocal;                      // queue q's waves all run on XCD q (checked at env creation)
 };
 
 constexpr int kPhysThreads = 64;   // one wave64 = two 32-lane world groups
+constexpr int kQueues = 8;         // one work queue per XCD of the MI355X
+constexpr unsigned kSpinLimit = 1u << 22;
 
+// Substeps per work item: uniform chunks of kChunk (the last one shorter when S is not a multiple).
+// Measured at config 3 (N = 8192, S = 10): chunks of 2 beat 1, 3, 5 and 10, and a 4-3-2-1 schedule.
+constexpr int kChunk = 2;
+__host__ __device__ inline int chunk_count(int S) { return (S + kChunk - 1) / kChunk; }
+__host__ __device__ inline int chunk_start(int c) { return c * kChunk; }
+
+__device__ __forceinline__ int xcc_id() { return (int)__builtin_amdgcn_s_getreg(20 | (0 << 6) | ((4 - 1) << 11)); }
+
+// A value stored by another wave earlier in this launch: read from the L2, bypassing this CU's L1
+// (an agent-scope load), so a line cached by an earlier item on this CU is never used.
+template <class T>
+__device__ __forceinline__ T ld_l2(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One physics launch advances every world pair (the two 32-lane groups of a wave64) by K control
+// steps of S substeps: PD torques, world_qacc, Euler, then the control step's reward, termination
+// and auto-reset (reference: src/g1_env.cu:118-212, the k_rollout substep loop :319-325).
+//
+// The work is cut into items (world pair, chunk of substeps of one control step) that
+// persistent waves claim from a queue, instead of one block per pair for the whole launch: a pair
+// with contacts costs 2-3x a contact-free one, which contact state one control step earlier does
+// not predict, and with whole-launch blocks the heavy blocks dispatched last keep a few SIMDs busy
+// long after the rest have drained. Items are claimed in chunk-major order, so every pair advances
+// about equally and the launch ends within about one item of its average.
+//
+// Queue q serves the pairs p = q (mod 8) and is claimed by the blocks with blockIdx = q (mod 8).
+// Item (p, j) needs item (p, j - 1), which was claimed earlier from the same queue by a wave that
+// is running, so a wait always ends; the pair's flag counts its completed items. A wait that
+// exceeds kSpinLimit polls sets qerr and continues rather than spin on.
+// Hand-over of a pair's state between items: the hardware places blocks on the 8 XCDs
+// round-robin, so all waves of queue q share XCD q's L2 (xlocal, verified when the env is created
+// and re-checked by every wave). The L2 is then the coherence point: the producer waits for its
+// stores to be acknowledged by the L2 before it moves the flag, and the consumer reads the flag and
+// the state from the L2 past its L1. Without xlocal the hand-over uses agent-scope release/acquire
+// fences, which also write back and invalidate the L2 (correct on any placement, much slower).
 __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
   __shared__ WorldLds lds[2];
   const int g = group_id(), l = group_lane();
-  const int w = blockIdx.x * 2 + g;
-  const bool wvalid = w < a.N;
-  const int wc = wvalid ? w : a.N - 1;
   WorldLds& s = lds[g];
   const LaneModel L = lane_model(l);
-
-  LaneState st;
-  const float* gq = a.qp + (long)wc * kNQ;
-  const float* gv = a.qv + (long)wc * kNV;
-#pragma unroll
-  for (int k = 0; k < 7; ++k) st.bq[k] = gq[k];
-#pragma unroll
-  for (int k = 0; k < 6; ++k) st.bqd[k] = gv[k];
-  st.jq = L.hinge ? gq[L.b + 5] : 0.f;
-  st.jqd = L.hinge ? gv[L.b + 4] : 0.f;
+  const int q = blockIdx.x % kQueues;
+  if (blockIdx.x == 0 && threadIdx.x < kQueues) a.qctr[(a.qpar ^ 1) * kQueues + threadIdx.x] = 0u;
+  const int npairs = (a.N + 1) >> 1;
+  const unsigned nq = npairs > q ? (unsigned)((npairs - q + kQueues - 1) / kQueues) : 0u;
+  const int nch = chunk_count(a.S);
+  const unsigned nitems = nq * (unsigned)(a.K * nch);
+  unsigned* const ctr = a.qctr + a.qpar * kQueues + q;
   const int ai = L.hinge ? L.b - 2 : 0;
-  float pa = L.hinge ? a.pa[(long)wc * kAct + ai] : 0.f;
-  int step = a.steps[wc];
-  unsigned rng = a.rng[wc];
   const SolveParams P{a.pgs, a.mu, true, true};
   unsigned hcnt = 0;   // lane q < 9 counts substeps with q contacts
+  if (a.xlocal && threadIdx.x == 0 && xcc_id() != q)
+    __hip_atomic_store(a.qerr, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
 #pragma unroll 1
-  for (int k = 0; k < a.K; ++k) {
+  for (;;) {
+    unsigned mine = 0;
+    if (threadIdx.x == 0) mine = atomicAdd(ctr, 1u);
+    const unsigned it = __builtin_amdgcn_readfirstlane(mine);
+    if (it >= nitems) break;
+    const int j = (int)(it / nq);
+    const int p = q + kQueues * (int)(it - (unsigned)j * nq);
+    const int k = j / nch, c = j - k * nch;
+    if (j > 0) {
+      const unsigned want = a.fbase + (unsigned)j;
+      unsigned spins = 0;
+#pragma unroll 1
+      for (;;) {
+        const unsigned f = __builtin_amdgcn_readfirstlane(ld_l2(a.flags + p));
+        if ((int)(f - want) >= 0) break;
+        if (++spins > kSpinLimit) {
+          if (threadIdx.x == 0) __hip_atomic_store(a.qerr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (a.xlocal) __asm__ volatile("" ::: "memory");
+      else __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    const int w = 2 * p + g;
+    const bool wvalid = w < a.N;
+    const int wc = wvalid ? w : a.N - 1;   // an odd N's last group repeats world N - 1 and stores nothing
+
+    LaneState st;
+    const float* gq = a.qp + (long)wc * kNQ;
+    const float* gv = a.qv + (long)wc * kNV;
+#pragma unroll
+    for (int m = 0; m < 7; ++m) st.bq[m] = ld_l2(gq + m);
+#pragma unroll
+    for (int m = 0; m < 6; ++m) st.bqd[m] = ld_l2(gv + m);
+    st.jq = L.hinge ? ld_l2(gq + L.b + 5) : 0.f;
+    st.jqd = L.hinge ? ld_l2(gv + L.b + 4) : 0.f;
     const int t = a.t0 + k * a.astep;
     const float act = L.hinge ? a.act[((long)t * a.N + wc) * kAct + ai] : 0.f;
     // PD target = clamp(stand + 0.5 a) (reference: src/g1_env.cu:123-130)
@@ -83,8 +160,13 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
     if (target < L.clo) target = L.clo;
     if (target > L.chi) target = L.chi;
     float vx_sum = 0.f, energy = 0.f;
+    if (c > 0) {
+      energy = ld_l2(a.acc + (long)wc * kGroup + l);
+      vx_sum = ld_l2(a.vxs + wc);
+    }
+    const int s0 = chunk_start(c), s1 = c + 1 < nch ? chunk_start(c + 1) : a.S;
 #pragma unroll 1
-    for (int sub = 0; sub < a.S; ++sub) {
+    for (int sub = s0; sub < s1; ++sub) {
       float jtau = 0.f;
       if (L.hinge) {
         float pdt = fmaf_(-L.kd, st.jqd, L.kp * (target - st.jq));
@@ -95,88 +177,110 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
       }
       float bqacc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, jqacc = 0.f;
       const int nc = world_qacc(l, s, st, jtau, P, bqacc, jqacc);
-      hcnt += (l == nc) ? 1u : 0u;
+      hcnt += (l == nc && wvalid) ? 1u : 0u;
       integrate_lane(L, st, bqacc, jqacc, true);
       vx_sum += st.bqd[0];
     }
-    // ---- reward / termination / auto-reset (reference: src/g1_env.cu:164-211), lane 1 decides
-    const float da = L.hinge ? act - pa : 0.f;
-    float act_pen = gsum(da * da);
-    const float energy_tot = gsum(energy);
-    int d_flag = 0;
-    float r = 0.f;
-    if (l == 1) {
-      const float vx = vx_sum / (float)a.S;
-      const float height = st.bq[2];
-      const float qw = st.bq[3], qx = st.bq[4], qy = st.bq[5];
-      const float up = fmaf_(-2.f, fmaf_(qy, qy, qx * qx), 1.f);   // quat2mat(q)[2][2]
-      const int alive = !(height < 0.45f || up < 0.5f);
-      (void)qw;
-      const float upc = up < 0.f ? 0.f : (up > 1.f ? 1.f : up);
-      float vx_c = vx > 0.8f ? 0.8f : vx;
-      if (vx_c < 0.f) vx_c = 0.f;
-      const float r_vel = 1.0f * vx_c * upc;
-      const float r_lat = -0.2f * fabsf(st.bqd[1]) - 0.05f * fabsf(st.bqd[5]);
-      const float r_up = 0.3f * upc;
-      const float r_h = -0.5f * fabsf(height - 0.78f);
-      if (act_pen > 10.f) act_pen = 10.f;
-      r = alive ? 1.0f + r_vel + r_lat + r_up + r_h - 0.005f * act_pen - 1e-4f * energy_tot : -5.0f;
-      const int won = alive && st.bq[0] >= 5.0f;
-      if (won) r += 50.0f;
-      d_flag = (!alive || won || step + 1 >= 1000) ? 1 : 0;
-    }
-    d_flag = gshfl(d_flag, 1);
-    step += 1;
-    pa = act;
-    if (d_flag) {
-      const float u = a.reset_noise ? a.reset_noise[((long)t * a.N + wc) * kAct + ai]
-                                    : rng_pm1(a.seed, wc, rng, kStreamReset, ai);
-      if (L.hinge) { st.jq = L.qstand + 0.05f * u; st.jqd = 0.f; pa = 0.f; }
+    if (c < nch - 1) {
+      if (wvalid) {
+        a.acc[(long)w * kGroup + l] = energy;
+        if (l == 1) a.vxs[w] = vx_sum;
+      }
+    } else {
+      // ---- reward / termination / auto-reset (reference: src/g1_env.cu:164-211), lane 1 decides
+      float pa = L.hinge ? ld_l2(a.pa + (long)wc * kAct + ai) : 0.f;
+      int step = ld_l2(a.steps + wc);
+      unsigned rng = ld_l2(a.rng + wc);
+      const float da = L.hinge ? act - pa : 0.f;
+      float act_pen = gsum(da * da);
+      const float energy_tot = gsum(energy);
+      int d_flag = 0;
+      float r = 0.f;
+      if (l == 1) {
+        const float vx = vx_sum / (float)a.S;
+        const float height = st.bq[2];
+        const float qx = st.bq[4], qy = st.bq[5];
+        const float up = fmaf_(-2.f, fmaf_(qy, qy, qx * qx), 1.f);   // quat2mat(q)[2][2]
+        const int alive = !(height < 0.45f || up < 0.5f);
+        const float upc = up < 0.f ? 0.f : (up > 1.f ? 1.f : up);
+        float vx_c = vx > 0.8f ? 0.8f : vx;
+        if (vx_c < 0.f) vx_c = 0.f;
+        const float r_vel = 1.0f * vx_c * upc;
+        const float r_lat = -0.2f * fabsf(st.bqd[1]) - 0.05f * fabsf(st.bqd[5]);
+        const float r_up = 0.3f * upc;
+        const float r_h = -0.5f * fabsf(height - 0.78f);
+        if (act_pen > 10.f) act_pen = 10.f;
+        r = alive ? 1.0f + r_vel + r_lat + r_up + r_h - 0.005f * act_pen - 1e-4f * energy_tot : -5.0f;
+        const int won = alive && st.bq[0] >= 5.0f;
+        if (won) r += 50.0f;
+        d_flag = (!alive || won || step + 1 >= 1000) ? 1 : 0;
+      }
+      d_flag = gshfl(d_flag, 1);
+      step += 1;
+      pa = act;
+      if (d_flag) {
+        const float u = a.reset_noise ? a.reset_noise[((long)t * a.N + wc) * kAct + ai]
+                                      : rng_pm1(a.seed, wc, rng, kStreamReset, ai);
+        if (L.hinge) { st.jq = L.qstand + 0.05f * u; st.jqd = 0.f; pa = 0.f; }
 #pragma unroll
-      for (int q = 0; q < 7; ++q) st.bq[q] = MF::qpos_stand[q];
+        for (int m = 0; m < 7; ++m) st.bq[m] = MF::qpos_stand[m];
 #pragma unroll
-      for (int q = 0; q < 6; ++q) st.bqd[q] = 0.f;
-      step = 0;
-    }
-    rng += 1;
-    if (wvalid && l == 1) {
-      const long o = (long)(a.t0 + k * a.rstep) * a.N + w;
-      a.R[o] = r;
-      a.D[o] = (float)d_flag;
-    }
-  }
-  if (wvalid) {
-    float* oq = a.qp + (long)w * kNQ;
-    float* ov = a.qv + (long)w * kNV;
-    if (l == 1) {
+        for (int m = 0; m < 6; ++m) st.bqd[m] = 0.f;
+        step = 0;
+      }
+      rng += 1;
+      if (wvalid) {
+        if (l == 1) {
+          const long o = (long)(a.t0 + k * a.rstep) * a.N + w;
+          a.R[o] = r;
+          a.D[o] = (float)d_flag;
+          a.steps[w] = step;
+          a.rng[w] = rng;
+        }
+        if (L.hinge) a.pa[(long)w * kAct + ai] = pa;
+        if (a.obs && k == a.K - 1) {
+          // observation of the final state, each lane writing its own entries (same values as k_obs)
+          float* o = a.obs + (long)w * kObs;
+          if (l == 1) {
 #pragma unroll
-      for (int q = 0; q < 7; ++q) oq[q] = st.bq[q];
-#pragma unroll
-      for (int q = 0; q < 6; ++q) ov[q] = st.bqd[q];
-      a.steps[w] = step;
-      a.rng[w] = rng;
+            for (int m = 0; m < 6; ++m) o[m] = st.bqd[m];
+            const float qw = st.bq[3], qx = st.bq[4], qy = st.bq[5], qz = st.bq[6];
+            o[6] = -(2.f * fmaf_(-qw, qy, qx * qz));
+            o[7] = -(2.f * fmaf_(qw, qx, qy * qz));
+            o[8] = -fmaf_(-2.f, fmaf_(qy, qy, qx * qx), 1.f);
+          }
+          if (L.hinge) { o[9 + ai] = st.jq; o[38 + ai] = st.jqd; o[67 + ai] = pa; }
+          if (l == 0) { o[96] = 0.8f; o[97] = 0.f; o[98] = 0.f; o[99] = 0.f; }
+        }
+      }
     }
-    if (L.hinge) {
-      oq[L.b + 5] = st.jq;
-      ov[L.b + 4] = st.jqd;
-      a.pa[(long)w * kAct + ai] = pa;
-    }
-    if (a.ncon_hist && l < 9 && hcnt) atomicAdd(&a.ncon_hist[l], (unsigned long long)hcnt);
-    if (a.obs) {
-      // observation of the final state, each lane writing its own entries (same values as k_obs)
-      float* o = a.obs + (long)w * kObs;
+    if (wvalid) {
+      float* oq = a.qp + (long)w * kNQ;
+      float* ov = a.qv + (long)w * kNV;
       if (l == 1) {
 #pragma unroll
-        for (int q = 0; q < 6; ++q) o[q] = st.bqd[q];
-        const float qw = st.bq[3], qx = st.bq[4], qy = st.bq[5], qz = st.bq[6];
-        o[6] = -(2.f * fmaf_(-qw, qy, qx * qz));
-        o[7] = -(2.f * fmaf_(qw, qx, qy * qz));
-        o[8] = -fmaf_(-2.f, fmaf_(qy, qy, qx * qx), 1.f);
+        for (int m = 0; m < 7; ++m) oq[m] = st.bq[m];
+#pragma unroll
+        for (int m = 0; m < 6; ++m) ov[m] = st.bqd[m];
       }
-      if (L.hinge) { o[9 + ai] = st.jq; o[38 + ai] = st.jqd; o[67 + ai] = pa; }
-      if (l == 0) { o[96] = 0.8f; o[97] = 0.f; o[98] = 0.f; o[99] = 0.f; }
+      if (L.hinge) {
+        oq[L.b + 5] = st.jq;
+        ov[L.b + 4] = st.jqd;
+      }
     }
+    __syncthreads();
+    // every store of the item is acknowledged before the pair's flag moves on
+    if (a.xlocal) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (threadIdx.x == 0)
+      __hip_atomic_store(a.flags + p, a.fbase + (unsigned)j + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  if (a.ncon_hist && l < 9 && hcnt) atomicAdd(&a.ncon_hist[l], (unsigned long long)hcnt);
+}
+
+// XCD of each block of a grid shaped like k_physics' (placement check of the work queue)
+__global__ void __launch_bounds__(kPhysThreads) k_xcc(int* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
 // ---- probes: the same world_qacc device code on caller-given states (parity harnesses)
@@ -458,6 +562,15 @@ struct EnvState {
   long Wp_cap;
   unsigned long long* ncon_hist;
   int hist_on;
+  // physics work queue (k_physics): per-pair item flags, claim counters, split-step accumulators
+  unsigned* qflags;
+  unsigned* qctr;
+  int* qerr;
+  float *qacc_e, *qacc_vx;
+  unsigned qdone;   // value of every pair flag after the launches enqueued so far
+  int qpar;         // counter row of the next launch
+  int pgrid;        // persistent grid: resident blocks of k_physics, a multiple of kQueues
+  int xlocal;       // blocks land on XCD blockIdx % kQueues (measured at creation)
   // per-launch HIP events of the rollout's physics / policy kernels (null stream)
   int prof_on;
   std::vector<hipEvent_t> ev_phys, ev_pol;
@@ -558,12 +671,32 @@ static PhysArgs phys_args(EnvState* E) {
   a.qp = E->qp; a.qv = E->qv; a.pa = E->pa; a.steps = E->steps; a.rng = E->rng;
   a.N = E->N; a.S = E->S; a.pgs = E->pgs; a.K = 1; a.mu = E->mu; a.seed = E->seed;
   a.ncon_hist = E->hist_on ? E->ncon_hist : nullptr;
+  a.flags = E->qflags; a.qctr = E->qctr; a.acc = E->qacc_e; a.vxs = E->qacc_vx; a.qerr = E->qerr;
   return a;
 }
 
-static void launch_physics(const PhysArgs& a) {
-  hipLaunchKernelGGL(k_physics, dim3((a.N + 1) / 2), dim3(kPhysThreads), 0, 0, a);
+// Enqueue one physics launch on the null stream; the queue state (flag base, counter row) advances
+// on the host in launch order, which is the stream's execution order.
+static void launch_physics(EnvState* E, PhysArgs& a) {
+  if (a.K <= 0) fail("physics launch: K must be positive");
+  const int nch = chunk_count(a.S);
+  const long per_pair = (long)a.K * nch;
+  if (per_pair > (1L << 30)) fail("physics launch: too many work items per pair");
+  a.fbase = E->qdone;
+  a.qpar = E->qpar;
+  a.xlocal = E->xlocal;
+  hipLaunchKernelGGL(k_physics, dim3((unsigned)E->pgrid), dim3(kPhysThreads), 0, 0, a);
   HIPCHECK(hipGetLastError());
+  E->qdone += (unsigned)per_pair;
+  E->qpar ^= 1;
+}
+
+// nonzero if a physics launch saw a dependency wait exceed its bound (results then undefined)
+static void check_queue(EnvState* E) {
+  int err = 0;
+  HIPCHECK(hipMemcpy(&err, E->qerr, sizeof(int), hipMemcpyDeviceToHost));
+  if (err == 1) fail("physics work queue: a dependency wait exceeded its bound");
+  if (err) fail("physics work queue: a block ran outside the XCD its queue was placed on");
 }
 
 static void rollout_impl(EnvState* E, int H, const float* W, const float* mean, const float* var, float* O, float* A,
@@ -580,7 +713,7 @@ static void rollout_impl(EnvState* E, int H, const float* W, const float* mean, 
     launch_policy(E, pp, t, H, mean, var, act_noise, O, A, LP, V, Vlast);
     if (prof) { prof_mark(E->ev_pol, E->n_pol); prof_mark(E->ev_phys, E->n_phys); }
     pa.t0 = t;
-    launch_physics(pa);
+    launch_physics(E, pa);
     if (prof) prof_mark(E->ev_phys, E->n_phys);
   }
   if (prof) prof_mark(E->ev_pol, E->n_pol);
@@ -608,6 +741,39 @@ void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
   HIPCHECK(hipMalloc(&E->bench_r, (size_t)N * 4));
   HIPCHECK(hipMalloc(&E->bench_d, (size_t)N * 4));
   HIPCHECK(hipMalloc(&E->ncon_hist, 9 * sizeof(unsigned long long)));
+  const int npairs = (N + 1) / 2;
+  HIPCHECK(hipMalloc(&E->qflags, (size_t)npairs * sizeof(unsigned)));
+  HIPCHECK(hipMalloc(&E->qctr, 2 * kQueues * sizeof(unsigned)));
+  HIPCHECK(hipMalloc(&E->qerr, sizeof(int)));
+  HIPCHECK(hipMalloc(&E->qacc_e, (size_t)N * kGroup * 4));
+  HIPCHECK(hipMalloc(&E->qacc_vx, (size_t)N * 4));
+  HIPCHECK(hipMemset(E->qflags, 0, (size_t)npairs * sizeof(unsigned)));
+  HIPCHECK(hipMemset(E->qctr, 0, 2 * kQueues * sizeof(unsigned)));
+  HIPCHECK(hipMemset(E->qerr, 0, sizeof(int)));
+  E->qdone = 0; E->qpar = 0;
+  {
+    // persistent grid: every resident block of k_physics, in whole rounds of the kQueues queues,
+    // and no more blocks than there are pairs (rounded up to the queues)
+    int dev = 0, cus = 0, per_cu = 0;
+    HIPCHECK(hipGetDevice(&dev));
+    HIPCHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    HIPCHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_physics, kPhysThreads, 0));
+    int cap = (cus * (per_cu > 0 ? per_cu : 1)) / kQueues * kQueues;
+    if (cap < kQueues) cap = kQueues;
+    const int need = (npairs + kQueues - 1) / kQueues * kQueues;
+    E->pgrid = need < cap ? need : cap;
+    // placement of the blocks on the XCDs: round-robin lets each queue hand over state in one L2
+    int* dx = nullptr;
+    HIPCHECK(hipMalloc(&dx, (size_t)E->pgrid * sizeof(int)));
+    hipLaunchKernelGGL(k_xcc, dim3((unsigned)E->pgrid), dim3(kPhysThreads), 0, 0, dx);
+    HIPCHECK(hipGetLastError());
+    std::vector<int> hx(E->pgrid);
+    HIPCHECK(hipMemcpy(hx.data(), dx, (size_t)E->pgrid * sizeof(int), hipMemcpyDeviceToHost));
+    HIPCHECK(hipFree(dx));
+    E->xlocal = 1;
+    for (int b = 0; b < E->pgrid; ++b)
+      if (hx[b] != b % kQueues) E->xlocal = 0;
+  }
   HIPCHECK(hipMalloc(&E->dout, (size_t)N * (kObs + 2) * 4));
   HIPCHECK(hipHostMalloc((void**)&E->h_act, (size_t)N * kAct * 4, hipHostMallocDefault));
   HIPCHECK(hipHostMalloc((void**)&E->h_out, (size_t)N * (kObs + 2) * 4, hipHostMallocDefault));
@@ -627,8 +793,9 @@ void g1_env_destroy(void* h) {
   EnvState* E = (EnvState*)h;
   if (!E) return;
   HIPCHECK(hipDeviceSynchronize());
-  void* bufs[] = {E->qp, E->qv, E->pa, E->steps, E->rng, E->dact,
-                  E->zero_act, E->bench_r, E->bench_d, E->ncon_hist, E->Wp, E->dout};
+  void* bufs[] = {E->qp,       E->qv,      E->pa,        E->steps,   E->rng,  E->dact,
+                  E->zero_act, E->bench_r, E->bench_d,   E->ncon_hist, E->Wp,  E->dout,
+                  E->qflags,   E->qctr,    E->qerr,      E->qacc_e,  E->qacc_vx};
   for (void* b : bufs)
     if (b) HIPCHECK(hipFree(b));
   if (E->h_act) HIPCHECK(hipHostFree(E->h_act));
@@ -662,9 +829,10 @@ void g1_env_step(void* h, const float* act, float* obs, float* rew, float* done)
   PhysArgs pa = phys_args(E);
   pa.act = E->dact; pa.t0 = 0; pa.astep = 0; pa.rstep = 0;
   pa.obs = E->dout; pa.R = E->dout + (size_t)N * kObs; pa.D = E->dout + (size_t)N * (kObs + 1);
-  launch_physics(pa);
+  launch_physics(E, pa);
   HIPCHECK(hipMemcpyAsync(E->h_out, E->dout, (size_t)N * (kObs + 2) * 4, hipMemcpyDeviceToHost, 0));
   HIPCHECK(hipStreamSynchronize(0));
+  check_queue(E);
   std::memcpy(obs, E->h_out, (size_t)N * kObs * 4);
   std::memcpy(rew, E->h_out + (size_t)N * kObs, (size_t)N * 4);
   std::memcpy(done, E->h_out + (size_t)N * (kObs + 1), (size_t)N * 4);
@@ -684,18 +852,21 @@ void g1_env_bench_phys(void* h, int K) {
   EnvState* E = (EnvState*)h;
   PhysArgs pa = phys_args(E);
   pa.K = K; pa.act = E->zero_act; pa.t0 = 0; pa.astep = 0; pa.rstep = 0; pa.R = E->bench_r; pa.D = E->bench_d;
-  launch_physics(pa);
+  launch_physics(E, pa);
   HIPCHECK(hipDeviceSynchronize());
+  check_queue(E);
 }
 
 void g1_env_qpos(void* h, float* out) {
   EnvState* E = (EnvState*)h;
   HIPCHECK(hipMemcpy(out, E->qp, (size_t)kNQ * 4, hipMemcpyDeviceToHost));
+  check_queue(E);
 }
 
 void g1_env_qpos_all(void* h, float* out) {
   EnvState* E = (EnvState*)h;
   HIPCHECK(hipMemcpy(out, E->qp, (size_t)E->N * kNQ * 4, hipMemcpyDeviceToHost));
+  check_queue(E);
 }
 
 void g1_occupancy_report(void) {
@@ -736,6 +907,7 @@ void g1_env_get_state(void* h, float* qp, float* qv, float* pa, int* steps) {
   HIPCHECK(hipMemcpy(qv, E->qv, N * kNV * 4, hipMemcpyDeviceToHost));
   HIPCHECK(hipMemcpy(pa, E->pa, N * kAct * 4, hipMemcpyDeviceToHost));
   HIPCHECK(hipMemcpy(steps, E->steps, N * 4, hipMemcpyDeviceToHost));
+  check_queue(E);
 }
 
 int g1_env_set_policy(void* h, int nlayers, const int* hidden, int activation) {
@@ -768,6 +940,7 @@ void g1_env_set_contact(void* h, float mu, int pgs_iters) {
 void g1_env_ncon_hist(void* h, int enable, unsigned long long* out9) {
   EnvState* E = (EnvState*)h;
   if (out9) HIPCHECK(hipMemcpy(out9, E->ncon_hist, 9 * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+  check_queue(E);
   HIPCHECK(hipMemset(E->ncon_hist, 0, 9 * sizeof(unsigned long long)));
   E->hist_on = enable;
 }
@@ -781,6 +954,7 @@ void g1_env_profile(void* h, int enable) {
 void g1_env_profile_read(void* h, double* out4) {
   EnvState* E = (EnvState*)h;
   HIPCHECK(hipDeviceSynchronize());
+  check_queue(E);
   double tp = 0.0, tq = 0.0;
   for (size_t i = 0; i + 1 < E->n_phys; i += 2) {
     float ms = 0.f;

@@ -155,6 +155,70 @@ def test_host_step_matches_oracle(g1, orc):
     assert relerr_rows(obs1[live], orc.obs(oq, ov, opa)[live]).max() <= 1e-4
 
 
+def test_work_queue_matches_small_launch(g1):
+    """The physics work queue at scale: a rollout over 8193 worlds (many work items per wave, state
+    handed between waves, an odd last pair) gives each of its first 97 worlds bit for bit the
+    trajectory those worlds get in a 97-world launch (world 96 then has no partner)."""
+    H, N, n = 3, 8193, 97
+    qp, qv, pa, steps, W, mean, var, an, rn = _setup(N, H, 21)
+    env = g1.G1Env(N, substeps=10, pgs_iters=8, seed=1)
+    env.set_state(qp, qv, pa, steps)
+    big = _run(g1, env, W, mean, var, H, N, an, rn)
+    big_state = env.get_state()
+    env.close()
+    env = g1.G1Env(n, substeps=10, pgs_iters=8, seed=1)
+    env.set_state(qp[:n], qv[:n], pa[:n], steps[:n])
+    small = _run(g1, env, W, mean, var, H, n, np.ascontiguousarray(an[:, :n]), np.ascontiguousarray(rn[:, :n]))
+    small_state = env.get_state()
+    env.close()
+    for b, s in zip(big[:6], small[:6]):
+        assert np.array_equal(b[:, :n], s)
+    assert np.array_equal(big[6][:n], small[6])
+    for b, s in zip(big_state, small_state):
+        assert np.array_equal(b[:n], s)
+    assert not np.array_equal(big_state[0], qp)   # the worlds moved
+
+
+def test_work_queue_split_control_steps(g1):
+    """K control steps in one launch equal K one-step launches bit for bit (the queue's items then
+    span control steps), with S = 5 substeps (items of 2, 2 and 1 substeps) and an odd world count."""
+    import configs
+    N, S, K = 301, 5, 3
+    qp, qv, pa, steps = configs.reset_states(np.random.default_rng(5), N)
+    states = []
+    for split in (False, True):
+        env = g1.G1Env(N, substeps=S, pgs_iters=8, seed=2)
+        env.set_state(qp, qv, pa, steps)
+        if split:
+            for _ in range(K):
+                g1._lib.g1_env_bench_phys(env.h, 1)
+        else:
+            g1._lib.g1_env_bench_phys(env.h, K)
+        states.append(env.get_state())
+        env.close()
+    for a, b in zip(*states):
+        assert np.array_equal(a, b)
+    assert not np.array_equal(states[0][0], qp)
+
+
+def test_host_step_five_substeps_matches_oracle(g1, orc):
+    """g1_env_step with S = 5 (a control step split into work items of 2, 2 and 1 substeps, its
+    reward sums carried between items) against the oracle's control step."""
+    N, S = 129, 5
+    env = g1.G1Env(N, substeps=S, pgs_iters=8, seed=3)
+    env.reset()
+    qp, qv, pa, st = env.get_state()
+    act = np.random.default_rng(6).normal(0, 0.3, (N, 29)).astype(np.float32)
+    obs1, rew, done = env.step(act)
+    env.close()
+    oq, ov, opa, ost = qp.copy(), qv.copy(), pa.copy(), st.copy()
+    rr, dd = orc.env_advance(oq, ov, opa, ost, act, np.zeros((N, 29), np.float32), S=S, threads=8)
+    live = dd == 0
+    assert np.array_equal(done, dd)
+    assert np.abs(rew[live] - rr[live]).max() <= 1e-4
+    assert relerr_rows(obs1[live], orc.obs(oq, ov, opa)[live]).max() <= 1e-4
+
+
 def test_reference_trained_policy_walks(g1):
     """End-to-end check of observation, action, physics and reward semantics: the reference's
     trained checkpoint (converted, g1.cu_amd/data) driven through g1_rollout walks forward at about
