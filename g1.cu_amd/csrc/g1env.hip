@@ -58,14 +58,20 @@ struct PhysArgs {
 };
 
 constexpr int kPhysThreads = 64;   // one wave64 = two 32-lane world groups
-constexpr int kQueues = 8;         // one work queue per XCD of the MI355X
+constexpr int kXcds = 8;           // XCDs of the MI355X
+constexpr int kQueues = 32;        // work queues, kQueues / kXcds per XCD (spreads the claim atomics)
 constexpr unsigned kSpinLimit = 1u << 22;
 
-// Substeps per work item: uniform chunks of kChunk (the last one shorter when S is not a multiple).
-// Measured at config 3 (N = 8192, S = 10): chunks of 2 beat 1, 3, 5 and 10, and a 4-3-2-1 schedule.
-constexpr int kChunk = 2;
-__host__ __device__ inline int chunk_count(int S) { return (S + kChunk - 1) / kChunk; }
-__host__ __device__ inline int chunk_start(int c) { return c * kChunk; }
+// Substep chunks of a control step (the work items of one pair): pairs of substeps, except that
+// the last two substeps are single items (S = 10: 2, 2, 2, 2, 1, 1). Short last items shorten the
+// launch's tail; two-substep items amortise the hand-over of a pair's state. Measured at config 3
+// (N = 8192, S = 10) against uniform chunks of 1, 2, 3, 5 and 10 substeps and a 4-3-2-1 schedule.
+__host__ __device__ inline int front_pairs(int S) { return S > 2 ? (S - 2) / 2 : 0; }
+__host__ __device__ inline int chunk_count(int S) { return S - front_pairs(S); }
+__host__ __device__ inline int chunk_start(int S, int c) {
+  const int f = front_pairs(S);
+  return c <= f ? 2 * c : f + c;
+}
 
 __device__ __forceinline__ int xcc_id() { return (int)__builtin_amdgcn_s_getreg(20 | (0 << 6) | ((4 - 1) << 11)); }
 
@@ -87,13 +93,13 @@ __device__ __forceinline__ T ld_l2(const T* p) {
 // long after the rest have drained. Items are claimed in chunk-major order, so every pair advances
 // about equally and the launch ends within about one item of its average.
 //
-// Queue q serves the pairs p = q (mod 8) and is claimed by the blocks with blockIdx = q (mod 8).
+// Queue q serves the pairs p = q (mod 32) and is claimed by the blocks with blockIdx = q (mod 32).
 // Item (p, j) needs item (p, j - 1), which was claimed earlier from the same queue by a wave that
 // is running, so a wait always ends; the pair's flag counts its completed items. A wait that
 // exceeds kSpinLimit polls sets qerr and continues rather than spin on.
 // Hand-over of a pair's state between items: the hardware places blocks on the 8 XCDs
-// round-robin, so all waves of queue q share XCD q's L2 (xlocal, verified when the env is created
-// and re-checked by every wave). The L2 is then the coherence point: the producer waits for its
+// round-robin, so all waves of queue q share the L2 of XCD q mod 8 (xlocal, verified when the env
+// is created and re-checked by every wave). The L2 is then the coherence point: the producer waits for its
 // stores to be acknowledged by the L2 before it moves the flag, and the consumer reads the flag and
 // the state from the L2 past its L1. Without xlocal the hand-over uses agent-scope release/acquire
 // fences, which also write back and invalidate the L2 (correct on any placement, much slower).
@@ -112,7 +118,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
   const int ai = L.hinge ? L.b - 2 : 0;
   const SolveParams P{a.pgs, a.mu, true, true};
   unsigned hcnt = 0;   // lane q < 9 counts substeps with q contacts
-  if (a.xlocal && threadIdx.x == 0 && xcc_id() != q)
+  if (a.xlocal && threadIdx.x == 0 && xcc_id() != q % kXcds)
     __hip_atomic_store(a.qerr, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
 #pragma unroll 1
@@ -164,7 +170,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
       energy = ld_l2(a.acc + (long)wc * kGroup + l);
       vx_sum = ld_l2(a.vxs + wc);
     }
-    const int s0 = chunk_start(c), s1 = c + 1 < nch ? chunk_start(c + 1) : a.S;
+    const int s0 = chunk_start(a.S, c), s1 = c + 1 < nch ? chunk_start(a.S, c + 1) : a.S;
 #pragma unroll 1
     for (int sub = s0; sub < s1; ++sub) {
       float jtau = 0.f;
@@ -570,7 +576,7 @@ struct EnvState {
   unsigned qdone;   // value of every pair flag after the launches enqueued so far
   int qpar;         // counter row of the next launch
   int pgrid;        // persistent grid: resident blocks of k_physics, a multiple of kQueues
-  int xlocal;       // blocks land on XCD blockIdx % kQueues (measured at creation)
+  int xlocal;       // blocks land on XCD blockIdx % kXcds (measured at creation)
   // per-launch HIP events of the rollout's physics / policy kernels (null stream)
   int prof_on;
   std::vector<hipEvent_t> ev_phys, ev_pol;
@@ -772,7 +778,7 @@ void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
     HIPCHECK(hipFree(dx));
     E->xlocal = 1;
     for (int b = 0; b < E->pgrid; ++b)
-      if (hx[b] != b % kQueues) E->xlocal = 0;
+      if (hx[b] != b % kXcds) E->xlocal = 0;
   }
   HIPCHECK(hipMalloc(&E->dout, (size_t)N * (kObs + 2) * 4));
   HIPCHECK(hipHostMalloc((void**)&E->h_act, (size_t)N * kAct * 4, hipHostMallocDefault));
