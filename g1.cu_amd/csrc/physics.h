@@ -25,6 +25,7 @@
 
 #include "g1_model_tables.h"
 #include "lanes.h"
+#include "tree.h"
 
 namespace g1k {
 
@@ -297,27 +298,37 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   const LaneModel L = lane_model(l);
   const bool base = (l == 1);
 
-  // ---------------- forward kinematics (reference: src/dynamics.cuh:47-88)
-  // Hinge anchors sit at the body origin (jnt_pos == 0, generator-checked), so the reference's
-  // anchor shift pos = (pos + q*0) - q'*0 is the identity and is omitted.
+  // ---------------- forward kinematics (reference: src/dynamics.cuh:47-88) by ancestor doubling
+  // Each lane starts from its body's transform relative to its parent (hinge: translation
+  // body_pos, rotation body_quat (x) the joint rotation; pelvis: the free-joint pose), and round r
+  // composes it with the transform held by the 2^r-th ancestor, T <- T_anc o T, which leaves it
+  // relative to the 2^(r+1)-th ancestor; after kFkRounds rounds every body is in the world frame.
+  // The same per-body transforms as the reference's root -> leaf recursion, associated as a tree
+  // (4 rounds instead of 10 levels); the CPU oracle composes in the same association. Hinge
+  // anchors sit at the body origin (jnt_pos == 0, generator-checked), so the reference's anchor
+  // shift pos = (pos + q*0) - q'*0 is the identity and is omitted.
   V3 xp{0.f, 0.f, 0.f};
   Q4 xq{1.f, 0.f, 0.f, 0.f};
+  {
+    const float h = 0.5f * st.jq, sn = sin_rn(h);
+    const Q4 aa{cos_rn(h), L.axis.x * sn, L.axis.y * sn, L.axis.z * sn};
+    if (L.hinge) {
+      xp = L.bpos;
+      xq = qmul(L.bquat, aa);
+    }
+  }
   if (base) {
     xp = {st.bq[0], st.bq[1], st.bq[2]};
     xq = qnorm(Q4{st.bq[3], st.bq[4], st.bq[5], st.bq[6]});
   }
-  Q4 aa;
-  {
-    float h = 0.5f * st.jq, sn = sin_rn(h);
-    aa = {cos_rn(h), L.axis.x * sn, L.axis.y * sn, L.axis.z * sn};
-  }
 #pragma unroll
-  for (int r = 2; r <= kMaxDepth; ++r) {
-    Q4 qp{gshfl(xq.w, L.par), gshfl(xq.x, L.par), gshfl(xq.y, L.par), gshfl(xq.z, L.par)};
-    V3 pp{gshfl(xp.x, L.par), gshfl(xp.y, L.par), gshfl(xp.z, L.par)};
-    if (L.depth == r) {
-      xp = vadd(pp, qrot(qp, L.bpos));
-      xq = qmul(qmul(qp, L.bquat), aa);
+  for (int r = 0; r < kFkRounds; ++r) {
+    const int an = kAncestors.a[r][l];
+    const Q4 qa{gshfl(xq.w, an), gshfl(xq.x, an), gshfl(xq.y, an), gshfl(xq.z, an)};
+    const V3 pa{gshfl(xp.x, an), gshfl(xp.y, an), gshfl(xp.z, an)};
+    if (an > 0) {
+      xp = vadd(pa, qrot(qa, xp));
+      xq = qmul(qa, xq);
     }
   }
   const V3 xip = vadd(xp, qrot(xq, L.ipos));

@@ -27,6 +27,7 @@
 #endif
 
 #include "../g1.cu_amd/csrc/g1_model_tables.h"
+#include "../g1.cu_amd/csrc/tree.h"
 
 namespace orc {
 
@@ -141,8 +142,57 @@ template <class R> static inline Q4<R> ldq(const R* p) { return {p[0], p[1], p[2
 template <class R> static inline V3<R> ldv(const R* p) { return {p[0], p[1], p[2]}; }
 
 // ---------------------------------------------------------------- forward kinematics
-// (reference: src/dynamics.cuh:47-88)
+// (reference: src/dynamics.cuh:47-88) The reference composes each body's world frame from its
+// parent's, root to leaf: pos = pos_parent + rot(q_parent, body_pos), q = (q_parent (x)
+// body_quat) (x) rot(axis, qpos), with the hinge anchor shift pos + rot(q, jnt_pos) -
+// rot(q', jnt_pos), the identity since every jnt_pos is 0 (gen_model_tables.py asserts it).
+// This restatement composes the same per-body transforms (translation body_pos, rotation
+// body_quat (x) rot(axis, qpos); the pelvis: its free-joint pose) by ancestor doubling, the
+// association the GPU uses: round r sets T_b <- T_a o T_b with a the 2^r-th ancestor of b, reading
+// the transforms of the previous round (tree.h). Only the fp rounding association differs from the
+// reference's recursion; it is pinned, like the recursion was, against the MuJoCo frames of
+// bench/ref_traj.npz, and tests/test_oracle_fixtures.py checks the fp32 doubling against the
+// fp32 root -> leaf recursion (fk_recursive below).
 template <class R> void fk(const R* qpos, R* xpos, R* xquat, R* xipos) {
+  V3<R> tp[kNBody];
+  Q4<R> tq[kNBody];
+  tp[0] = {0, 0, 0};
+  tq[0] = {1, 0, 0, 0};
+  for (int b = 1; b < kNBody; ++b) {
+    const int j = body_jntadr[b], qa = jnt_qposadr[j];
+    if (jnt_type[j] == 0) {
+      tp[b] = {qpos[qa], qpos[qa + 1], qpos[qa + 2]};
+      tq[b] = qnorm(Q4<R>{qpos[qa + 3], qpos[qa + 4], qpos[qa + 5], qpos[qa + 6]});
+    } else {
+      tp[b] = ldv(&M<R>::body_pos[3 * b]);
+      tq[b] = qmul(ldq(&M<R>::body_quat[4 * b]), axisangle(ldv(&M<R>::jnt_axis[3 * j]), qpos[qa]));
+    }
+  }
+  for (int r = 0; r < kFkRounds; ++r) {
+    V3<R> op[kNBody];
+    Q4<R> oq[kNBody];
+    std::copy(tp, tp + kNBody, op);
+    std::copy(tq, tq + kNBody, oq);
+    for (int b = 1; b < kNBody; ++b) {
+      const int a = kAncestors.a[r][b];
+      if (a > 0) {
+        tp[b] = vadd(op[a], qrot(oq[a], op[b]));
+        tq[b] = qmul(oq[a], oq[b]);
+      }
+    }
+  }
+  for (int b = 0; b < kNBody; ++b) {
+    xpos[3 * b] = tp[b].x; xpos[3 * b + 1] = tp[b].y; xpos[3 * b + 2] = tp[b].z;
+    xquat[4 * b] = tq[b].w; xquat[4 * b + 1] = tq[b].x; xquat[4 * b + 2] = tq[b].y; xquat[4 * b + 3] = tq[b].z;
+    V3<R> cw = vadd(tp[b], qrot(tq[b], ldv(&M<R>::body_ipos[3 * b])));
+    xipos[3 * b] = cw.x; xipos[3 * b + 1] = cw.y; xipos[3 * b + 2] = cw.z;
+  }
+  xipos[0] = xipos[1] = xipos[2] = 0;
+}
+
+// The reference's root -> leaf recursion, literally (reference: src/dynamics.cuh:47-88): kept to
+// check the doubling association against it (tests/test_oracle_fixtures.py).
+template <class R> void fk_recursive(const R* qpos, R* xpos, R* xquat, R* xipos) {
   xpos[0] = xpos[1] = xpos[2] = 0;
   xquat[0] = 1; xquat[1] = xquat[2] = xquat[3] = 0;
   for (int b = 1; b < kNBody; ++b) {
@@ -1099,6 +1149,10 @@ int orc_nq() { return kNQ; }
 int orc_nv() { return kNV; }
 
 void orc_fk_f(int n, const float* q, float* xp, float* xq, float* xi) { fk_batch(n, q, xp, xq, xi); }
+void orc_fk_recursive_f(int n, const float* q, float* xp, float* xq, float* xi) {
+  for (int w = 0; w < n; ++w)
+    fk_recursive(q + (long)w * kNQ, xp + (long)w * kNBody * 3, xq + (long)w * kNBody * 4, xi + (long)w * kNBody * 3);
+}
 void orc_fk_d(int n, const double* q, double* xp, double* xq, double* xi) { fk_batch(n, q, xp, xq, xi); }
 void orc_bias_f(int n, const float* q, const float* v, float* S, float* b) { bias_batch(n, q, v, S, b); }
 void orc_bias_d(int n, const double* q, const double* v, double* S, double* b) { bias_batch(n, q, v, S, b); }

@@ -46,6 +46,7 @@ def _load():
         getattr(lib, f"orc_bdt_{suf}").argtypes = [fp]
         getattr(lib, f"orc_smooth_traj_{suf}").argtypes = [fp, fp, _c.c_int, fp, fp]
         getattr(lib, f"orc_implicit_traj_{suf}").argtypes = [fp, fp, fp, fp, _c.c_int, fp, fp]
+    lib.orc_fk_recursive_f.argtypes = [_c.c_int, _f32p, _f32p, _f32p, _f32p]
     lib.orc_qacc_debug_f.argtypes = [_f32p, _f32p, _f32p, _c.c_void_p, _c.c_int, _c.c_float] + [_f32p] * 7
     lib.orc_qacc_debug_f.restype = _c.c_int
     lib.orc_obs_f.argtypes = [_c.c_int, _f32p, _f32p, _f32p, _f32p]
@@ -90,6 +91,17 @@ def fk(qpos, dtype=np.float64):
     n = q.shape[0]
     xp = np.zeros((n, NBODY, 3), dtype); xq = np.zeros((n, NBODY, 4), dtype); xi = np.zeros((n, NBODY, 3), dtype)
     getattr(lib(), f"orc_fk_{_dt(dtype)}")(n, q, xp, xq, xi)
+    return xp, xq, xi
+
+
+def fk_recursive(qpos):
+    """fp32 forward kinematics by the reference's root -> leaf recursion (src/dynamics.cuh:47-88),
+    the association check of fk's ancestor doubling."""
+    q = _arr(np.atleast_2d(qpos), np.float32)
+    n = q.shape[0]
+    xp = np.zeros((n, NBODY, 3), np.float32); xq = np.zeros((n, NBODY, 4), np.float32)
+    xi = np.zeros((n, NBODY, 3), np.float32)
+    lib().orc_fk_recursive_f(n, q, xp, xq, xi)
     return xp, xq, xi
 
 

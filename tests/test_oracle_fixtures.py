@@ -23,6 +23,28 @@ def test_fk_matches_mujoco(orc, ref_traj):
     assert np.abs(xi - ref_traj["xipos"]).max() < 1e-8
 
 
+def test_fk_doubling_matches_recursion(orc, ref_traj):
+    """FK by ancestor doubling (the GPU's association) against the reference's root -> leaf
+    recursion, both fp32: the same transforms, so the frames agree to fp32 rounding (a wrong
+    ancestor, composition order or missing round would be off by O(1)); and both are pinned to
+    MuJoCo's fp64 frames at the same fp32 tolerance."""
+    rng = np.random.default_rng(3)
+    q = np.tile(ref_traj["qpos"][0], (512, 1)).astype(np.float64)
+    q[:, 7:] += rng.uniform(-1.0, 1.0, (512, 29))
+    q[:, 3:7] = rng.normal(size=(512, 4)); q[:, 3:7] /= np.linalg.norm(q[:, 3:7], axis=1, keepdims=True)
+    q = q.astype(np.float32)
+    a = orc.fk(q, dtype=np.float32)
+    b = orc.fk_recursive(q)
+    for x, y in zip(a, b):
+        assert np.abs(x - y).max() <= 2e-6, np.abs(x - y).max()
+    assert not all(np.array_equal(x, y) for x, y in zip(a, b))   # the associations do differ
+    qf, _ = _prestep(ref_traj)
+    for f in (lambda: orc.fk(qf.astype(np.float32), dtype=np.float32), lambda: orc.fk_recursive(qf.astype(np.float32))):
+        xp, xq, xi = f()
+        assert np.abs(xp - ref_traj["xpos"]).max() < 1e-5
+        assert np.abs(xq - ref_traj["xquat"]).max() < 1e-5
+
+
 def test_bias_matches_mujoco(orc, ref_traj):
     q, v = _prestep(ref_traj)
     _, b = orc.bias(q, v, dtype=np.float64)
