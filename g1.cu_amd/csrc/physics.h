@@ -141,6 +141,21 @@ __device__ __forceinline__ int symidx(int i, int j) {
   if (i > j) { int t = i; i = j; j = t; }
   return i * 6 - (i * (i - 1)) / 2 + (j - i);
 }
+// The free joint's motion subspace S_base: translation k = (0,0,0, e_k), rotation k = (R1 col k,
+// 0,0,0). Its products below skip the structural zeros (a generic 6-term sum adds exact zeros to
+// the one or three nonzero terms in the same order), which can change only the sign of an
+// exactly-zero result: -0 and +0 compare equal, and no later operation distinguishes them (every
+// divisor is positive). The oracle keeps the generic products.
+// S_base row k . x for k = 0..5 (x a 6-vector; R1col[k] = column k of R1 in S rows 3..5)
+__device__ __forceinline__ float sbase_dot(int k, const float* Srow, const float* x) {
+  return k < 3 ? x[3 + k] : fmaf_(Srow[2], x[2], fmaf_(Srow[1], x[1], Srow[0] * x[0]));
+}
+// component i of S_base' q (q the 6 base dofs): angular rows from the rotations, linear from the
+// translations
+__device__ __forceinline__ float sbase_col(int i, const float (&S3)[3][3], const float* q) {
+  return i < 3 ? fmaf_(S3[2][i], q[5], fmaf_(S3[1][i], q[4], S3[0][i] * q[3])) : q[i - 3];
+}
+
 __device__ __forceinline__ float dot6(const float* a, const float* b) {
   float s = 0.f;
 #pragma unroll
@@ -347,12 +362,11 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   }
   if (base) {
     R1 = quat2mat(xq);
+    // only the rotations' angular parts (R1 columns) are stored: every use of the free joint's
+    // subspace takes its structure from sbase_dot / sbase_col
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-#pragma unroll
-      for (int i = 0; i < 6; ++i) s.u.fac.S[k][i] = (i == 3 + k) ? 1.f : 0.f;
       s.u.fac.S[3 + k][0] = R1.m[k]; s.u.fac.S[3 + k][1] = R1.m[3 + k]; s.u.fac.S[3 + k][2] = R1.m[6 + k];
-      s.u.fac.S[3 + k][3] = 0.f; s.u.fac.S[3 + k][4] = 0.f; s.u.fac.S[3 + k][5] = 0.f;
     }
 #pragma unroll
     for (int k = 0; k < 6; ++k) s.qvel[k] = st.bqd[k];
@@ -379,38 +393,22 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   if (l == 0) av = {-MF::gravity[0], -MF::gravity[1], -MF::gravity[2]};
   if (base) {
     // free joint: translations accumulate normally; the three rotational cdof_dot use the
-    // post-translation partial velocity (reference: src/aba_bias.cuh:68-85)
-    V3 w{0.f, 0.f, 0.f}, v{0.f, 0.f, 0.f};
-    V3 Sdw[6], Sdv[6];
+    // post-translation partial velocity (reference: src/aba_bias.cuh:68-85). With the subspace's
+    // structural zeros skipped (see sbase_dot): the translations leave w = 0, v = (qd0, qd1, qd2)
+    // and cdof_dot = 0; rotation k has cdof_dot = (0, v x R1 col k), and w sums R1 col k qd(3+k)
+    const V3 vr{st.bqd[0], st.bqd[1], st.bqd[2]};
+    V3 w{R1.m[0] * st.bqd[3], R1.m[3] * st.bqd[3], R1.m[6] * st.bqd[3]};
+    V3 a_v{-MF::gravity[0], -MF::gravity[1], -MF::gravity[2]};
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-      V3 tw{0.f, 0.f, 0.f}, tv{k == 0 ? 1.f : 0.f, k == 1 ? 1.f : 0.f, k == 2 ? 1.f : 0.f};
-      crossm(w, v, tw, tv, Sdw[k], Sdv[k]);
-      const float qd = st.bqd[k];
-      w = {fmaf_(tw.x, qd, w.x), fmaf_(tw.y, qd, w.y), fmaf_(tw.z, qd, w.z)};
-      v = {fmaf_(tv.x, qd, v.x), fmaf_(tv.y, qd, v.y), fmaf_(tv.z, qd, v.z)};
-    }
-    const V3 wr = w, vr = v;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      V3 tw{R1.m[k], R1.m[3 + k], R1.m[6 + k]}, tv{0.f, 0.f, 0.f};
-      crossm(wr, vr, tw, tv, Sdw[3 + k], Sdv[3 + k]);
-    }
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
+      const V3 Rk{R1.m[k], R1.m[3 + k], R1.m[6 + k]};
       const float qd = st.bqd[3 + k];
-      w = {fmaf_(R1.m[k], qd, w.x), fmaf_(R1.m[3 + k], qd, w.y), fmaf_(R1.m[6 + k], qd, w.z)};
-      v = {fmaf_(0.f, qd, v.x), fmaf_(0.f, qd, v.y), fmaf_(0.f, qd, v.z)};
+      if (k > 0) w = {fmaf_(Rk.x, qd, w.x), fmaf_(Rk.y, qd, w.y), fmaf_(Rk.z, qd, w.z)};
+      const V3 sdv = cross(vr, Rk);
+      a_v = {fmaf_(sdv.x, qd, a_v.x), fmaf_(sdv.y, qd, a_v.y), fmaf_(sdv.z, qd, a_v.z)};
     }
-    vw = w; vv = v;
-    V3 a_w{0.f, 0.f, 0.f}, a_v{-MF::gravity[0], -MF::gravity[1], -MF::gravity[2]};
-#pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      const float qd = st.bqd[k];
-      a_w = {fmaf_(Sdw[k].x, qd, a_w.x), fmaf_(Sdw[k].y, qd, a_w.y), fmaf_(Sdw[k].z, qd, a_w.z)};
-      a_v = {fmaf_(Sdv[k].x, qd, a_v.x), fmaf_(Sdv[k].y, qd, a_v.y), fmaf_(Sdv[k].z, qd, a_v.z)};
-    }
-    aw = a_w; av = a_v;
+    vw = w; vv = vr;
+    aw = {0.f, 0.f, 0.f}; av = a_v;
   }
   // Hinge bodies, chain-parallel: the hinges form four chains (left leg 2..7, right leg 8..13,
   // waist 14..16 continued by the left arm 17..23, right arm 24..30 off the torso 16), walked
@@ -656,16 +654,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const float F1 = ((Fo[6 + rowc] + gshfl(Fc, 16 + rowc)) + gshfl(Fc, 8 + rowc)) + Fc;
     const V3 Fw{gshfl(F1, 0), gshfl(F1, 1), gshfl(F1, 2)}, Fv{gshfl(F1, 3), gshfl(F1, 4), gshfl(F1, 5)};
     if (base) {
+      // x_base = 0 - S_base.F_1 (see sbase_dot): translation k takes Fv_k, rotation k R1 col k . Fw
+      xb[0] = -Fv.x; xb[1] = -Fv.y; xb[2] = -Fv.z;
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        // translation axis e_k: S = (0,0,0, e_k); rotation axis R1 col k: S = (R1 col, 0,0,0)
-        const float e0 = k == 0 ? 1.f : 0.f, e1 = k == 1 ? 1.f : 0.f, e2 = k == 2 ? 1.f : 0.f;
-        const float bt = fmaf_(e2, Fv.z, fmaf_(e1, Fv.y, fmaf_(e0, Fv.x, fmaf_(0.f, Fw.z, fmaf_(0.f, Fw.y, 0.f * Fw.x)))));
-        const float br = fmaf_(0.f, Fv.z, fmaf_(0.f, Fv.y, fmaf_(0.f, Fv.x,
-                         fmaf_(R1.m[6 + k], Fw.z, fmaf_(R1.m[3 + k], Fw.y, R1.m[k] * Fw.x)))));
-        xb[k] = -bt + 0.f;
-        xb[3 + k] = -br + 0.f;
-      }
+      for (int k = 0; k < 3; ++k) xb[3 + k] = -fmaf_(R1.m[6 + k], Fw.z, fmaf_(R1.m[3 + k], Fw.y, R1.m[k] * Fw.x));
     }
     float I1[6];
 #pragma unroll
@@ -686,23 +678,20 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // base of the smooth system.
   __syncthreads();   // I^A of the pelvis and the hinge factor complete in LDS
   if (l < 6) {
-    float Sc[6], U6c[6];
-#pragma unroll
-    for (int j = 0; j < 6; ++j) Sc[j] = s.u.fac.S[l][j];
+    // column l of U6 = I^A S_base: translation l < 3 picks column 3 + l of I^A, rotation l >= 3
+    // is I^A's angular columns times R1 col (l - 3) (structural zeros skipped, see sbase_dot)
+    const int lt = l < 3 ? l : 0;
+    const float* Sc = s.u.fac.S[l < 3 ? 3 : l];   // (translation lanes: any stored row, unused)
+    float U6c[6];
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
-      float a = 0.f;
-#pragma unroll
-      for (int j = 0; j < 6; ++j) a = fmaf_(s.u.fac.IA1[symidx(i, j)], Sc[j], a);
-      U6c[i] = a;
+      const float rot = fmaf_(s.u.fac.IA1[symidx(i, 2)], Sc[2],
+                              fmaf_(s.u.fac.IA1[symidx(i, 1)], Sc[1], s.u.fac.IA1[symidx(i, 0)] * Sc[0]));
+      U6c[i] = l < 3 ? s.u.fac.IA1[symidx(i, 3 + lt)] : rot;
     }
+    // D = S_base' U6 (+ armature and dt*damping, both 0 on the free joint)
 #pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      float a = 0.f;
-#pragma unroll
-      for (int i = 0; i < 6; ++i) a = fmaf_(s.u.fac.S[k][i], U6c[i], a);
-      s.u.fac.Dm[k * 6 + l] = a + 0.f;   // + armature (0) + dt*damping (0) on the free joint
-    }
+    for (int k = 0; k < 6; ++k) s.u.fac.Dm[k * 6 + l] = sbase_dot(k, s.u.fac.S[k], U6c);
   }
   __syncthreads();
   float a6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -731,12 +720,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     // smooth solve, free joint: L L' qdd = x_base - S_base.pA_1 (reference: src/aba_factor.cuh:139-155)
     float qdd[6];
 #pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      float Sk[6];
-#pragma unroll
-      for (int i = 0; i < 6; ++i) Sk[i] = s.u.fac.S[k][i];
-      qdd[k] = xb[k] - dot6(Sk, pAs);
-    }
+    for (int k = 0; k < 6; ++k) qdd[k] = xb[k] - sbase_dot(k, s.u.fac.S[k], pAs);
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
       float a = qdd[i];
@@ -753,13 +737,13 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
 #pragma unroll
     for (int k = 0; k < 6; ++k) s.Mm[0][k] = qdd[k];
+    float S3[3][3];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      float a = 0.f;
+    for (int k = 0; k < 3; ++k)
 #pragma unroll
-      for (int k = 0; k < 6; ++k) a = fmaf_(s.u.fac.S[k][i], qdd[k], a);
-      a6[i] = a;
-    }
+      for (int i = 0; i < 3; ++i) S3[k][i] = s.u.fac.S[3 + k][i];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) a6[i] = sbase_col(i, S3, qdd);
   }
   // ---------------- smooth solve root -> leaf (reference: src/aba_factor.cuh:156-164)
   float Uk[6];
@@ -813,9 +797,18 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int k = 0; k < kContactDofs; ++k) {
       // ancestor dofs walked foot -> root: leg hinges (foot first), then the free base 0..5
       const int a = (k < 6) ? legbase + 5 - k : k - 6;
-      V3 w{s.u.fac.S[a][0], s.u.fac.S[a][1], s.u.fac.S[a][2]};
-      V3 lv{s.u.fac.S[a][3], s.u.fac.S[a][4], s.u.fac.S[a][5]};
-      V3 jc = vadd(cross(w, r), lv);
+      // point Jacobian column w x r + lv; on the free base (k >= 6) the structural zeros of
+      // S_base are skipped (see sbase_dot): translation a gives e_a, rotation a gives w x r
+      V3 jc;
+      if (k < 6) {
+        const V3 w{s.u.fac.S[a][0], s.u.fac.S[a][1], s.u.fac.S[a][2]};
+        const V3 lv{s.u.fac.S[a][3], s.u.fac.S[a][4], s.u.fac.S[a][5]};
+        jc = vadd(cross(w, r), lv);
+      } else if (a < 3) {
+        jc = {a == 0 ? 1.f : 0.f, a == 1 ? 1.f : 0.f, a == 2 ? 1.f : 0.f};
+      } else {
+        jc = cross(V3{s.u.fac.S[a][0], s.u.fac.S[a][1], s.u.fac.S[a][2]}, r);
+      }
       const float e0 = jc.z, e1 = mu * jc.y, e2 = -mu * jc.x;
       s.Eb[c][0][k] = e0; s.Eb[c][1][k] = e1; s.Eb[c][2][k] = e2;
       const float qd = s.qvel[a];
@@ -898,7 +891,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     {
       float rhs6[6];
 #pragma unroll
-      for (int k = 0; k < 6; ++k) rhs6[k] = xrhs(k) - dot6(s.u.fac.S[k], p1);
+      for (int k = 0; k < 6; ++k) rhs6[k] = xrhs(k) - sbase_dot(k, s.u.fac.S[k], p1);
       const float* Lf = s.u.fac.Dfac;
 #pragma unroll
       for (int i = 0; i < 6; ++i) {
@@ -918,12 +911,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     float* ycol = s.Mm[(j >= 1 && j < kCols) ? j : kCols - 1];
     const bool wr = j >= 1 && j < kCols;
     float a1[6];
+    {
+      float S3[3][3];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      float a = 0.f;
+      for (int k = 0; k < 3; ++k)
 #pragma unroll
-      for (int k = 0; k < 6; ++k) a = fmaf_(s.u.fac.S[k][i], qdd[k], a);
-      a1[i] = a;
+        for (int i = 0; i < 3; ++i) S3[k][i] = s.u.fac.S[3 + k][i];
+#pragma unroll
+      for (int i = 0; i < 6; ++i) a1[i] = sbase_col(i, S3, qdd);
     }
     if (wr) {
 #pragma unroll
