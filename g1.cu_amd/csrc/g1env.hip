@@ -380,20 +380,50 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
   const int tid = threadIdx.x;
   const int w0 = blockIdx.x * kTileWorlds;
   // ---- observation + frozen normalisation (reference: src/g1_env.cu:297-304)
-  for (int idx = tid; idx < kTileWorlds * kObs; idx += kPolicyThreads) {
-    const int m = idx / kObs, i = idx - m * kObs;
-    const int w = w0 + m;
-    float z = 0.f;
-    if (w < a.N) {
-      if (a.obs_in) z = a.obs_in[(long)w * kObs + i];
-      else {
-        const float o = obs_value(a.qp + (long)w * kNQ, a.qv + (long)w * kNV, a.pa + (long)w * kAct, i);
+  if (!a.obs_in) {
+    // the tile's state first, with coalesced loads all in flight together (qp, qv, pa of worlds
+    // w0.. are contiguous blocks), into the second activation buffer (free until layer 1)
+    float* Sq = Y;
+    float* Sv = Sq + kTileWorlds * kNQ;
+    float* Sp = Sv + kTileWorlds * kNV;
+    const int nw = a.N - w0 < kTileWorlds ? a.N - w0 : kTileWorlds;
+    for (int idx = tid; idx < kTileWorlds * (kNQ + kNV + kAct); idx += kPolicyThreads) {
+      float v = 0.f;
+      if (idx < kTileWorlds * kNQ) {
+        if (idx < nw * kNQ) v = a.qp[(long)w0 * kNQ + idx];
+      } else if (idx < kTileWorlds * (kNQ + kNV)) {
+        const int r = idx - kTileWorlds * kNQ;
+        if (r < nw * kNV) v = a.qv[(long)w0 * kNV + r];
+      } else {
+        const int r = idx - kTileWorlds * (kNQ + kNV);
+        if (r < nw * kAct) v = a.pa[(long)w0 * kAct + r];
+      }
+      Sq[idx] = v;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < kTileWorlds * kObs; idx += kPolicyThreads) {
+      const int m = idx / kObs, i = idx - m * kObs;
+      const int w = w0 + m;
+      float z = 0.f;
+      if (w < a.N) {
+        const float o = obs_value(Sq + m * kNQ, Sv + m * kNV, Sp + m * kAct, i);
         if (a.t < a.H) a.O[((long)a.t * a.N + w) * kObs + i] = o;
         z = (o - a.mean[i]) / sqrtf(a.var[i] + 1e-8f);
         if (z < -10.f) z = -10.f; else if (z > 10.f) z = 10.f;
       }
+      X[m * kLdx + kperm(i)] = z;
     }
-    X[m * kLdx + i] = z;
+  } else {
+    for (int idx = tid; idx < kTileWorlds * kObs; idx += kPolicyThreads) {
+      const int m = idx / kObs, i = idx - m * kObs;
+      const int w = w0 + m;
+      X[m * kLdx + kperm(i)] = w < a.N ? a.obs_in[(long)w * kObs + i] : 0.f;
+    }
+  }
+  // zero the first layer's K padding (observation index kObs .. K0 - 1; its weight rows are zero)
+  for (int idx = tid; idx < kTileWorlds * (a.pp.K[0] - kObs); idx += kPolicyThreads) {
+    const int m = idx / (a.pp.K[0] - kObs), i = kObs + idx % (a.pp.K[0] - kObs);
+    X[m * kLdx + kperm(i)] = 0.f;
   }
   __syncthreads();
   // ---- hidden layers
@@ -401,7 +431,7 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
   float* out = Y;
   for (int ly = 0; ly < a.shape.nl; ++ly) {
     mfma_layer(in, kLdx, out, kLdx, a.pp.Wp + a.pp.woff[ly], a.pp.Wp + a.pp.boff[ly], a.pp.K[ly], a.pp.Np[ly],
-               a.shape.act, true);
+               a.shape.act, true, true);
     __syncthreads();
     float* t = in; in = out; out = t;
   }
@@ -414,7 +444,7 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
     head = in;
   } else {
     mfma_layer(in, kLdx, out, kLdx, a.pp.Wp + a.pp.woff[a.shape.nl], a.pp.Wp + a.pp.boff[a.shape.nl],
-               a.pp.K[a.shape.nl], 32, 0, false);
+               a.pp.K[a.shape.nl], 32, 0, false, false);
   }
   __syncthreads();
   // ---- sampling + log-prob (reference: src/g1_env.cu:308-318): one thread per (world, action)
@@ -472,15 +502,18 @@ __global__ void k_pack(PackArgs a) {
   const long base = a.pp.woff[ly];
   const long rel = idx - base;
   const int K = a.pp.K[ly], Np = a.pp.Np[ly];
-  const long wsize = (long)(K / 2) * Np * 2;
+  const long wsize = (long)K * Np;
   // source offsets in torch order
   long src = 0;
   int in = kObs;
   for (int q = 0; q < ly; ++q) { src += (long)a.shape.hid[q] * in + a.shape.hid[q]; in = a.shape.hid[q]; }
   const int Kin = in;
   if (rel < wsize) {
-    const int kk = (int)(rel / (Np * 2)), rem = (int)(rel % (Np * 2));
-    const int n = rem / 2, k = 2 * kk + (rem & 1);
+    // k-octet-major: rel = ((o * Np + n) * 2 + khalf) * 4 + j holds W[n][8o + 2j + khalf]
+    const int j = (int)(rel & 3), khalf = (int)((rel >> 2) & 1);
+    const long r8 = rel >> 3;
+    const int n = (int)(r8 % Np), o = (int)(r8 / Np);
+    const int k = 8 * o + 2 * j + khalf;
     float v = 0.f;
     if (ly < a.shape.nl) {
       if (n < a.shape.hid[ly] && k < Kin) v = a.W[src + (long)n * Kin + k];
@@ -599,10 +632,10 @@ static PackedPolicy make_packed(const PolicyShape& sh, float* Wp, const float* W
   int in = kObs;
   for (int ly = 0; ly <= sh.nl; ++ly) {
     const int out = ly < sh.nl ? sh.hid[ly] : 32;
-    pp.K[ly] = (in + 1) & ~1;
+    pp.K[ly] = (in + 7) & ~7;
     pp.Np[ly] = (out + 31) & ~31;
-    pp.woff[ly] = off;
-    off += (long)(pp.K[ly] / 2) * pp.Np[ly] * 2;
+    pp.woff[ly] = off;   // a multiple of 4 floats: every term below is (float4 loads)
+    off += (long)pp.K[ly] * pp.Np[ly];
     pp.boff[ly] = off;
     off += pp.Np[ly];
     if (ly < sh.nl) in = sh.hid[ly];
@@ -646,8 +679,9 @@ static void pack_policy(EnvState* E, const float* W, PackedPolicy* out) {
   *out = pp;
 }
 
-// activation tile pitch: widest layer + 4 floats (keeps rows off the same LDS banks)
-static int policy_ldx(const PolicyShape& sh) { return max_width(sh) + 4; }
+// activation tile pitch: widest layer rounded up to the 32-column tiles, + 4 floats (keeps rows off
+// the same LDS banks; a multiple of 4 for the 16-byte operand reads)
+static int policy_ldx(const PolicyShape& sh) { return (max_width(sh) + 31) / 32 * 32 + 4; }
 static size_t policy_smem(const PolicyShape& sh) { return 2 * (size_t)kTileWorlds * policy_ldx(sh) * sizeof(float); }
 
 static void launch_policy_kernel(const PolicyArgs& a, int N, const PolicyShape& sh) {

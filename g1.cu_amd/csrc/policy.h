@@ -1,10 +1,10 @@
 // policy.h -- observation, frozen normalisation, policy MLP on fp32 MFMA, Gaussian sampling.
 //
-// One workgroup (8 waves) owns a tile of 32 worlds. Activations live in LDS ([32][K] row-major,
-// padded); each dense layer is a [32 x K] . [K x N] contraction on v_mfma_f32_32x32x2f32 with the
-// weights pre-packed k-pair-major (Wp[k/2][n][k%2]) so every B-operand load is one contiguous
-// 256-byte line. Waves take 32-column output tiles round-robin. The mu (29) and value (1) heads are
-// fused into one 32-wide tile.
+// One workgroup (8 waves) owns a tile of 32 worlds. Activations live in LDS ([32][K], k-octet
+// interleaved, padded rows); each dense layer is a [32 x K] . [K x N] contraction on
+// v_mfma_f32_32x32x2f32 with the weights pre-packed k-octet-major, so the operands of four MFMA
+// steps are one float4 global load (B) and one 16-byte LDS read (A) per lane. Waves take 32-column
+// output tiles round-robin. The mu (29) and value (1) heads are fused into one 32-wide tile.
 //
 // Reference: obs src/g1_env.cu:46-81; normalise/clamp :298-302; MLP :219-239 (AC of
 // scripts/ppo.py:85-99, packing scripts/ppo_fused.py:35-44); sampling + log-prob :308-318.
@@ -32,13 +32,14 @@ struct PolicyShape {
   int act;   // 0 tanh, 1 ELU
 };
 
-// Offsets of each packed layer inside the packed buffer (floats). Layer l: weights Kp/2 x Np x 2,
-// then bias Np. The head is layer nl with Np = 32 (mu 0..28, value 29, zero pad).
+// Offsets of each packed layer inside the packed buffer (floats). Layer l: weights Kp/8 x Np x 2 x 4
+// (k-octet-major, see mfma_layer), then bias Np. The head is layer nl with Np = 32 (mu 0..28,
+// value 29, zero pad).
 struct PackedPolicy {
   const float* Wp;
   long woff[kMaxLayers + 1];
   long boff[kMaxLayers + 1];
-  int K[kMaxLayers + 1];   // padded to even
+  int K[kMaxLayers + 1];   // padded to a multiple of 8
   int Np[kMaxLayers + 1];  // padded to 32
   const float* log_std;    // 29 values (torch order, unpacked tail of W)
 };
@@ -96,12 +97,53 @@ __device__ __forceinline__ float rng_pm1(unsigned long long seed, int w, unsigne
   return u01(r.x) * 2.f - 1.f;
 }
 
-// ---------------------------------------------------------------- one dense layer on MFMA
+// ---------------------------------------------------------------- dense layers on MFMA
+// v_mfma_f32_32x32x2f32 step kk: lane (mrow = lane & 31, khalf = lane >> 5) supplies A = x[mrow][2kk
+// + khalf] and B = W[n0 + mrow][2kk + khalf]. Four consecutive steps (one k-octet o: k = 8o + 2j +
+// khalf, j = 0..3) take their operands from one 16-byte load each:
+// * weights packed k-octet-major, Wp[o][n][khalf][j] = W[n][8o + 2j + khalf] (K padded to a multiple
+//   of 8 with zero rows): the 64 lanes' float4 loads of one octet are one contiguous 1 KB line;
+// * activations in LDS k-octet interleaved, X[m][kperm(k)] with kperm(8o + 2j + khalf) = 8o +
+//   4 khalf + j, so a lane's four A operands are one ds_read_b128.
+__host__ __device__ __forceinline__ int kperm(int k) { return (k & ~7) | ((k & 1) << 2) | ((k >> 1) & 3); }
+
+// acc += A . B over k-octets [o0, o1) of one 32-column tile (B base at the tile's column), in
+// batches of kO octets whose loads are all in flight before the batch's MFMAs
+__device__ __forceinline__ void mfma_octets(f32x16& acc, const float* __restrict__ arow,
+                                            const float4* __restrict__ wq, long wstride, int o0, int o1) {
+  constexpr int kO = 8;
+  int o = o0;
+  for (; o + kO <= o1; o += kO) {
+    float4 b[kO], av[kO];
+#pragma unroll
+    for (int u = 0; u < kO; ++u) {
+      b[u] = wq[(long)(o + u) * wstride];
+      av[u] = *reinterpret_cast<const float4*>(arow + 8 * (o + u));
+    }
+#pragma unroll
+    for (int u = 0; u < kO; ++u) {
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].x, b[u].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].y, b[u].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].z, b[u].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].w, b[u].w, acc, 0, 0, 0);
+    }
+  }
+  for (; o < o1; ++o) {
+    const float4 b = wq[(long)o * wstride];
+    const float4 av = *reinterpret_cast<const float4*>(arow + 8 * o);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, b.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, b.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, b.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, b.w, acc, 0, 0, 0);
+  }
+}
+
 // out[m][n] = act(sum_k in[m][k] W[n][k] + b[n]) for the 32 worlds of the tile.
-// in: LDS [32][ldi], out: LDS [32][ldo]; wave wv takes n-tiles wv, wv + kPolicyWaves, ...
+// in: LDS [32][ldi] k-octet interleaved; out: LDS [32][ldo], interleaved when it feeds another
+// layer (permute_out), natural otherwise; wave wv takes n-tiles wv, wv + kPolicyWaves, ...
 __device__ __forceinline__ void mfma_layer(const float* __restrict__ in, int ldi, float* __restrict__ out, int ldo,
                                            const float* __restrict__ Wp, const float* __restrict__ bias, int K,
-                                           int Np, int act, bool apply_act) {
+                                           int Np, int act, bool apply_act, bool permute_out) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int mrow = lane & 31, khalf = lane >> 5;
   for (int nt = wv; nt < Np / 32; nt += kPolicyWaves) {
@@ -110,65 +152,37 @@ __device__ __forceinline__ void mfma_layer(const float* __restrict__ in, int ldi
     f32x16 acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = bv;
-    const float* wcol = Wp + (long)(n0 + mrow) * 2 + khalf;
-    const float* arow = in + mrow * ldi + khalf;
-    // k-pairs in batches of kB: all kB weight loads (L2 latency) are in flight before the first
-    // MFMA of the batch waits on them
-    constexpr int kB = 16;
-    const int K2 = K / 2;
-    int kk = 0;
-    for (; kk + kB <= K2; kk += kB) {
-      float a[kB], b[kB];
-#pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        b[u] = wcol[(long)(kk + u) * Np * 2];
-        a[u] = arow[2 * (kk + u)];
-      }
-#pragma unroll
-      for (int u = 0; u < kB; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u], b[u], acc, 0, 0, 0);
-    }
-    for (; kk < K2; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(arow[2 * kk], wcol[(long)kk * Np * 2], acc, 0, 0, 0);
+    const float4* wq = reinterpret_cast<const float4*>(Wp) + (long)(n0 + mrow) * 2 + khalf;
+    mfma_octets(acc, in + mrow * ldi + 4 * khalf, wq, (long)Np * 2, 0, K / 8);
+    const int nc = permute_out ? kperm(n0 + mrow) : n0 + mrow;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int m = (i & 3) + 4 * khalf + 8 * (i >> 2);
       const float v = acc[i];
-      out[m * ldo + n0 + mrow] = apply_act ? act_fn(v, act) : v;
+      out[m * ldo + nc] = apply_act ? act_fn(v, act) : v;
     }
   }
 }
 
-// The fused 32-wide head has a single output tile: its K range is split over the waves and the
+// The fused 32-wide head has a single output tile: its k-octets are split over the waves and the
 // partial tiles are summed through LDS in wave order (scratch: kPolicyWaves x 32 x 32 floats, not
 // aliasing `in`; `out` may alias `in`: every wave has finished reading `in` at the barrier before
-// the sum is written).
+// the sum is written). Output in natural column order.
 __device__ __forceinline__ void mfma_head_splitk(const float* in, int ldi, float* out, int ldo,
                                                  float* __restrict__ scratch, const float* __restrict__ Wp,
                                                  const float* __restrict__ bias, int K) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int mrow = lane & 31, khalf = lane >> 5;
   constexpr int Np = 32;
-  const int K2 = K / 2;
-  const int q = (K2 + kPolicyWaves - 1) / kPolicyWaves;
-  const int k0 = wv * q, k1 = min(K2, k0 + q);
+  const int K8 = K / 8;
+  const int q = (K8 + kPolicyWaves - 1) / kPolicyWaves;
+  const int o0 = wv * q, o1 = min(K8, o0 + q);
   f32x16 acc;
   const float bv = wv == 0 ? bias[mrow] : 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = bv;
-  const float* wcol = Wp + (long)mrow * 2 + khalf;
-  const float* arow = in + mrow * ldi + khalf;
-  constexpr int kB = 16;
-  int kk = k0;
-  for (; kk + kB <= k1; kk += kB) {
-    float a[kB], b[kB];
-#pragma unroll
-    for (int u = 0; u < kB; ++u) {
-      b[u] = wcol[(long)(kk + u) * Np * 2];
-      a[u] = arow[2 * (kk + u)];
-    }
-#pragma unroll
-    for (int u = 0; u < kB; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u], b[u], acc, 0, 0, 0);
-  }
-  for (; kk < k1; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(arow[2 * kk], wcol[(long)kk * Np * 2], acc, 0, 0, 0);
+  const float4* wq = reinterpret_cast<const float4*>(Wp) + (long)mrow * 2 + khalf;
+  if (o0 < o1) mfma_octets(acc, in + mrow * ldi + 4 * khalf, wq, (long)Np * 2, o0, o1);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int m = (i & 3) + 4 * khalf + 8 * (i >> 2);
