@@ -383,20 +383,29 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
   if (!a.obs_in) {
     // the tile's state first, with coalesced loads all in flight together (qp, qv, pa of worlds
     // w0.. are contiguous blocks), into the second activation buffer (free until layer 1)
+    // (with the frozen statistics: mean and the divisor sqrt(var + 1e-8) per observation index)
     float* Sq = Y;
     float* Sv = Sq + kTileWorlds * kNQ;
     float* Sp = Sv + kTileWorlds * kNV;
+    float* Smean = Sp + kTileWorlds * kAct;
+    float* Sdiv = Smean + kObs;
+    static_assert(kTileWorlds * (kNQ + kNV + kAct) + 2 * kObs <= kTileWorlds * ((kObs + 31) / 32 * 32 + 4),
+                  "staging fits the smallest activation tile (pitch of policy_ldx)");
     const int nw = a.N - w0 < kTileWorlds ? a.N - w0 : kTileWorlds;
-    for (int idx = tid; idx < kTileWorlds * (kNQ + kNV + kAct); idx += kPolicyThreads) {
+    for (int idx = tid; idx < kTileWorlds * (kNQ + kNV + kAct) + kObs; idx += kPolicyThreads) {
       float v = 0.f;
       if (idx < kTileWorlds * kNQ) {
         if (idx < nw * kNQ) v = a.qp[(long)w0 * kNQ + idx];
       } else if (idx < kTileWorlds * (kNQ + kNV)) {
         const int r = idx - kTileWorlds * kNQ;
         if (r < nw * kNV) v = a.qv[(long)w0 * kNV + r];
-      } else {
+      } else if (idx < kTileWorlds * (kNQ + kNV + kAct)) {
         const int r = idx - kTileWorlds * (kNQ + kNV);
         if (r < nw * kAct) v = a.pa[(long)w0 * kAct + r];
+      } else {
+        const int i = idx - kTileWorlds * (kNQ + kNV + kAct);
+        v = a.mean[i];
+        Sdiv[i] = sqrtf(a.var[i] + 1e-8f);
       }
       Sq[idx] = v;
     }
@@ -408,7 +417,7 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
       if (w < a.N) {
         const float o = obs_value(Sq + m * kNQ, Sv + m * kNV, Sp + m * kAct, i);
         if (a.t < a.H) a.O[((long)a.t * a.N + w) * kObs + i] = o;
-        z = (o - a.mean[i]) / sqrtf(a.var[i] + 1e-8f);
+        z = (o - Smean[i]) / Sdiv[i];
         if (z < -10.f) z = -10.f; else if (z > 10.f) z = 10.f;
       }
       X[m * kLdx + kperm(i)] = z;
