@@ -128,13 +128,24 @@ __device__ __forceinline__ void mfma_octets(f32x16& acc, const float* __restrict
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].w, b[u].w, acc, 0, 0, 0);
     }
   }
-  for (; o < o1; ++o) {
-    const float4 b = wq[(long)o * wstride];
-    const float4 av = *reinterpret_cast<const float4*>(arow + 8 * o);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, b.x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, b.y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, b.z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, b.w, acc, 0, 0, 0);
+  // the last partial batch: its loads are also all issued before its MFMAs (rem is wave-uniform)
+  const int rem = o1 - o;
+  if (rem > 0) {
+    float4 b[kO - 1], av[kO - 1];
+#pragma unroll
+    for (int u = 0; u < kO - 1; ++u)
+      if (u < rem) {
+        b[u] = wq[(long)(o + u) * wstride];
+        av[u] = *reinterpret_cast<const float4*>(arow + 8 * (o + u));
+      }
+#pragma unroll
+    for (int u = 0; u < kO - 1; ++u)
+      if (u < rem) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].x, b[u].x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].y, b[u].y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].z, b[u].z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].w, b[u].w, acc, 0, 0, 0);
+      }
   }
 }
 
