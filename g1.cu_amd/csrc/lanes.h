@@ -39,6 +39,17 @@ __device__ __forceinline__ float gsum(float v) {
   return v;
 }
 
+// gsum when only lanes 0..15 of the group can be nonzero (lanes 16..31 hold +-0): the permlane16
+// stage would add those zeros, so it is skipped; the row rotations give every lane of row 0 the
+// same sum as gsum's, equal to it except for the sign of an exactly-zero result.
+__device__ __forceinline__ float gsum16(float v) {
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
+  return v;
+}
+
 // maximum of an int over the whole wave (both groups): uniform trip counts for loops whose
 // length depends on per-world data
 __device__ __forceinline__ int wave_max(int v) {
