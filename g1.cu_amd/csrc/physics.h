@@ -352,6 +352,30 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   const V3 xip = vadd(xp, qrot(xq, L.ipos));
   const V3 p{gshfl(xp.x, 1), gshfl(xp.y, 1), gshfl(xp.z, 1)};   // pelvis origin
 
+  // ---------------- contact detection: lane s = foot sphere s (reference: src/contact.cuh:31-46)
+  int ncon = 0;
+  if (P.contact) {
+    const int sph = l < kNFoot ? l : 0;
+    const int fb = foot_body[sph];
+    Q4 fq{gshfl(xq.w, fb), gshfl(xq.x, fb), gshfl(xq.y, fb), gshfl(xq.z, fb)};
+    V3 fp{gshfl(xp.x, fb), gshfl(xp.y, fb), gshfl(xp.z, fb)};
+    V3 lp{MF::foot_lpos[3 * sph], MF::foot_lpos[3 * sph + 1], MF::foot_lpos[3 * sph + 2]};
+    V3 c = vadd(fp, qrot(fq, lp));
+    const float pen = c.z - MF::foot_radius;
+    const bool hit = (l < kNFoot) && (pen < 0.f);
+    const unsigned mask = group_ballot8(hit);
+    ncon = __popc(mask);
+    if (hit) {
+      const int idx = __popc(mask & ((1u << l) - 1u));
+      s.con[idx][0] = c.x; s.con[idx][1] = c.y; s.con[idx][2] = pen * 0.5f; s.con[idx][3] = pen;
+      s.con_w0[idx] = MF::foot_invweight0[sph];
+      s.con_leg[idx] = (fb == foot_body[kNFoot - 1]) ? 1 : 0;
+    }
+  }
+  // (detected right after FK: the contact count decides below who computes the smooth solve's
+  // base and root -> leaf parts; the LDS writes are read after the later barriers)
+  const int ncon_max = wave_max(ncon);
+
   // ---------------- motion axes (reference: src/aba_bias.cuh:25-43)
   V3 sw{0.f, 0.f, 0.f}, sv{0.f, 0.f, 0.f};   // hinge axis (angular; linear)
   M3 R1{};
@@ -720,74 +744,58 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int i = 0; i < 36; ++i) s.u.fac.Dfac[i] = Dm[i];
 #pragma unroll
     for (int i = 0; i < 6; ++i) s.u.fac.Dinv[i] = Dinv[i];
-    // smooth solve, free joint: L L' qdd = x_base - S_base.pA_1 (reference: src/aba_factor.cuh:139-155)
-    float qdd[6];
+    // With contacts the smooth solve's base and root -> leaf parts run as column 0 of the contact
+    // solves below (lane 0, the same operations in the same order); without, here and in the
+    // level-synchronous sweep.
+    if (ncon_max == 0) {
+      // smooth solve, free joint: L L' qdd = x_base - S_base.pA_1 (reference: src/aba_factor.cuh:139-155)
+      float qdd[6];
 #pragma unroll
-    for (int k = 0; k < 6; ++k) qdd[k] = xb[k] - sbase_dot(k, s.u.fac.S[k], pAs);
+      for (int k = 0; k < 6; ++k) qdd[k] = xb[k] - sbase_dot(k, s.u.fac.S[k], pAs);
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      float a = qdd[i];
+      for (int i = 0; i < 6; ++i) {
+        float a = qdd[i];
 #pragma unroll
-      for (int k = 0; k < i; ++k) a = fmaf_(-Dm[i * 6 + k], qdd[k], a);
-      qdd[i] = div_rn(a, Dm[i * 6 + i], Dinv[i]);
+        for (int k = 0; k < i; ++k) a = fmaf_(-Dm[i * 6 + k], qdd[k], a);
+        qdd[i] = div_rn(a, Dm[i * 6 + i], Dinv[i]);
+      }
+#pragma unroll
+      for (int i = 5; i >= 0; --i) {
+        float a = qdd[i];
+#pragma unroll
+        for (int k = i + 1; k < 6; ++k) a = fmaf_(-Dm[k * 6 + i], qdd[k], a);
+        qdd[i] = div_rn(a, Dm[i * 6 + i], Dinv[i]);
+      }
+#pragma unroll
+      for (int k = 0; k < 6; ++k) s.Mm[0][k] = qdd[k];
+      float S3[3][3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+#pragma unroll
+        for (int i = 0; i < 3; ++i) S3[k][i] = s.u.fac.S[3 + k][i];
+#pragma unroll
+      for (int i = 0; i < 6; ++i) a6[i] = sbase_col(i, S3, qdd);
     }
-#pragma unroll
-    for (int i = 5; i >= 0; --i) {
-      float a = qdd[i];
-#pragma unroll
-      for (int k = i + 1; k < 6; ++k) a = fmaf_(-Dm[k * 6 + i], qdd[k], a);
-      qdd[i] = div_rn(a, Dm[i * 6 + i], Dinv[i]);
-    }
-#pragma unroll
-    for (int k = 0; k < 6; ++k) s.Mm[0][k] = qdd[k];
-    float S3[3][3];
-#pragma unroll
-    for (int k = 0; k < 3; ++k)
-#pragma unroll
-      for (int i = 0; i < 3; ++i) S3[k][i] = s.u.fac.S[3 + k][i];
-#pragma unroll
-    for (int i = 0; i < 6; ++i) a6[i] = sbase_col(i, S3, qdd);
   }
   // ---------------- smooth solve root -> leaf (reference: src/aba_factor.cuh:156-164)
-  float Uk[6];
+  if (ncon_max == 0) {
+    float Uk[6];
 #pragma unroll
-  for (int k = 0; k < 6; ++k) Uk[k] = s.u.fac.U[L.b][k];
-  const float usk = s.u.fac.us[L.b], iDk = s.u.fac.invD[L.b];
+    for (int k = 0; k < 6; ++k) Uk[k] = s.u.fac.U[L.b][k];
+    const float usk = s.u.fac.us[L.b], iDk = s.u.fac.invD[L.b];
 #pragma unroll
-  for (int r = 2; r <= kMaxDepth; ++r) {
-    float ap[6];
+    for (int r = 2; r <= kMaxDepth; ++r) {
+      float ap[6];
 #pragma unroll
-    for (int k = 0; k < 6; ++k) ap[k] = gshfl(a6[k], L.par);
-    if (L.depth == r) {
-      const float q = (usk - dot6(Uk, ap)) * iDk;
+      for (int k = 0; k < 6; ++k) ap[k] = gshfl(a6[k], L.par);
+      if (L.depth == r) {
+        const float q = (usk - dot6(Uk, ap)) * iDk;
 #pragma unroll
-      for (int k = 0; k < 6; ++k) a6[k] = fmaf_(S6[k], q, ap[k]);
-      s.Mm[0][L.b + 4] = q;
+        for (int k = 0; k < 6; ++k) a6[k] = fmaf_(S6[k], q, ap[k]);
+        s.Mm[0][L.b + 4] = q;
+      }
     }
   }
-
-  // ---------------- contact detection: lane s = foot sphere s (reference: src/contact.cuh:31-46)
-  int ncon = 0;
-  if (P.contact) {
-    const int sph = l < kNFoot ? l : 0;
-    const int fb = foot_body[sph];
-    Q4 fq{gshfl(xq.w, fb), gshfl(xq.x, fb), gshfl(xq.y, fb), gshfl(xq.z, fb)};
-    V3 fp{gshfl(xp.x, fb), gshfl(xp.y, fb), gshfl(xp.z, fb)};
-    V3 lp{MF::foot_lpos[3 * sph], MF::foot_lpos[3 * sph + 1], MF::foot_lpos[3 * sph + 2]};
-    V3 c = vadd(fp, qrot(fq, lp));
-    const float pen = c.z - MF::foot_radius;
-    const bool hit = (l < kNFoot) && (pen < 0.f);
-    const unsigned mask = group_ballot8(hit);
-    ncon = __popc(mask);
-    if (hit) {
-      const int idx = __popc(mask & ((1u << l) - 1u));
-      s.con[idx][0] = c.x; s.con[idx][1] = c.y; s.con[idx][2] = pen * 0.5f; s.con[idx][3] = pen;
-      s.con_w0[idx] = MF::foot_invweight0[sph];
-      s.con_leg[idx] = (fb == foot_body[kNFoot - 1]) ? 1 : 0;
-    }
-  }
-  const int ncon_max = wave_max(ncon);
-  __syncthreads();
 
   // ---------------- PASS 1: basis rows, R, aref (reference: src/env_qacc.cuh:67-136)
   const float mu = P.mu;
@@ -832,7 +840,9 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   __syncthreads();
 
   // ---------------- PASS 2: M^-1 solves, lane j = basis column j (reference: src/aba_factor.cuh:121-165,
-  // src/env_qacc.cuh:137-152); column 0 (the smooth solve) was computed by the tree sweeps above.
+  // src/env_qacc.cuh:137-152). Lane 0 finishes column 0, the smooth solve: its leaf -> root part
+  // (pA_1, u) came with the factor, its base and root -> leaf parts are the code below with
+  // x_base, pA_1 and u from the smooth solve.
   // The traversal is unrolled over the static tree. Articulated bias forces travel as explicit
   // carries along each chain (arm chains end in the torso 16, leg and waist chains in the pelvis 1);
   // parents with several children accumulate them in the reference's descending-child order.
@@ -887,14 +897,18 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       up(7 - i, carL, c2);
     }
     float p1[6];
+    const bool smooth = j == 0;
 #pragma unroll
-    for (int k = 0; k < 6; ++k) p1[k] = c8[k] + c2[k];
+    for (int k = 0; k < 6; ++k) p1[k] = smooth ? pAs[k] : c8[k] + c2[k];
+    float xb0[6];   // the smooth right-hand side on the base dofs (lane 1 holds it)
+#pragma unroll
+    for (int k = 0; k < 6; ++k) xb0[k] = gshfl(xb[k], 1);
     // free joint: D qdd = x_base - S_base.pA_1 with D = L L'
     float qdd[6];
     {
       float rhs6[6];
 #pragma unroll
-      for (int k = 0; k < 6; ++k) rhs6[k] = xrhs(k) - sbase_dot(k, s.u.fac.S[k], p1);
+      for (int k = 0; k < 6; ++k) rhs6[k] = (smooth ? xb0[k] : xrhs(k)) - sbase_dot(k, s.u.fac.S[k], p1);
       const float* Lf = s.u.fac.Dfac;
 #pragma unroll
       for (int i = 0; i < 6; ++i) {
@@ -911,8 +925,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         qdd[i] = div_rn(a, Lf[i * 6 + i], s.u.fac.Dinv[i]);
       }
     }
-    float* ycol = s.Mm[(j >= 1 && j < kCols) ? j : kCols - 1];
-    const bool wr = j >= 1 && j < kCols;
+    float* ycol = s.Mm[j < kCols ? j : kCols - 1];
+    const bool wr = j < kCols;
     float a1[6];
     {
       float S3[3][3];
@@ -935,7 +949,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const int d = b + 4;
       const float* Ub = s.u.fac.U[b];
       const float* Sd = s.u.fac.S[d];
-      const float q = (u[b] - dot6(Ub, ap)) * s.u.fac.invD[b];
+      const float ub = smooth ? s.u.fac.us[b] : u[b];
+      const float q = (ub - dot6(Ub, ap)) * s.u.fac.invD[b];
       if (wr) ycol[d] = q;
 #pragma unroll
       for (int k = 0; k < 6; ++k) ac[k] = fmaf_(Sd[k], q, ap[k]);
