@@ -389,7 +389,8 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
     float* Sp = Sv + kTileWorlds * kNV;
     float* Smean = Sp + kTileWorlds * kAct;
     float* Sdiv = Smean + kObs;
-    static_assert(kTileWorlds * (kNQ + kNV + kAct) + 2 * kObs <= kTileWorlds * ((kObs + 31) / 32 * 32 + 4),
+    float* Srcp = Sdiv + kObs;   // RN(1 / divisor): the quotient below is div_rn, the IEEE quotient
+    static_assert(kTileWorlds * (kNQ + kNV + kAct) + 3 * kObs <= kTileWorlds * ((kObs + 31) / 32 * 32 + 4),
                   "staging fits the smallest activation tile (pitch of policy_ldx)");
     const int nw = a.N - w0 < kTileWorlds ? a.N - w0 : kTileWorlds;
     for (int idx = tid; idx < kTileWorlds * (kNQ + kNV + kAct) + kObs; idx += kPolicyThreads) {
@@ -405,7 +406,9 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
       } else {
         const int i = idx - kTileWorlds * (kNQ + kNV + kAct);
         v = a.mean[i];
-        Sdiv[i] = sqrtf(a.var[i] + 1e-8f);
+        const float dv = sqrtf(a.var[i] + 1e-8f);
+        Sdiv[i] = dv;
+        Srcp[i] = rcp_rn(dv);
       }
       Sq[idx] = v;
     }
@@ -417,7 +420,7 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
       if (w < a.N) {
         const float o = obs_value(Sq + m * kNQ, Sv + m * kNV, Sp + m * kAct, i);
         if (a.t < a.H) a.O[((long)a.t * a.N + w) * kObs + i] = o;
-        z = (o - Smean[i]) / Sdiv[i];
+        z = div_rn(o - Smean[i], Sdiv[i], Srcp[i]);
         if (z < -10.f) z = -10.f; else if (z > 10.f) z = 10.f;
       }
       X[m * kLdx + kperm(i)] = z;
@@ -462,18 +465,30 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
   float* lpt = (head == in) ? out : in;   // [32][kAct] log-prob terms
   const bool sample = !a.mu_out && a.t < a.H;
   if (sample) {
+    // one thread per (world, action pair 2p, 2p + 1): both Box-Muller normals of one draw
     const float LOG2PI = 1.8378770664093453f;
-    for (int idx = tid; idx < kTileWorlds * kAct; idx += kPolicyThreads) {
-      const int m = idx / kAct, i = idx - m * kAct;
-      const int w = w0 + m;
-      if (w < a.N) {
-        const float* h = head + m * kLdx;
-        const float ls = a.pp.log_std[i];
-        const float sd = expf(ls);
-        const long ab = ((long)a.t * a.N + w) * kAct;
-        const float nz = a.act_noise ? a.act_noise[ab + i] : rng_normal(a.seed, w, a.rng[w], kStreamAction, i);
-        a.A[ab + i] = h[i] + sd * nz;
-        lpt[m * kAct + i] = -0.5f * nz * nz - ls - 0.5f * LOG2PI;
+    constexpr int kPairs = (kAct + 1) / 2;
+    static_assert(kTileWorlds * kPairs <= kPolicyThreads, "one pass");
+    const int m = tid / kPairs, pi = tid - m * kPairs;
+    const int w = w0 + m;
+    if (m < kTileWorlds && w < a.N) {
+      const float* h = head + m * kLdx;
+      const long ab = ((long)a.t * a.N + w) * kAct;
+      float nz[2];
+      if (a.act_noise) {
+        nz[0] = a.act_noise[ab + 2 * pi];
+        nz[1] = 2 * pi + 1 < kAct ? a.act_noise[ab + 2 * pi + 1] : 0.f;
+      } else {
+        rng_normal2(a.seed, w, a.rng[w], kStreamAction, pi, nz[0], nz[1]);
+      }
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int i = 2 * pi + e;
+        if (i < kAct) {
+          const float ls = a.pp.log_std[i];
+          a.A[ab + i] = h[i] + expf(ls) * nz[e];
+          lpt[m * kAct + i] = -0.5f * nz[e] * nz[e] - ls - 0.5f * LOG2PI;
+        }
       }
     }
     __syncthreads();

@@ -87,10 +87,16 @@ __host__ __device__ __forceinline__ float u01(unsigned v) { return ((v >> 8) + 0
 
 enum RngStream : unsigned { kStreamAction = 0, kStreamReset = 1, kStreamInit = 2 };
 
-__device__ __forceinline__ float rng_normal(unsigned long long seed, int w, unsigned step, unsigned stream, int i) {
+// the two standard normals of one Box-Muller draw (counter index i: actions 2i and 2i + 1)
+__device__ __forceinline__ void rng_normal2(unsigned long long seed, int w, unsigned step, unsigned stream, int i,
+                                            float& z0, float& z1) {
   U4 r = philox4x32_10(U4{(unsigned)w, step, stream, (unsigned)i}, (unsigned)seed, (unsigned)(seed >> 32));
   const float u1 = u01(r.x), u2 = u01(r.y);
-  return sqrtf(-2.f * logf(u1)) * cosf(6.2831853071795864f * u2);
+  const float rad = sqrtf(-2.f * logf(u1));
+  float sn, cs;
+  sincosf(6.2831853071795864f * u2, &sn, &cs);
+  z0 = rad * cs;
+  z1 = rad * sn;
 }
 __device__ __forceinline__ float rng_pm1(unsigned long long seed, int w, unsigned step, unsigned stream, int i) {
   U4 r = philox4x32_10(U4{(unsigned)w, step, stream, (unsigned)i}, (unsigned)seed, (unsigned)(seed >> 32));
