@@ -61,6 +61,7 @@ constexpr int kPhysThreads = 64;   // one wave64 = two 32-lane world groups
 constexpr int kXcds = 8;           // XCDs of the MI355X
 constexpr int kQueues = 32;        // work queues, kQueues / kXcds per XCD (spreads the claim atomics)
 constexpr unsigned kSpinLimit = 1u << 22;
+constexpr int kStepChunks = 4;     // host-step copies between pageable and pinned memory, pipelined
 
 // Substep chunks of a control step (the work items of one pair): pairs of substeps, except that
 // the last two substeps are single items (S = 10: 2, 2, 2, 2, 1, 1). Short last items shorten the
@@ -620,7 +621,8 @@ struct EnvState {
   unsigned* rng;
   float *dact, *zero_act, *bench_r, *bench_d;
   float* dout;            // host-step outputs on the device: [obs N x 100 | reward N | done N]
-  float *h_act, *h_out;   // pinned host staging of the host-step path (actions in, outputs out)
+  float *h_act, *h_out;   // pinned host staging of the host-step path: actions in; obs, reward, done, queue error out
+  hipEvent_t step_ev[kStepChunks + 1];   // host-step output copies done: observation chunks, reward/done
   float* Wp;
   long Wp_cap;
   unsigned long long* ncon_hist;
@@ -756,11 +758,15 @@ static void launch_physics(EnvState* E, PhysArgs& a) {
 }
 
 // nonzero if a physics launch saw a dependency wait exceed its bound (results then undefined)
+static void check_queue_error(int err) {
+  if (err == 1) fail("physics work queue: a dependency wait exceeded its bound");
+  if (err) fail("physics work queue: a block ran outside the XCD its queue was placed on");
+}
+
 static void check_queue(EnvState* E) {
   int err = 0;
   HIPCHECK(hipMemcpy(&err, E->qerr, sizeof(int), hipMemcpyDeviceToHost));
-  if (err == 1) fail("physics work queue: a dependency wait exceeded its bound");
-  if (err) fail("physics work queue: a block ran outside the XCD its queue was placed on");
+  check_queue_error(err);
 }
 
 static void rollout_impl(EnvState* E, int H, const float* W, const float* mean, const float* var, float* O, float* A,
@@ -840,7 +846,8 @@ void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
   }
   HIPCHECK(hipMalloc(&E->dout, (size_t)N * (kObs + 2) * 4));
   HIPCHECK(hipHostMalloc((void**)&E->h_act, (size_t)N * kAct * 4, hipHostMallocDefault));
-  HIPCHECK(hipHostMalloc((void**)&E->h_out, (size_t)N * (kObs + 2) * 4, hipHostMallocDefault));
+  HIPCHECK(hipHostMalloc((void**)&E->h_out, ((size_t)N * (kObs + 2) + 1) * 4, hipHostMallocDefault));
+  for (hipEvent_t& e : E->step_ev) HIPCHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   HIPCHECK(hipMemset(E->zero_act, 0, (size_t)N * kAct * 4));
   HIPCHECK(hipMemset(E->rng, 0, (size_t)N * 4));
   HIPCHECK(hipMemset(E->ncon_hist, 0, 9 * sizeof(unsigned long long)));
@@ -865,6 +872,7 @@ void g1_env_destroy(void* h) {
   if (E->h_act) HIPCHECK(hipHostFree(E->h_act));
   if (E->h_out) HIPCHECK(hipHostFree(E->h_out));
   for (auto e : E->ev_phys) (void)hipEventDestroy(e);
+  for (hipEvent_t e : E->step_ev) (void)hipEventDestroy(e);
   for (auto e : E->ev_pol) (void)hipEventDestroy(e);
   delete E;
 }
@@ -888,16 +896,38 @@ void g1_env_reset(void* h, float* obs_out) {
 void g1_env_step(void* h, const float* act, float* obs, float* rew, float* done) {
   EnvState* E = (EnvState*)h;
   const int N = E->N;
-  std::memcpy(E->h_act, act, (size_t)N * kAct * 4);
-  HIPCHECK(hipMemcpyAsync(E->dact, E->h_act, (size_t)N * kAct * 4, hipMemcpyHostToDevice, 0));
+  // The caller's arrays are pageable: they pass through the pinned staging in chunks of worlds,
+  // so the host copy of one chunk overlaps the DMA of another.
+  const size_t per = ((size_t)N + kStepChunks - 1) / kStepChunks;
+  for (int c = 0; c < kStepChunks; ++c) {
+    const size_t w0 = c * per, w1 = w0 + per < (size_t)N ? w0 + per : (size_t)N;
+    if (w0 >= w1) break;
+    std::memcpy(E->h_act + w0 * kAct, act + w0 * kAct, (w1 - w0) * kAct * 4);
+    HIPCHECK(hipMemcpyAsync(E->dact + w0 * kAct, E->h_act + w0 * kAct, (w1 - w0) * kAct * 4, hipMemcpyHostToDevice, 0));
+  }
   PhysArgs pa = phys_args(E);
   pa.act = E->dact; pa.t0 = 0; pa.astep = 0; pa.rstep = 0;
   pa.obs = E->dout; pa.R = E->dout + (size_t)N * kObs; pa.D = E->dout + (size_t)N * (kObs + 1);
   launch_physics(E, pa);
-  HIPCHECK(hipMemcpyAsync(E->h_out, E->dout, (size_t)N * (kObs + 2) * 4, hipMemcpyDeviceToHost, 0));
-  HIPCHECK(hipStreamSynchronize(0));
-  check_queue(E);
-  std::memcpy(obs, E->h_out, (size_t)N * kObs * 4);
+  for (int c = 0; c < kStepChunks; ++c) {
+    const size_t w0 = c * per, w1 = w0 + per < (size_t)N ? w0 + per : (size_t)N;
+    if (w0 < w1)
+      HIPCHECK(hipMemcpyAsync(E->h_out + w0 * kObs, E->dout + w0 * kObs, (w1 - w0) * kObs * 4, hipMemcpyDeviceToHost, 0));
+    HIPCHECK(hipEventRecord(E->step_ev[c], 0));
+  }
+  HIPCHECK(hipMemcpyAsync(E->h_out + (size_t)N * kObs, E->dout + (size_t)N * kObs, (size_t)N * 2 * 4,
+                          hipMemcpyDeviceToHost, 0));
+  HIPCHECK(hipMemcpyAsync(E->h_out + (size_t)N * (kObs + 2), E->qerr, sizeof(int), hipMemcpyDeviceToHost, 0));
+  HIPCHECK(hipEventRecord(E->step_ev[kStepChunks], 0));
+  for (int c = 0; c < kStepChunks; ++c) {
+    HIPCHECK(hipEventSynchronize(E->step_ev[c]));
+    const size_t w0 = c * per, w1 = w0 + per < (size_t)N ? w0 + per : (size_t)N;
+    if (w0 < w1) std::memcpy(obs + w0 * kObs, E->h_out + w0 * kObs, (w1 - w0) * kObs * 4);
+  }
+  HIPCHECK(hipEventSynchronize(E->step_ev[kStepChunks]));
+  int err;
+  std::memcpy(&err, E->h_out + (size_t)N * (kObs + 2), sizeof(int));
+  check_queue_error(err);
   std::memcpy(rew, E->h_out + (size_t)N * kObs, (size_t)N * 4);
   std::memcpy(done, E->h_out + (size_t)N * (kObs + 1), (size_t)N * 4);
 }
