@@ -94,9 +94,11 @@ __device__ __forceinline__ T ld_l2(const T* p) {
 // long after the rest have drained. Items are claimed in chunk-major order, so every pair advances
 // about equally and the launch ends within about one item of its average.
 //
-// Queue q serves the pairs p = q (mod 32) and is claimed by the blocks with blockIdx = q (mod 32).
-// Item (p, j) needs item (p, j - 1), which was claimed earlier from the same queue by a wave that
-// is running, so a wait always ends; the pair's flag counts its completed items. A wait that
+// Queue q serves the pairs p = q (mod 32) and is claimed by the blocks with blockIdx = q (mod 32);
+// a block whose queue is empty goes on with the other queues of its XCD (q + 8, q + 16, q + 24 mod
+// 32), which evens out queues that drew more pairs with contacts. Item (p, j) needs item (p, j - 1),
+// which was claimed earlier from the same queue by a wave that is running, so a wait always ends;
+// the pair's flag counts its completed items. A wait that
 // exceeds kSpinLimit polls sets qerr and continues rather than spin on.
 // Hand-over of a pair's state between items: the hardware places blocks on the 8 XCDs
 // round-robin, so all waves of queue q share the L2 of XCD q mod 8 (xlocal, verified when the env
@@ -112,10 +114,18 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
   const int q = blockIdx.x % kQueues;
   if (blockIdx.x == 0 && threadIdx.x < kQueues) a.qctr[(a.qpar ^ 1) * kQueues + threadIdx.x] = 0u;
   const int npairs = (a.N + 1) >> 1;
-  const unsigned nq = npairs > q ? (unsigned)((npairs - q + kQueues - 1) / kQueues) : 0u;
   const int nch = chunk_count(a.S);
-  const unsigned nitems = nq * (unsigned)(a.K * nch);
-  unsigned* const ctr = a.qctr + a.qpar * kQueues + q;
+  // queue qc being drained: the block's own, then the other queues of its XCD (same L2, so the
+  // hand-over below holds; every item waited for was claimed earlier by a running wave)
+  int qc = q;
+  unsigned nq, nitems;
+  unsigned* ctr;
+  auto set_queue = [&](int qq) {
+    nq = npairs > qq ? (unsigned)((npairs - qq + kQueues - 1) / kQueues) : 0u;
+    nitems = nq * (unsigned)(a.K * nch);
+    ctr = a.qctr + a.qpar * kQueues + qq;
+  };
+  set_queue(q);
   const int ai = L.hinge ? L.b - 2 : 0;
   const SolveParams P{a.pgs, a.mu, true, true};
   unsigned hcnt = 0;   // lane q < 9 counts substeps with q contacts
@@ -127,9 +137,14 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
     unsigned mine = 0;
     if (threadIdx.x == 0) mine = atomicAdd(ctr, 1u);
     const unsigned it = __builtin_amdgcn_readfirstlane(mine);
-    if (it >= nitems) break;
+    if (it >= nitems) {
+      qc = qc + kXcds < kQueues ? qc + kXcds : qc + kXcds - kQueues;
+      if (qc == q) break;
+      set_queue(qc);
+      continue;
+    }
     const int j = (int)(it / nq);
-    const int p = q + kQueues * (int)(it - (unsigned)j * nq);
+    const int p = qc + kQueues * (int)(it - (unsigned)j * nq);
     const int k = j / nch, c = j - k * nch;
     if (j > 0) {
       const unsigned want = a.fbase + (unsigned)j;
