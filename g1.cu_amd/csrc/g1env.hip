@@ -9,6 +9,7 @@
 // buffers written in place, exactly as the reference's k_rollout does (src/g1_env.cu:278-338).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -35,6 +36,8 @@ static void fail(const char* msg) {
 }
 
 // ====================================================================== physics kernels
+constexpr int kMaxChunks = 16;     // substep chunks per control step (work items of one pair)
+
 struct PhysArgs {
   float* qp; float* qv; float* pa; int* steps; unsigned* rng;
   int N, S, pgs, K;                // K control steps per launch (same action buffer row t0 + k*astep)
@@ -55,6 +58,8 @@ struct PhysArgs {
   int* qerr;                       // 1: a dependency wait exceeded kSpinLimit polls; 2: a wave of
                                    //   queue q ran outside XCD q while xlocal is set
   int xlocal;                      // queue q's waves all run on XCD q (checked at env creation)
+  int nch;                         // work items (substep chunks) per pair and control step:
+  int cst[kMaxChunks + 1];         //   chunk c = substeps [cst[c], cst[c + 1]), cst[nch] = S
 };
 
 constexpr int kPhysThreads = 64;   // one wave64 = two 32-lane world groups
@@ -62,17 +67,6 @@ constexpr int kXcds = 8;           // XCDs of the MI355X
 constexpr int kQueues = 32;        // work queues, kQueues / kXcds per XCD (spreads the claim atomics)
 constexpr unsigned kSpinLimit = 1u << 22;
 constexpr int kStepChunks = 4;     // host-step copies between pageable and pinned memory, pipelined
-
-// Substep chunks of a control step (the work items of one pair): pairs of substeps, except that
-// the last two substeps are single items (S = 10: 2, 2, 2, 2, 1, 1). Short last items shorten the
-// launch's tail; two-substep items amortise the hand-over of a pair's state. Measured at config 3
-// (N = 8192, S = 10) against uniform chunks of 1, 2, 3, 5 and 10 substeps and a 4-3-2-1 schedule.
-__host__ __device__ inline int front_pairs(int S) { return S > 2 ? (S - 2) / 2 : 0; }
-__host__ __device__ inline int chunk_count(int S) { return S - front_pairs(S); }
-__host__ __device__ inline int chunk_start(int S, int c) {
-  const int f = front_pairs(S);
-  return c <= f ? 2 * c : f + c;
-}
 
 __device__ __forceinline__ int xcc_id() { return (int)__builtin_amdgcn_s_getreg(20 | (0 << 6) | ((4 - 1) << 11)); }
 
@@ -114,7 +108,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
   const int q = blockIdx.x % kQueues;
   if (blockIdx.x == 0 && threadIdx.x < kQueues) a.qctr[(a.qpar ^ 1) * kQueues + threadIdx.x] = 0u;
   const int npairs = (a.N + 1) >> 1;
-  const int nch = chunk_count(a.S);
+  const int nch = a.nch;
   // queue qc being drained: the block's own, then the other queues of its XCD (same L2, so the
   // hand-over below holds; every item waited for was claimed earlier by a running wave)
   int qc = q;
@@ -186,7 +180,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
       energy = ld_l2(a.acc + (long)wc * kGroup + l);
       vx_sum = ld_l2(a.vxs + wc);
     }
-    const int s0 = chunk_start(a.S, c), s1 = c + 1 < nch ? chunk_start(a.S, c + 1) : a.S;
+    const int s0 = a.cst[c], s1 = a.cst[c + 1];
 #pragma unroll 1
     for (int sub = s0; sub < s1; ++sub) {
       float jtau = 0.f;
@@ -756,12 +750,43 @@ static PhysArgs phys_args(EnvState* E) {
   return a;
 }
 
+// Substep chunks of a control step, the work items of one pair. Large items amortise the hand-over
+// of a pair's state between waves; small last items shorten the launch's tail, which matters when
+// each wave holds little work. Measured at S = 10 (same-box A/B of the physics launch):
+// * 2 pairs per wave (config 3, N = 8192): 3,3,2,2 0.434 ms; 4,3,3 0.440; 3,3,2,1,1 0.442;
+//   2,2,2,2,1,1 0.444; 4,4,2 0.446; 4,3,2,1 0.448; 2 x 5 0.437; 3,3,3,1 0.457; 5,5 0.466.
+// * 32 pairs per wave (config 4, N = 131072): 6,4 5.81 ms; 5,5 5.83; 10 5.83; 4,3,3 5.86;
+//   2 x 5 5.98; 2,2,2,2,1,1 6.02.
+static void chunk_schedule(PhysArgs& a, int pgrid) {
+  const int S = a.S;
+  int n = 0, s0 = 0;
+  auto add = [&](int len) { a.cst[n++] = s0; s0 += len; };
+  const double work_per_wave = (double)((a.N + 1) / 2) * a.K / pgrid;   // pair-control-steps
+  if (work_per_wave >= 8.0) {
+    // two items: 60% of the substeps, then the rest
+    const int first = (3 * S + 4) / 5;
+    add(first);
+    if (S > first) add(S - first);
+  } else {
+    // three-substep items (longer for S > 46, within kMaxChunks) while more than four substeps
+    // remain, then two, a single one last
+    const int big = std::max(3, (S - 4 + kMaxChunks - 3) / (kMaxChunks - 2));
+    while (S - s0 > 4) add(std::min(big, S - s0 - 2));
+    while (s0 < S) add(S - s0 >= 2 ? 2 : 1);
+  }
+  a.cst[n] = S;
+  a.nch = n;
+  if (n < 1 || n > kMaxChunks || s0 != S) fail("physics launch: bad substep chunk schedule");
+  for (int c = 0; c < n; ++c)
+    if (a.cst[c + 1] <= a.cst[c]) fail("physics launch: bad substep chunk schedule");
+}
+
 // Enqueue one physics launch on the null stream; the queue state (flag base, counter row) advances
 // on the host in launch order, which is the stream's execution order.
 static void launch_physics(EnvState* E, PhysArgs& a) {
   if (a.K <= 0) fail("physics launch: K must be positive");
-  const int nch = chunk_count(a.S);
-  const long per_pair = (long)a.K * nch;
+  chunk_schedule(a, E->pgrid);
+  const long per_pair = (long)a.K * a.nch;
   if (per_pair > (1L << 30)) fail("physics launch: too many work items per pair");
   a.fbase = E->qdone;
   a.qpar = E->qpar;

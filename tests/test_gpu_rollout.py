@@ -181,7 +181,7 @@ def test_work_queue_matches_small_launch(g1):
 
 def test_work_queue_split_control_steps(g1):
     """K control steps in one launch equal K one-step launches bit for bit (the queue's items then
-    span control steps), with S = 5 substeps (items of 2, 2 and 1 substeps) and an odd world count."""
+    span control steps), with S = 5 substeps (items of 3 and 2 substeps) and an odd world count."""
     import configs
     N, S, K = 301, 5, 3
     qp, qv, pa, steps = configs.reset_states(np.random.default_rng(5), N)
@@ -201,8 +201,31 @@ def test_work_queue_split_control_steps(g1):
     assert not np.array_equal(states[0][0], qp)
 
 
+def test_work_queue_item_schedules_agree(g1):
+    """The chunk schedule follows the work per wave: 200 control steps in one launch (151 pairs x 200
+    steps over the persistent grid: at least 8 pair-steps per wave, so items of 6 and 4 substeps)
+    equal 200 one-step launches (items of 3, 3, 2 and 2 substeps) bit for bit."""
+    import configs
+    N, K = 301, 200
+    qp, qv, pa, steps = configs.reset_states(np.random.default_rng(8), N)
+    states = []
+    for split in (False, True):
+        env = g1.G1Env(N, substeps=10, pgs_iters=8, seed=4)
+        env.set_state(qp, qv, pa, steps)
+        if split:
+            for _ in range(K):
+                g1._lib.g1_env_bench_phys(env.h, 1)
+        else:
+            g1._lib.g1_env_bench_phys(env.h, K)
+        states.append(env.get_state())
+        env.close()
+    for a, b in zip(*states):
+        assert np.array_equal(a, b)
+    assert not np.array_equal(states[0][0], qp)
+
+
 def test_host_step_five_substeps_matches_oracle(g1, orc):
-    """g1_env_step with S = 5 (a control step split into work items of 2, 2 and 1 substeps, its
+    """g1_env_step with S = 5 (a control step split into work items of 3 and 2 substeps, its
     reward sums carried between items) against the oracle's control step."""
     N, S = 129, 5
     env = g1.G1Env(N, substeps=S, pgs_iters=8, seed=3)
