@@ -23,7 +23,7 @@ HBM_PEAK_GBS = 8000.0            # MI355X published HBM3E bandwidth
 RTX3090_SUBSTEPS_PER_S = 4.96e6  # reference's published fused-rollout number (N=8192, H=32, S=10)
 # HBM bytes per k_physics dispatch at config 3 from rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled
 # by the same counter on a copy of known size (profiles/k_physics_config3_pmc.md)
-PHYS_TRAFFIC_BYTES = {3: 16.95e6}
+PHYS_TRAFFIC_BYTES = {3: 16.04e6}
 
 
 def bytes_per_world_substep(c, p):
