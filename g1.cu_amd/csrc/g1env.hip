@@ -797,7 +797,8 @@ static void launch_physics(EnvState* E, PhysArgs& a) {
   E->qpar ^= 1;
 }
 
-// nonzero if a physics launch saw a dependency wait exceed its bound (results then undefined)
+// The work queue's error word (nonzero: a physics launch saw a dependency wait exceed its bound,
+// or a block off its queue's XCD; results are then undefined): print and exit, as HIP errors do.
 static void check_queue_error(int err) {
   if (err == 1) fail("physics work queue: a dependency wait exceeded its bound");
   if (err) fail("physics work queue: a block ran outside the XCD its queue was placed on");
