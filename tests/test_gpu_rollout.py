@@ -179,6 +179,28 @@ def test_work_queue_matches_small_launch(g1):
     assert not np.array_equal(big_state[0], qp)   # the worlds moved
 
 
+@pytest.mark.parametrize("n", [1, 2, 3])
+def test_rollout_of_one_to_three_worlds(g1, n):
+    """Ragged smallest sizes: a rollout of n = 1, 2, 3 worlds (one or two pairs, an odd last pair;
+    31 of the 32 work queues empty, their blocks drain the one queue of their XCD or exit) gives
+    those worlds bit for bit the trajectory they get as the first n worlds of a 64-world launch."""
+    H, N = 4, 64
+    qp, qv, pa, steps, W, mean, var, an, rn = _setup(N, H, 31)
+    runs = []
+    for m in (N, n):
+        env = g1.G1Env(m, substeps=10, pgs_iters=8, seed=5)
+        env.set_state(qp[:m], qv[:m], pa[:m], steps[:m])
+        out = _run(g1, env, W, mean, var, H, m, np.ascontiguousarray(an[:, :m]), np.ascontiguousarray(rn[:, :m]))
+        runs.append((out, env.get_state()))
+        env.close()
+    (big, big_state), (small, small_state) = runs
+    for b, s in zip(big[:6], small[:6]):
+        assert np.array_equal(b[:, :n], s)
+    assert np.array_equal(big[6][:n], small[6])
+    for b, s in zip(big_state, small_state):
+        assert np.array_equal(b[:n], s)
+
+
 def test_work_queue_split_control_steps(g1):
     """K control steps in one launch equal K one-step launches bit for bit (the queue's items then
     span control steps), with S = 5 substeps (items of 3 and 2 substeps) and an odd world count."""
