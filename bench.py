@@ -8,7 +8,6 @@ A "step" is one fused rollout (one g1_rollout call: H control steps x S substeps
 with the policy weights and frozen statistics already resident in HBM. Prints ONE JSON line.
 """
 import argparse
-import ctypes
 import json
 import os
 import sys
@@ -16,6 +15,7 @@ import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "g1.cu_amd", "scripts"))
+sys.path.insert(0, os.path.join(ROOT, "g1.cu_amd"))
 
 import numpy as np  # noqa: E402
 
@@ -73,11 +73,11 @@ def main():
 
     import torch
     import configs
-    import ppo
+    import g1env
     cfg = configs.ROLLOUT_CONFIGS[args.config]
     N, H, S, pgs = cfg["N"], cfg["H"], cfg["S"], cfg["pgs"]
     rng = np.random.default_rng(1234)
-    env = ppo.G1Env(N, substeps=S, pgs_iters=pgs, seed=1)
+    env = g1env.Env(N, substeps=S, pgs_iters=pgs, seed=1)
     env.set_policy(cfg["hidden"], cfg["act"])
     env.reset()
     if args.policy == "trained":
@@ -89,33 +89,31 @@ def main():
     else:
         W = torch.from_numpy(configs.policy_init(rng, hidden=cfg["hidden"])).cuda()
         mean = torch.zeros(100, device="cuda"); var = torch.ones(100, device="cuda")
-    O = torch.zeros(H, N, 100, device="cuda"); A = torch.zeros(H, N, 29, device="cuda")
-    LP, V, R, D = (torch.zeros(H, N, device="cuda") for _ in range(4))
-    Vlast = torch.zeros(N, device="cuda")
-    ptrs = [ppo._dp(t) for t in (W, mean, var, O, A, LP, V, R, D, Vlast)]
+    traj = g1env.Trajectory(H, N)
 
     def rollout():
-        ppo._lib.g1_rollout(env.h, H, *ptrs)
+        traj.run(env, W, mean, var)
 
     for _ in range(args.warmup):
         rollout()
     torch.cuda.synchronize()
     env.ncon_hist(enable=True)
-    ppo._lib.g1_env_profile(env.h, 1)
+    env.profile(1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         rollout()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    prof = (ctypes.c_double * 4)()
-    ppo._lib.g1_env_profile_read(env.h, prof)
-    ppo._lib.g1_env_profile(env.h, 0)
+    pr = env.profile_read()
+    env.profile(0)
     hist = env.ncon_hist(enable=False)
+    if env.check() != 0:
+        sys.exit("physics work queue error: results undefined")
     ms_rollout = wall * 1e3 / args.steps
     substeps_per_s = N * H * S / (wall / args.steps)
 
-    phys_ms, phys_n, pol_ms, pol_n = prof[0], int(prof[1]), prof[2], int(prof[3])
+    phys_ms, phys_n, pol_ms = pr["physics_ms"], pr["physics_launches"], pr["policy_ms"]
     nsub = hist.sum()
     bytes_total = sum(int(hist[c]) * bytes_per_world_substep(c, pgs) for c in range(9))
     launches = phys_n

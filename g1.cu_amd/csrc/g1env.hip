@@ -645,6 +645,8 @@ struct EnvState {
   int qpar;         // counter row of the next launch
   int pgrid;        // persistent grid: resident blocks of k_physics, a multiple of kQueues
   int xlocal;       // blocks land on XCD blockIdx % kXcds (measured at creation)
+  int fences;       // 1: hand over state with agent-scope fences even where xlocal holds
+  int* h_qerr;      // pinned copy of qerr, refreshed asynchronously after every rollout
   // per-launch HIP events of the rollout's physics / policy kernels (null stream)
   int prof_on;
   std::vector<hipEvent_t> ev_phys, ev_pol;
@@ -790,7 +792,7 @@ static void launch_physics(EnvState* E, PhysArgs& a) {
   if (per_pair > (1L << 30)) fail("physics launch: too many work items per pair");
   a.fbase = E->qdone;
   a.qpar = E->qpar;
-  a.xlocal = E->xlocal;
+  a.xlocal = E->xlocal && !E->fences;
   hipLaunchKernelGGL(k_physics, dim3((unsigned)E->pgrid), dim3(kPhysThreads), 0, 0, a);
   HIPCHECK(hipGetLastError());
   E->qdone += (unsigned)per_pair;
@@ -810,10 +812,19 @@ static void check_queue(EnvState* E) {
   check_queue_error(err);
 }
 
+// The asynchronous entry points (g1_rollout*) end with a copy of the error word into pinned host
+// memory; every later entry reads that copy without synchronising, so an error stops the caller at
+// its next call into the library once the copy has landed (and at the latest in g1_env_destroy or
+// at the next synchronising call, which read the device word itself).
+static void poll_queue_error(EnvState* E) {
+  check_queue_error(*(volatile int*)E->h_qerr);
+}
+
 static void rollout_impl(EnvState* E, int H, const float* W, const float* mean, const float* var, float* O, float* A,
                          float* LP, float* V, float* R, float* D, float* Vlast, const float* act_noise,
                          const float* reset_noise) {
-  if (H <= 0) fail("g1_rollout: H must be positive");
+  poll_queue_error(E);
+  if (H < 0) H = 0;   // no control step; the bootstrap value is still computed (as the reference's k_rollout)
   PackedPolicy pp;
   pack_policy(E, W, &pp);
   PhysArgs pa = phys_args(E);
@@ -830,6 +841,7 @@ static void rollout_impl(EnvState* E, int H, const float* W, const float* mean, 
   if (prof) prof_mark(E->ev_pol, E->n_pol);
   launch_policy(E, pp, H, H, mean, var, act_noise, O, A, LP, V, Vlast);
   if (prof) prof_mark(E->ev_pol, E->n_pol);
+  HIPCHECK(hipMemcpyAsync(E->h_qerr, E->qerr, sizeof(int), hipMemcpyDeviceToHost, 0));
 }
 
 extern "C" {
@@ -888,6 +900,8 @@ void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
   HIPCHECK(hipMalloc(&E->dout, (size_t)N * (kObs + 2) * 4));
   HIPCHECK(hipHostMalloc((void**)&E->h_act, (size_t)N * kAct * 4, hipHostMallocDefault));
   HIPCHECK(hipHostMalloc((void**)&E->h_out, ((size_t)N * (kObs + 2) + 1) * 4, hipHostMallocDefault));
+  HIPCHECK(hipHostMalloc((void**)&E->h_qerr, sizeof(int), hipHostMallocDefault));
+  *E->h_qerr = 0;
   for (hipEvent_t& e : E->step_ev) HIPCHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   HIPCHECK(hipMemset(E->zero_act, 0, (size_t)N * kAct * 4));
   HIPCHECK(hipMemset(E->rng, 0, (size_t)N * 4));
@@ -905,6 +919,7 @@ void g1_env_destroy(void* h) {
   EnvState* E = (EnvState*)h;
   if (!E) return;
   HIPCHECK(hipDeviceSynchronize());
+  check_queue(E);
   void* bufs[] = {E->qp,       E->qv,      E->pa,        E->steps,   E->rng,  E->dact,
                   E->zero_act, E->bench_r, E->bench_d,   E->ncon_hist, E->Wp,  E->dout,
                   E->qflags,   E->qctr,    E->qerr,      E->qacc_e,  E->qacc_vx};
@@ -912,6 +927,7 @@ void g1_env_destroy(void* h) {
     if (b) HIPCHECK(hipFree(b));
   if (E->h_act) HIPCHECK(hipHostFree(E->h_act));
   if (E->h_out) HIPCHECK(hipHostFree(E->h_out));
+  if (E->h_qerr) HIPCHECK(hipHostFree(E->h_qerr));
   for (auto e : E->ev_phys) (void)hipEventDestroy(e);
   for (hipEvent_t e : E->step_ev) (void)hipEventDestroy(e);
   for (auto e : E->ev_pol) (void)hipEventDestroy(e);
@@ -920,6 +936,7 @@ void g1_env_destroy(void* h) {
 
 void g1_env_reset(void* h, float* obs_out) {
   EnvState* E = (EnvState*)h;
+  poll_queue_error(E);
   const int N = E->N;
   hipLaunchKernelGGL(k_reset, dim3((N + 255) / 256), dim3(256), 0, 0, E->qp, E->qv, E->pa, E->steps, E->rng, N, 0.02f,
                      (const float*)nullptr, E->seed);
@@ -936,6 +953,7 @@ void g1_env_reset(void* h, float* obs_out) {
 // one launch that also writes the observation, one device-to-host copy of [obs | reward | done].
 void g1_env_step(void* h, const float* act, float* obs, float* rew, float* done) {
   EnvState* E = (EnvState*)h;
+  poll_queue_error(E);
   const int N = E->N;
   // The caller's arrays are pageable: they pass through the pinned staging in chunks of worlds,
   // so the host copy of one chunk overlaps the DMA of another.
@@ -985,6 +1003,8 @@ void g1_rollout_ex(void* h, int H, const float* W, const float* mean, const floa
 
 void g1_env_bench_phys(void* h, int K) {
   EnvState* E = (EnvState*)h;
+  poll_queue_error(E);
+  if (K <= 0) return;   // no control step (the reference's loop runs zero times)
   PhysArgs pa = phys_args(E);
   pa.K = K; pa.act = E->zero_act; pa.t0 = 0; pa.astep = 0; pa.rstep = 0; pa.R = E->bench_r; pa.D = E->bench_d;
   launch_physics(E, pa);
@@ -1028,6 +1048,7 @@ void g1_occupancy_report(void) {
 // ---- additive exports (no counterpart in the reference ABI) --------------------------------
 void g1_env_set_state(void* h, const float* qp, const float* qv, const float* pa, const int* steps) {
   EnvState* E = (EnvState*)h;
+  poll_queue_error(E);
   const size_t N = E->N;
   HIPCHECK(hipMemcpy(E->qp, qp, N * kNQ * 4, hipMemcpyHostToDevice));
   HIPCHECK(hipMemcpy(E->qv, qv, N * kNV * 4, hipMemcpyHostToDevice));
@@ -1102,6 +1123,22 @@ void g1_env_profile_read(void* h, double* out4) {
     tq += ms;
   }
   out4[0] = tp; out4[1] = (double)(E->n_phys / 2); out4[2] = tq; out4[3] = (double)(E->n_pol / 2);
+}
+
+int g1_env_check(void* h) {
+  EnvState* E = (EnvState*)h;
+  HIPCHECK(hipDeviceSynchronize());
+  int err = 0;
+  HIPCHECK(hipMemcpy(&err, E->qerr, sizeof(int), hipMemcpyDeviceToHost));
+  return err;
+}
+
+int g1_env_set_handover(void* h, int fences) {
+  EnvState* E = (EnvState*)h;
+  if (fences != 0 && fences != 1) return -1;
+  if (!fences && !E->xlocal) return -1;   // the L2 hand-over needs the round-robin placement
+  E->fences = fences;
+  return 0;
 }
 
 void g1_probe_qacc(int n, float* qpos, float* qvel, const float* tau, int damped, int contact, int pgs, float mu,

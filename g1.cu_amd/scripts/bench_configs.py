@@ -14,6 +14,9 @@ config 2  N=8192 contact solve on config-2 states (0..8 penetrating spheres, mu=
           qacc evaluations/s with the realised contact histogram, relerr against the fp32 oracle;
           CPU oracle evaluations/s.
 config 3/4 CPU oracle rollout world-substeps/s at N=1024 (the GPU numbers come from bench.py).
+standing  the physics-only bench of the reference (scripts/bench_env_phys.py: g1_env_bench_phys
+          after g1_env_reset, zero action, S=10, pgs=8) at N=8192 and 16384: substeps/s and the
+          contact-count histogram of the standing robot (continuous foot contact).
 Prints one JSON object per line.
 """
 import argparse
@@ -25,6 +28,7 @@ import time
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, HERE)
+sys.path.insert(0, os.path.dirname(HERE))
 
 import numpy as np  # noqa: E402
 
@@ -53,7 +57,7 @@ def main():
     args = ap.parse_args()
     import torch
     import configs
-    import ppo
+    import g1env
     orc = _oracle()
     T = args.cpu_threads
     dev = "cuda"
@@ -66,7 +70,7 @@ def main():
     q = torch.from_numpy(qp.astype(np.float32)).to(dev); v = torch.from_numpy(qv.astype(np.float32)).to(dev)
     t = torch.from_numpy(tau.astype(np.float32)).to(dev)
     qa = torch.zeros(len(qp), 35, device=dev); nc = torch.zeros(len(qp), dtype=torch.int32, device=dev)
-    ppo._lib.g1_probe_qacc(len(qp), ppo._dp(q), ppo._dp(v), ppo._dp(t), 0, 0, 0, 0.6, ppo._dp(qa), ppo._dp(nc))
+    g1env.lib.g1_probe_qacc(len(qp), g1env.dev_ptr(q), g1env.dev_ptr(v), g1env.dev_ptr(t), 0, 0, 0, 0.6, g1env.dev_ptr(qa), g1env.dev_ptr(nc))
     torch.cuda.synchronize()
     out(dict(config=0, cpu_fp64_us_per_state=t64 / len(qp) * 1e6, cpu_threads=1,
              gpu_fp32_vs_fp64_worst_relerr=float(relerr_rows(qa.cpu().numpy(), ref64).max())))
@@ -82,8 +86,8 @@ def main():
 
     def run_c1(dq_, dv_, n):
         for k in range(SUB // HOLD):
-            ppo._lib.g1_dynamics_bench(n, ppo._dp(dq_), ppo._dp(dv_), ppo._dp(dts[k][:n]), HOLD, 0, 0, 1, 8, 0.6,
-                                       ppo._dp(qa), ppo._dp(nc))
+            g1env.lib.g1_dynamics_bench(n, g1env.dev_ptr(dq_), g1env.dev_ptr(dv_), g1env.dev_ptr(dts[k][:n]), HOLD, 0, 0, 1, 8, 0.6,
+                                       g1env.dev_ptr(qa), g1env.dev_ptr(nc))
     run_c1(dq.clone(), dv.clone(), N); torch.cuda.synchronize()   # warm-up
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(); run_c1(dq, dv, N); e1.record(); torch.cuda.synchronize()
@@ -111,7 +115,7 @@ def main():
     q = torch.from_numpy(qp2.astype(np.float32)).to(dev); v = torch.from_numpy(qv2.astype(np.float32)).to(dev)
     t0 = torch.zeros(N, 35, device=dev)
     qa = torch.zeros(N, 35, device=dev); nc = torch.zeros(N, dtype=torch.int32, device=dev)
-    call = lambda: ppo._lib.g1_probe_qacc(N, ppo._dp(q), ppo._dp(v), ppo._dp(t0), 0, 1, 8, 1.0, ppo._dp(qa), ppo._dp(nc))
+    call = lambda: g1env.lib.g1_probe_qacc(N, g1env.dev_ptr(q), g1env.dev_ptr(v), g1env.dev_ptr(t0), 0, 1, 8, 1.0, g1env.dev_ptr(qa), g1env.dev_ptr(nc))
     call(); torch.cuda.synchronize()
     reps = 50
     e0.record()
@@ -133,7 +137,7 @@ def main():
     # ---------------- config 3 through the host-step path: H control steps of g1_env_step with host
     # numpy buffers (the reference's non-fused loop, scripts/ppo.py evaluate / DEVLOG's host-loop rollout)
     N3, H3 = 8192, 32
-    env = ppo.G1Env(N3, substeps=10, pgs_iters=8, seed=1)
+    env = g1env.Env(N3, substeps=10, pgs_iters=8, seed=1)
     env.reset()
     acts = np.random.default_rng(2).normal(0, 0.5, (H3, N3, 29)).astype(np.float32)
     for t in range(4):
@@ -145,6 +149,24 @@ def main():
     env.close()
     out(dict(config="3-host-step", N=N3, H=H3, ms_per_rollout=dt_h * 1e3, ms_per_step=dt_h * 1e3 / H3,
              substeps_per_s=N3 * H3 * 10 / dt_h))
+
+    # ---------------- standing regime: physics-only bench after reset with zero action (reference
+    # scripts/bench_env_phys.py: 5 warm-up control steps, then K = 50 timed)
+    for n_st in (8192, 16384):
+        with g1env.Env(n_st, substeps=10, pgs_iters=8, seed=1) as env:
+            env.reset()
+            env.bench_phys(5)
+            env.ncon_hist(enable=True)
+            t0 = time.perf_counter()
+            env.bench_phys(50)
+            dt_s = time.perf_counter() - t0
+            hist = env.ncon_hist(enable=False)
+            assert env.check() == 0
+        contact = hist[1:].sum()
+        out(dict(config="standing-physics", N=n_st, K=50, S=10, ms=dt_s * 1e3,
+                 substeps_per_s=n_st * 50 * 10 / dt_s, ncon_hist=hist.tolist(),
+                 share_ncon_6_7_8_of_contact_substeps=float(hist[6:9].sum() / max(contact, 1)),
+                 mean_ncon=float((hist * np.arange(9)).sum() / max(hist.sum(), 1))))
 
     # ---------------- configs 3 and 4: CPU oracle rollout rate (GPU: bench.py)
     if not args.skip_cpu:

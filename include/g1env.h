@@ -31,7 +31,9 @@ void g1_env_step(void* h, const float* act, float* obs, float* rew, float* done)
 
 /* Fused rollout of H control steps. All pointers DEVICE: W packed policy (torch order W0,b0,W1,b1,
  * Wmu,bmu,Wv,bv,log_std), mean/var [100] frozen obs stats; outputs O [H*N*100] (raw obs),
- * A [H*N*29], LP/V/R/D [H*N], Vlast [N]. Asynchronous on the null stream.
+ * A [H*N*29], LP/V/R/D [H*N], Vlast [N]. Asynchronous on the null stream. H <= 0 runs no control
+ * step and writes only Vlast, as the reference's loop does. A work-queue error of the rollout
+ * (see g1_env_check) stops the process at the caller's next call into the library.
  * (src/g1_env.cu:446-453, k_rollout :278-338) */
 void g1_rollout(void* h, int H, const float* W, const float* mean, const float* var, float* O, float* A,
                 float* LP, float* V, float* R, float* D, float* Vlast);
@@ -42,8 +44,8 @@ void g1_env_qpos(void* h, float* out);
 /* All worlds' qpos to HOST out [N*36].  (src/g1_env.cu:464-467) */
 void g1_env_qpos_all(void* h, float* out);
 
-/* K control steps of zero-action physics (reward/termination/auto-reset included). Blocks.
- * (src/g1_env.cu:385-389, k_phys_bench :343-359) */
+/* K control steps of zero-action physics (reward/termination/auto-reset included). Blocks; K <= 0
+ * does nothing.  (src/g1_env.cu:385-389, k_phys_bench :343-359) */
 void g1_env_bench_phys(void* h, int K);
 
 /* Print registers, scratch, LDS and occupancy of the kernels.  (src/g1_env.cu:365-382) */
@@ -86,6 +88,17 @@ void g1_env_ncon_hist(void* h, int enable, unsigned long long* out9);
  * {physics ms total, physics launches, policy ms total, policy launches}. */
 void g1_env_profile(void* h, int enable);
 void g1_env_profile_read(void* h, double* out4);
+
+/* Wait for the device and return the physics work queue's error word: 0 = no error, 1 = a
+ * dependency wait between work items exceeded its bound, 2 = a block ran off the XCD its queue was
+ * placed on. Results of the launches since the error are undefined. Does not exit. */
+int g1_env_check(void* h);
+
+/* State hand-over between the physics work items: fences = 0 hands a world pair's state over in
+ * the L2 of its queue's XCD (the default; needs the round-robin block placement verified at
+ * creation), fences = 1 uses agent-scope release/acquire fences (correct on any placement,
+ * slower). Returns 0, or -1 when the mode is unavailable. */
+int g1_env_set_handover(void* h, int fences);
 
 /* Parity probes running the same device code as the rollout on caller states (all DEVICE,
  * asynchronous): n worlds, qpos [n*36], qvel [n*35], qacc out [n*35], ncon out [n].

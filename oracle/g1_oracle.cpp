@@ -149,28 +149,38 @@ template <class R> static inline V3<R> ldv(const R* p) { return {p[0], p[1], p[2
 // This restatement composes the same per-body transforms (translation body_pos, rotation
 // body_quat (x) rot(axis, qpos); the pelvis: its free-joint pose) by ancestor doubling, the
 // association the GPU uses: round r sets T_b <- T_a o T_b with a the 2^r-th ancestor of b, reading
-// the transforms of the previous round (tree.h). Only the fp rounding association differs from the
-// reference's recursion; it is pinned, like the recursion was, against the MuJoCo frames of
-// bench/ref_traj.npz, and tests/test_oracle_fixtures.py checks the fp32 doubling against the
-// fp32 root -> leaf recursion (fk_recursive below).
+// the transforms of the previous round (tree.h). The per-body transforms are formed in R; the
+// compositions and the inertial-frame offsets run in fp64 for both instantiations and the frames
+// are rounded to R once. In fp32 that keeps the world frames within about one rounding of the exact
+// ones: the foot-ground contact is stiff in the foot height, and fp32 compositions (either
+// association) move qacc on MuJoCo's contact fixture by up to 2.2e-5 (root -> leaf) or 2.9e-5
+// (doubling) relative, fp64 compositions by 1.3e-5 (fp64 everywhere: 9.2e-6). The fp64
+// instantiation is pinned against the MuJoCo frames of bench/ref_traj.npz, and
+// tests/test_oracle_fixtures.py checks the fp32 frames against the fp32 root -> leaf recursion
+// (fk_recursive below).
 template <class R> void fk(const R* qpos, R* xpos, R* xquat, R* xipos) {
-  V3<R> tp[kNBody];
-  Q4<R> tq[kNBody];
+  using C = double;   // composition precision
+  V3<C> tp[kNBody];
+  Q4<C> tq[kNBody];
   tp[0] = {0, 0, 0};
   tq[0] = {1, 0, 0, 0};
   for (int b = 1; b < kNBody; ++b) {
     const int j = body_jntadr[b], qa = jnt_qposadr[j];
+    V3<R> p;
+    Q4<R> q;
     if (jnt_type[j] == 0) {
-      tp[b] = {qpos[qa], qpos[qa + 1], qpos[qa + 2]};
-      tq[b] = qnorm(Q4<R>{qpos[qa + 3], qpos[qa + 4], qpos[qa + 5], qpos[qa + 6]});
+      p = {qpos[qa], qpos[qa + 1], qpos[qa + 2]};
+      q = qnorm(Q4<R>{qpos[qa + 3], qpos[qa + 4], qpos[qa + 5], qpos[qa + 6]});
     } else {
-      tp[b] = ldv(&M<R>::body_pos[3 * b]);
-      tq[b] = qmul(ldq(&M<R>::body_quat[4 * b]), axisangle(ldv(&M<R>::jnt_axis[3 * j]), qpos[qa]));
+      p = ldv(&M<R>::body_pos[3 * b]);
+      q = qmul(ldq(&M<R>::body_quat[4 * b]), axisangle(ldv(&M<R>::jnt_axis[3 * j]), qpos[qa]));
     }
+    tp[b] = {C(p.x), C(p.y), C(p.z)};
+    tq[b] = {C(q.w), C(q.x), C(q.y), C(q.z)};
   }
   for (int r = 0; r < kFkRounds; ++r) {
-    V3<R> op[kNBody];
-    Q4<R> oq[kNBody];
+    V3<C> op[kNBody];
+    Q4<C> oq[kNBody];
     std::copy(tp, tp + kNBody, op);
     std::copy(tq, tq + kNBody, oq);
     for (int b = 1; b < kNBody; ++b) {
@@ -182,10 +192,12 @@ template <class R> void fk(const R* qpos, R* xpos, R* xquat, R* xipos) {
     }
   }
   for (int b = 0; b < kNBody; ++b) {
-    xpos[3 * b] = tp[b].x; xpos[3 * b + 1] = tp[b].y; xpos[3 * b + 2] = tp[b].z;
-    xquat[4 * b] = tq[b].w; xquat[4 * b + 1] = tq[b].x; xquat[4 * b + 2] = tq[b].y; xquat[4 * b + 3] = tq[b].z;
-    V3<R> cw = vadd(tp[b], qrot(tq[b], ldv(&M<R>::body_ipos[3 * b])));
-    xipos[3 * b] = cw.x; xipos[3 * b + 1] = cw.y; xipos[3 * b + 2] = cw.z;
+    xpos[3 * b] = R(tp[b].x); xpos[3 * b + 1] = R(tp[b].y); xpos[3 * b + 2] = R(tp[b].z);
+    xquat[4 * b] = R(tq[b].w); xquat[4 * b + 1] = R(tq[b].x); xquat[4 * b + 2] = R(tq[b].y);
+    xquat[4 * b + 3] = R(tq[b].z);
+    const V3<R> ip = ldv(&M<R>::body_ipos[3 * b]);
+    V3<C> cw = vadd(tp[b], qrot(tq[b], V3<C>{C(ip.x), C(ip.y), C(ip.z)}));
+    xipos[3 * b] = R(cw.x); xipos[3 * b + 1] = R(cw.y); xipos[3 * b + 2] = R(cw.z);
   }
   xipos[0] = xipos[1] = xipos[2] = 0;
 }

@@ -6,7 +6,8 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = os.path.join(ROOT, "tests", "golden")
-for p in (os.path.join(ROOT, "oracle"), os.path.join(ROOT, "g1.cu_amd", "scripts"), ROOT):
+for p in (os.path.join(ROOT, "oracle"), os.path.join(ROOT, "g1.cu_amd", "scripts"), os.path.join(ROOT, "g1.cu_amd"),
+          ROOT):
     if p not in sys.path:
         sys.path.insert(0, p)
 

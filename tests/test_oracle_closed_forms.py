@@ -208,3 +208,44 @@ def test_action_penalty_and_velocity_guard(orc):
     qv2 = np.zeros((1, 35), np.float32); qv2[0, 10] = np.nan; qv2[0, 12] = 1e4
     _advance(orc, qp2, qv2, np.zeros((1, 29), np.float32), np.zeros(1, np.int32), np.zeros((1, 29), np.float32), S=1)
     assert np.isfinite(qv2).all() and np.abs(qv2).max() <= 50.0
+
+
+def test_reward_closed_form(orc):
+    """The oracle's control-step reward equals the task's reward written out in fp64
+    (tests/reward_spec.py, from src/g1_env.cu:164-199) on states where it is known in closed form:
+    each case moves one term, so a wrong coefficient, sign, clip or gate fails by >= 1e-2."""
+    from reward_spec import crafted_cases, reward_spec
+    c = crafted_cases()
+    qp, qv, pa, st = c["qp"].copy(), c["qv"].copy(), c["pa"].copy(), c["steps"].copy()
+    noise = np.random.default_rng(1).uniform(-1, 1, (len(st), 29)).astype(np.float32)
+    r, d = _advance(orc, qp, qv, pa, st, c["act"], noise, S=10)
+    # the alive worlds' end state; done worlds are reset, so their reward needs only the flags
+    vx_mean = c["qv"][:, 0].astype(np.float64)          # free fall: constant forward speed
+    live = d == 0
+    r_spec, d_spec = reward_spec(np.where(live[:, None], qp, c["qp"]), np.where(live[:, None], qv, c["qv"]),
+                                 vx_mean, c["act"], c["pa"], c["steps"])
+    assert list(d.astype(bool)) == list(d_spec), c["names"]
+    for w in np.flatnonzero(live):
+        assert abs(float(r[w]) - r_spec[w]) <= 1e-6, (c["names"][w], r[w], r_spec[w])
+    # done worlds: the falls score exactly -5, the timeout and the finish line score their alive
+    # reward (+50 at the line); their end states are reset, so those two are checked against a twin
+    # stepped without the done condition (episode step 0; the finish-line twin at x = 4, which
+    # changes no term of the alive reward)
+    names = c["names"]
+    assert r[names.index("fallen (height)")] == -5.0 and r[names.index("fallen (tilt)")] == -5.0
+    for nm, bonus in (("timeout", 0.0), ("finish line", 50.0)):
+        w = names.index(nm)
+        q1, v1, p1 = c["qp"][w:w + 1].copy(), c["qv"][w:w + 1].copy(), c["pa"][w:w + 1].copy()
+        s1 = np.zeros(1, np.int32)
+        q1[0, 0] = min(q1[0, 0], 4.0)
+        r1, d1 = _advance(orc, q1, v1, p1, s1, c["act"][w:w + 1], noise[w:w + 1], S=10)
+        assert d1[0] == 0
+        rs, _ = reward_spec(q1, v1, vx_mean[w:w + 1], c["act"][w:w + 1], c["pa"][w:w + 1], s1)
+        # (r + 50 is rounded to fp32: one ulp of 51.5 is 3.8e-6)
+        assert abs(float(r[w]) - (rs[0] + bonus)) <= 1e-6 + float(np.spacing(np.float32(r[w]))), nm
+    # every done world restarts at the stand pose + 0.05 * its reset noise
+    import g1_model as gm
+    for w in np.flatnonzero(~live):
+        exp = gm.qpos_stand.astype(np.float32).copy()
+        exp[7:] += np.float32(0.05) * noise[w]
+        assert np.array_equal(qp[w], exp) and not qv[w].any() and not pa[w].any() and st[w] == 0
