@@ -72,7 +72,16 @@ template <class R> static inline V3<R> qrot(Q4<R> q, V3<R> v) {
 template <class R> static inline R sin_(R x) { return R(std::sin(double(x))); }
 template <class R> static inline R cos_(R x) { return R(std::cos(double(x))); }
 template <class R> static inline R pow_(R x, R y) { return R(std::pow(double(x), double(y))); }
-template <class R> static inline R rsqrt_(R x) { return R(1) / std::sqrt(x); }
+template <class R> static inline R sqrt_(R x) { return std::sqrt(x); }
+template <class R> static inline R rsqrt_(R x) { return R(1) / sqrt_(x); }
+template <class R> static inline R fabs_(R x) { return std::fabs(x); }
+template <class R> static inline bool isfinite_(R x) { return std::isfinite(x); }
+template <class R> static inline R tanh_(R x) { return std::tanh(x); }
+template <class R> static inline R expm1_(R x) { return std::expm1(x); }
+template <class R> static inline R exp_(R x) { return std::exp(x); }
+// Precision of the forward-kinematics compositions (fk below); a customisation point for the
+// operation-counting instantiation (flop_count.cpp), which counts them as its own scalar type.
+template <class R> struct ComposePrec { using type = double; };
 // (reference: src/dynamics.cuh:36-39)
 template <class R> static inline Q4<R> qnorm(Q4<R> q) {
   R n = rsqrt_(fma_(q.z, q.z, fma_(q.y, q.y, fma_(q.x, q.x, q.w * q.w))));
@@ -159,7 +168,7 @@ template <class R> static inline V3<R> ldv(const R* p) { return {p[0], p[1], p[2
 // tests/test_oracle_fixtures.py checks the fp32 frames against the fp32 root -> leaf recursion
 // (fk_recursive below).
 template <class R> void fk(const R* qpos, R* xpos, R* xquat, R* xipos) {
-  using C = double;   // composition precision
+  using C = typename ComposePrec<R>::type;   // composition precision (fp64)
   V3<C> tp[kNBody];
   Q4<C> tq[kNBody];
   tp[0] = {0, 0, 0};
@@ -341,6 +350,33 @@ template <class R> void compute_bias(const R* qvel, const Frames<R>& F, R* S, R*
   }
 }
 
+// ---------------------------------------------------------------- summation association
+// Three kinds of sum are associated differently by the GPU kernel than by the reference's serial
+// loops; the algorithm is the same and the results differ at rounding level. g_ref_order selects
+// the association: 0 (default) follows the kernel, so the fp32 oracle reproduces the kernel's
+// contact path bit for bit; 1 follows the reference's loops. The three:
+//  * the contact basis columns (M + dtB)^-1 e_{c,a}: the kernel solves them in the single
+//    right-hand-side form (reference src/aba_factor.cuh:121-165, solveM below), the reference in
+//    its K = 1 multi-RHS form (src/aba_solvem_multi.cuh:21-125, solveM_multi1);
+//  * the PGS row sum sum_j A_ij f_j: the kernel rounds each product and sums the 32 lanes of a
+//    world by an xor butterfly (16, 8, 4, 2, 1), then adds b_i; the reference accumulates
+//    b_i + A_i0 f_0 + ... serially with fused multiply-adds (src/contact.cuh:159-171);
+//  * the control step's energy and action-change penalty: the kernel sums each actuator's terms
+//    over the substeps on its own lane (lane = body = actuator + 2) and the lanes by the butterfly,
+//    the reference serially over substeps and actuators (src/g1_env.cu:150-151,186-188).
+static int g_ref_order = 0;
+
+// The value every lane of a 32-lane group holds after the kernel's group sum: the xor butterfly
+// over strides 16, 8, 4, 2, 1 (lane i adds lane i ^ m; additions commute, so lane 0's sum is
+// the pairwise tree below).
+template <class R> static inline R butterfly32(const R* v) {
+  R t[32];
+  for (int i = 0; i < 32; ++i) t[i] = v[i];
+  for (int m = 16; m >= 1; m >>= 1)
+    for (int i = 0; i < m; ++i) t[i] = t[i] + t[i + m];
+  return t[0];
+}
+
 // ---------------------------------------------------------------- packed symmetric 6x6 helpers
 // (reference: src/aba.cuh:15-27)
 static inline int symidx(int i, int j) {
@@ -423,7 +459,7 @@ template <class R> void factorize(const Frames<R>& F, const R* S, const R* Bdiag
     for (int j = 0; j <= i; ++j) {
       R s = Dm[i * 6 + j];
       for (int kk = 0; kk < j; ++kk) s = fma_(-Dm[i * 6 + kk], Dm[j * 6 + kk], s);
-      if (i == j) Dm[i * 6 + i] = std::sqrt(s); else Dm[i * 6 + j] = s / Dm[j * 6 + j];
+      if (i == j) Dm[i * 6 + i] = sqrt_(s); else Dm[i * 6 + j] = s / Dm[j * 6 + j];
     }
   for (int i = 0; i < 36; ++i) fac.Dfac6[i] = Dm[i];
 }
@@ -583,7 +619,7 @@ template <class R> void mass_matrix(const Frames<R>& F, const R* S, R* Mout) {
 template <class R> R foot_impedance(R pos) {
   const R* si = M<R>::foot_solimp;
   R dmin = si[0], dmax = si[1], width = si[2], mid = si[3], power = si[4];
-  R x = std::fabs(pos) / width;
+  R x = fabs_(pos) / width;
   R y;
   if (x >= R(1)) y = 1;
   else {
@@ -595,14 +631,22 @@ template <class R> R foot_impedance(R pos) {
 }
 
 // Projected Gauss-Seidel on min 0.5 f'Af + f'b, f >= 0 (reference: src/contact.cuh:159-171)
+// (row sum associated as selected by g_ref_order; n <= 32 in the kernel's association)
 template <class R> void solve_pgs(const R* A, const R* b, R* f, int n, int iters) {
   for (int i = 0; i < n; ++i) f[i] = 0;
   for (int it = 0; it < iters; ++it)
     for (int i = 0; i < n; ++i) {
       R Aii = A[i * n + i];
-      R ri = b[i];
-      for (int j = 0; j < n; ++j) ri = fma_(A[i * n + j], f[j], ri);
-      ri = fma_(-Aii, f[i], ri);
+      R ri;
+      if (g_ref_order || n > 32) {
+        ri = b[i];
+        for (int j = 0; j < n; ++j) ri = fma_(A[i * n + j], f[j], ri);
+        ri = fma_(-Aii, f[i], ri);
+      } else {
+        R p[32];
+        for (int j = 0; j < 32; ++j) p[j] = j < n ? A[i * n + j] * f[j] : R(0);
+        ri = fma_(-Aii, f[i], b[i] + butterfly32(p));
+      }
       R fi = -ri / Aii;
       f[i] = fi > R(0) ? fi : R(0);
     }
@@ -700,14 +744,16 @@ int env_qacc(const R* qp, const R* qv, const Frames<R>& F, const R* tau, const R
       aref[idx] = -bcoef * dkv - kip;
     }
   }
-  // PASS 2: m_{c,a} = (M + dtB)^-1 e_{c,a} (reference: src/env_qacc.cuh:143-152)
+  // PASS 2: m_{c,a} = (M + dtB)^-1 e_{c,a} (reference: src/env_qacc.cuh:143-152; solve form as
+  // selected by g_ref_order)
   R Mm[kNFoot][3][kNV];
   for (int c = 0; c < ncon; ++c)
     for (int a = 0; a < 3; ++a) {
       R basis[kNV];
       for (int i = 0; i < kNV; ++i) basis[i] = 0;
       for (int k = 0; k < cnd[c]; ++k) basis[cdof[c][k]] = Eb[c][a][k];
-      solveM_multi1(fac, S, basis, Mm[c][a]);
+      if (g_ref_order) solveM_multi1(fac, S, basis, Mm[c][a]);
+      else solveM(fac, S, basis, Mm[c][a]);
     }
   // A = J M^-1 J' + diag(R) from 3x3 Gram blocks expanded to the 4x4 pyramid blocks,
   // upper blocks copied symmetric (reference: src/env_qacc.cuh:154-192)
@@ -770,7 +816,7 @@ int env_qacc(const R* qp, const R* qv, const Frames<R>& F, const R* tau, const R
 // q <- normalize(q (x) exp(w dt)), w body-local (reference: src/dynamics.cuh:333-342)
 template <class R> void quat_integrate(R* q, V3<R> w, R dt) {
   V3<R> v{w.x * dt, w.y * dt, w.z * dt};
-  R ang = std::sqrt(fma_(v.z, v.z, fma_(v.y, v.y, v.x * v.x)));
+  R ang = sqrt_(fma_(v.z, v.z, fma_(v.y, v.y, v.x * v.x)));
   Q4<R> dq;
   if (ang < R(1e-9)) dq = {R(1), R(0.5) * v.x, R(0.5) * v.y, R(0.5) * v.z};
   else {
@@ -830,6 +876,8 @@ void env_advance(R* lp, R* lv, R* pa, int* pstep, const R* a, const R* reset_noi
   for (int i = 0; i < kNV; ++i) Bdt[i] = 0;
   for (int i = 0; i < kAct; ++i) Bdt[act_dof[i]] = dt * M<R>::act_kd[i];
   R vx_sum = 0, energy = 0;
+  R e_act[kAct];   // per-actuator energy over the substeps (kernel association)
+  for (int i = 0; i < kAct; ++i) e_act[i] = 0;
   int alive = 1;
   for (int s = 0; s < S; ++s) {
     fk(lp, F.xpos, F.xquat, F.xipos);
@@ -840,13 +888,14 @@ void env_advance(R* lp, R* lv, R* pa, int* pstep, const R* a, const R* reset_noi
       if (pdt < M<R>::act_frc_lo[i]) pdt = M<R>::act_frc_lo[i];
       else if (pdt > M<R>::act_frc_hi[i]) pdt = M<R>::act_frc_hi[i];
       tau[d] = pdt;
-      energy += std::fabs(pdt * lv[d]);
+      if (g_ref_order) energy += fabs_(pdt * lv[d]);
+      else e_act[i] += fabs_(pdt * lv[d]);
     }
     int nc = env_qacc(lp, lv, F, tau, Bdt, Sm, qacc, pgs, mu);
     if (ncon_hist) ncon_hist[nc] += 1;
     for (int i = 0; i < kNV; ++i) {
       R v = fma_(dt, qacc[i], lv[i]);
-      if (!std::isfinite(v)) v = 0;
+      if (!isfinite_(v)) v = 0;
       if (v > R(50)) v = R(50); else if (v < R(-50)) v = R(-50);
       lv[i] = v;
     }
@@ -862,11 +911,24 @@ void env_advance(R* lp, R* lv, R* pa, int* pstep, const R* a, const R* reset_noi
   R vx_c = vx > R(0.8) ? R(0.8) : vx;
   if (vx_c < R(0)) vx_c = 0;
   R r_vel = R(1) * vx_c * upc;
-  R r_lat = -R(0.2) * std::fabs(lv[1]) - R(0.05) * std::fabs(lv[5]);
+  R r_lat = -R(0.2) * fabs_(lv[1]) - R(0.05) * fabs_(lv[5]);
   R r_up = R(0.3) * upc;
-  R r_h = -R(0.5) * std::fabs(height - R(0.78));
+  R r_h = -R(0.5) * fabs_(height - R(0.78));
   R act_pen = 0;
-  for (int i = 0; i < kAct; ++i) { R da = a[i] - pa[i]; act_pen += da * da; }
+  if (g_ref_order) {
+    for (int i = 0; i < kAct; ++i) { R da = a[i] - pa[i]; act_pen += da * da; }
+  } else {
+    // actuator i on lane i + 2 (lanes 0, 1 and 31 carry no actuator)
+    R le[32], lp[32];
+    for (int k = 0; k < 32; ++k) le[k] = lp[k] = R(0);
+    for (int i = 0; i < kAct; ++i) {
+      R da = a[i] - pa[i];
+      le[i + 2] = e_act[i];
+      lp[i + 2] = da * da;
+    }
+    energy = butterfly32(le);
+    act_pen = butterfly32(lp);
+  }
   if (act_pen > R(10)) act_pen = R(10);
   R r;
   if (alive) r = R(1) + r_vel + r_lat + r_up + r_h - R(0.005) * act_pen - R(1e-4) * energy;
@@ -912,7 +974,7 @@ template <class R> void mlp_forward(const R* W, const PolicySpec& ps, const R* x
       R s = bl[o];
       const R* row = Wl + (long)o * in;
       for (int i = 0; i < in; ++i) s += row[i] * cur[i];
-      nxt[o] = ps.act == 0 ? std::tanh(s) : (s > R(0) ? s : std::expm1(s));
+      nxt[o] = ps.act == 0 ? tanh_(s) : (s > R(0) ? s : expm1_(s));
     }
     p = bl + out; in = out; cur.swap(nxt);
   }
@@ -933,7 +995,7 @@ template <class R> void mlp_forward(const R* W, const PolicySpec& ps, const R* x
 // obs normalisation with frozen stats, clamp +-10 (reference: src/g1_env.cu:298-302)
 template <class R> void normalize_obs(const R* o, const R* mean, const R* var, R* no) {
   for (int i = 0; i < kObs; ++i) {
-    R z = (o[i] - mean[i]) / std::sqrt(var[i] + R(1e-8));
+    R z = (o[i] - mean[i]) / sqrt_(var[i] + R(1e-8));
     if (z < R(-10)) z = R(-10); else if (z > R(10)) z = R(10);
     no[i] = z;
   }
@@ -958,7 +1020,7 @@ void rollout_world(int w, int N, int H, int S, int pgs, R mu_fric, R* qp, R* qv,
     R lpsum = 0;
     const R* nz = act_noise + ob * kAct;
     for (int i = 0; i < kAct; ++i) {
-      R sd = std::exp(ls[i]);
+      R sd = exp_(ls[i]);
       a[i] = mu[i] + sd * nz[i];
       lpsum += -R(0.5) * nz[i] * nz[i] - ls[i] - R(0.5) * LOG2PI;
     }
@@ -1043,7 +1105,7 @@ static void dyn_batch(int n, R* qpos, R* qvel, const R* tau, int nsub, int conta
       for (int i = 0; i < kNV; ++i) {
         R v = fma_(dt, qacc[i], lv[i]);
         if (guard) {   // (reference: src/g1_env.cu:154-160)
-          if (!std::isfinite(v)) v = 0;
+          if (!isfinite_(v)) v = 0;
           if (v > R(50)) v = R(50); else if (v < R(-50)) v = R(-50);
         }
         lv[i] = v;
@@ -1082,7 +1144,7 @@ static void substep_batch(int n, R* qpos, R* qvel, const R* target, int pgs, R m
     if (ncon) ncon[w] = nc;
     for (int i = 0; i < kNV; ++i) {
       R v = fma_(dt, qacc[i], lv[i]);
-      if (!std::isfinite(v)) v = 0;
+      if (!isfinite_(v)) v = 0;
       if (v > R(50)) v = R(50); else if (v < R(-50)) v = R(-50);
       lv[i] = v;
     }
@@ -1142,6 +1204,8 @@ template <class R> static void implicit_traj(const R* q0, const R* v0, const R* 
 }
 
 extern "C" {
+
+void orc_set_reference_order(int on) { g_ref_order = on ? 1 : 0; }
 
 void orc_smooth_traj_f(const float* q0, const float* v0, int n, float* qo, float* vo) { smooth_traj(q0, v0, n, qo, vo); }
 void orc_smooth_traj_d(const double* q0, const double* v0, int n, double* qo, double* vo) { smooth_traj(q0, v0, n, qo, vo); }

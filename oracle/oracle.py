@@ -47,6 +47,7 @@ def _load():
         getattr(lib, f"orc_smooth_traj_{suf}").argtypes = [fp, fp, _c.c_int, fp, fp]
         getattr(lib, f"orc_implicit_traj_{suf}").argtypes = [fp, fp, fp, fp, _c.c_int, fp, fp]
     lib.orc_fk_recursive_f.argtypes = [_c.c_int, _f32p, _f32p, _f32p, _f32p]
+    lib.orc_set_reference_order.argtypes = [_c.c_int]
     lib.orc_qacc_debug_f.argtypes = [_f32p, _f32p, _f32p, _c.c_void_p, _c.c_int, _c.c_float] + [_f32p] * 7
     lib.orc_qacc_debug_f.restype = _c.c_int
     lib.orc_obs_f.argtypes = [_c.c_int, _f32p, _f32p, _f32p, _f32p]
@@ -77,6 +78,23 @@ def _dt(dtype):
 
 def _arr(x, dtype):
     return np.ascontiguousarray(x, dtype=dtype)
+
+
+def set_reference_order(on):
+    """Associate the contact basis solves, the PGS row sums and the reward's energy and
+    action-penalty totals as the reference's serial loops do (on), or as the GPU kernel does (off,
+    the default). Same algorithm; the results differ at rounding level."""
+    lib().orc_set_reference_order(int(bool(on)))
+
+
+class reference_order:
+    """Context manager: the oracle in the reference's association inside the block."""
+
+    def __enter__(self):
+        set_reference_order(True)
+
+    def __exit__(self, *exc):
+        set_reference_order(False)
 
 
 def bdt(dtype=np.float32):

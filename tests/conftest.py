@@ -35,6 +35,18 @@ def load_contact_validate():
     return out
 
 
+def envqacc_states(n, seed=999):
+    """The reference gate's state family (src/test_envqacc.cu:29-39): stand pose + U(-0.2,0.2) on
+    every qpos entry, base dropped up to 0.15 m, renormalised quaternion, qvel U(-1,1)."""
+    import g1_model as gm
+    rng = np.random.default_rng(seed)
+    qp = (gm.qpos_stand.astype(np.float32)[None] + 0.2 * (rng.random((n, 36), np.float32) * 2 - 1)).astype(np.float32)
+    qp[:, 2] -= 0.15 * rng.random(n, np.float32)
+    qp[:, 3:7] /= np.linalg.norm(qp[:, 3:7], axis=1, keepdims=True)
+    qv = (rng.random((n, 35), np.float32) * 2 - 1).astype(np.float32)
+    return qp, qv
+
+
 @pytest.fixture(scope="session")
 def orc():
     import oracle

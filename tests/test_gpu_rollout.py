@@ -2,10 +2,10 @@
 the CPU oracle on identical states and pre-generated noise.
 
 Teacher forcing: every control step starts the oracle from the GPU's own state before that step
-(g1_env_get_state), so rounding differences cannot compound through the chaotic foot contacts and
-each step is held to the per-step bound: O bitwise, A/LP/V/R within 1e-5, D exact, qpos and qvel
-within 1e-5 per world (||a-b||/||b||, the reference's gate metric, src/test_envqacc.cu:74-90).
-The physics of a step is driven by the GPU's own actions, so it is checked apart from the policy.
+(g1_env_get_state). The policy runs on MFMA and its outputs are held to the per-step bound (A/LP/V
+within 1e-5, O bitwise). The physics of a step is driven by the GPU's own actions and compared bit
+for bit with the oracle in the kernel's summation association: qpos, qvel, reward, done, step
+counters and reset states.
 """
 import os
 
@@ -118,23 +118,27 @@ def _teacher_forced_run(g1, orc, env, n_check, H, W, mean, var, hidden, act, see
         gq, gv, gpa, gst = (x[k] for x in post)
         assert np.array_equal(gst, ost) and np.array_equal(gpa, opa), t
         e_q, e_qd = relerr_rows(gq, oq).max(), relerr_rows(gv, ov).max()
-        row = dict(t=t, A=e_a, LP=e_lp, V=e_v, R=e_r, qpos=e_q, qvel=e_qd, done=int(dd.sum()))
+        nbit = int((~(gq == oq).all(1) | ~(gv == ov).all(1) | (R != rr)).sum())
+        row = dict(t=t, A=e_a, LP=e_lp, V=e_v, R=e_r, qpos=e_q, qvel=e_qd, done=int(dd.sum()), nbit=nbit)
         if t in substep_probe:
             sel = np.arange(0, n_check, max(1, n_check // 256))[:256]
             row["substep"] = _substeps_teacher_forced(g1, orc, pq[sel], pv[sel], A[sel], env.S)
         rows.append(row)
         print(f"step {t:2d}: A {e_a:.1e} LP {e_lp:.1e} V {e_v:.1e} R {e_r:.1e} qpos {e_q:.1e} qvel {e_qd:.1e} "
-              f"done {row['done']}" + (f" | substeps qacc/qpos/qvel {np.array2string(row['substep'], precision=1)}"
+              f"done {row['done']} worlds not bit-identical {nbit}" + (f" | substeps qacc/qpos/qvel {np.array2string(row['substep'], precision=1)}"
                                         if "substep" in row else ""), flush=True)
     return rows
 
 
 def _assert_rows(rows):
+    """Policy outputs within 1e-5; the physics of each step (driven by the GPU's own actions) and
+    its reward bit for bit."""
     for r in rows:
-        for key in ("A", "LP", "V", "R", "qpos", "qvel"):
+        for key in ("A", "LP", "V"):
             assert r[key] <= TOL, (r["t"], key, r[key])
+        assert r["nbit"] == 0, (r["t"], r["nbit"], r["qpos"], r["qvel"], r["R"])
         if "substep" in r:
-            assert (r["substep"] <= TOL).all(), (r["t"], r["substep"])
+            assert (r["substep"] == 0).all(), (r["t"], r["substep"])
 
 
 @pytest.mark.timeout(900)
@@ -325,9 +329,9 @@ def test_reference_driver_call_sequence(g1):
 
 
 def test_host_step_matches_oracle(g1, orc):
-    """g1_env_step (host buffers) vs the oracle's control step on the same state; every world, done or
-    not, within the per-step bound (reset worlds compare their reset pose: zero injected noise is
-    not what the library draws, so those are excluded from the state check only)."""
+    """g1_env_step (host buffers) vs the oracle's control step on the same state and actions: done
+    flags, rewards and the observations of worlds still running bit for bit (a finished world
+    restarts with library noise, which the oracle does not draw)."""
     N = 128
     with g1.Env(N, substeps=10, pgs_iters=8, seed=3) as env:
         obs = env.reset()
@@ -338,9 +342,8 @@ def test_host_step_matches_oracle(g1, orc):
     oq, ov, opa, ost = qp.copy(), qv.copy(), pa.copy(), st.copy()
     rr, dd = orc.env_advance(oq, ov, opa, ost, act, np.zeros((N, 29), np.float32), threads=NTHREADS)
     live = dd == 0
-    assert np.array_equal(done, dd)
-    assert (np.abs(rew - rr) / np.maximum(1, np.abs(rr))).max() <= TOL
-    assert relerr_rows(obs1[live], orc.obs(oq, ov, opa)[live]).max() <= TOL
+    assert np.array_equal(done, dd) and np.array_equal(rew, rr)
+    assert np.array_equal(obs1[live], orc.obs(oq, ov, opa)[live])
 
 
 def test_work_queue_matches_small_launch(g1):
@@ -419,9 +422,8 @@ def test_host_step_five_substeps_matches_oracle(g1, orc):
     oq, ov, opa, ost = qp.copy(), qv.copy(), pa.copy(), st.copy()
     rr, dd = orc.env_advance(oq, ov, opa, ost, act, np.zeros((N, 29), np.float32), S=S, threads=NTHREADS)
     live = dd == 0
-    assert np.array_equal(done, dd)
-    assert (np.abs(rew - rr) / np.maximum(1, np.abs(rr))).max() <= TOL
-    assert relerr_rows(obs1[live], orc.obs(oq, ov, opa)[live]).max() <= TOL
+    assert np.array_equal(done, dd) and np.array_equal(rew, rr)
+    assert np.array_equal(obs1[live], orc.obs(oq, ov, opa)[live])
 
 
 def test_reference_trained_policy_walks(g1):

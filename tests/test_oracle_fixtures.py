@@ -141,3 +141,29 @@ def test_contact_qacc_matches_mujoco(orc, dtype, tol):
     # 8 unconverged sweeps stay far from MuJoCo: the sweep count is a real parameter
     qa8, _ = orc.qacc(cv["qpos"], cv["qvel"], pgs=8, mu=0.6, dtype=dtype)
     assert relerr_rows(qa8, cv["qacc"])[3:].min() > 1e-3
+
+
+def test_kernel_association_matches_reference_association(orc):
+    """The oracle's default association (the GPU kernel's: single-RHS contact solves, butterfly PGS
+    row sums and reward totals) against the reference's serial association: the same algorithm, so
+    per-state qacc agrees within the fp32 gate (1e-5, src/test_envqacc.cu:74-90) on the gate's
+    state family, and both meet the MuJoCo contact fixture's bound; the two are not bit-identical
+    (the switch takes effect)."""
+    from conftest import envqacc_states
+    qp, qv = envqacc_states(2048)
+    Bdt = orc.bdt(np.float32)
+    dev, nd = orc.qacc(qp, qv, Bdt=Bdt, pgs=8, mu=0.6, dtype=np.float32, threads=8)
+    with orc.reference_order():
+        ref, nr = orc.qacc(qp, qv, Bdt=Bdt, pgs=8, mu=0.6, dtype=np.float32, threads=8)
+    assert np.array_equal(nd, nr) and (nd > 0).mean() > 0.5
+    rel = relerr_rows(dev, ref)
+    assert rel.max() <= 1e-5, rel.max()
+    assert not np.array_equal(dev, ref)
+    cv = load_contact_validate()
+    for ctx in (None, orc.reference_order()):
+        if ctx:
+            ctx.__enter__()
+        qa, _ = orc.qacc(cv["qpos"], cv["qvel"], pgs=2000, mu=0.6, dtype=np.float32)
+        if ctx:
+            ctx.__exit__(None, None, None)
+        assert relerr_rows(qa, cv["qacc"]).max() < 1.5e-5
