@@ -701,16 +701,24 @@ static int max_width(const PolicyShape& sh) {
   return m;
 }
 
-static void pack_policy(EnvState* E, const float* W, PackedPolicy* out) {
+// Packs W into dst (capacity dst_cap floats, no allocation) or, with dst null, into the env's own
+// buffer, grown with hipMalloc as the policy shape requires.
+static void pack_policy(EnvState* E, const float* W, PackedPolicy* out, float* dst = nullptr, long dst_cap = 0) {
   long total = 0;
   PackedPolicy pp = make_packed(E->shape, nullptr, W, &total);
-  if (total > E->Wp_cap) {
-    if (E->Wp) HIPCHECK(hipFree(E->Wp));
-    HIPCHECK(hipMalloc(&E->Wp, total * sizeof(float)));
-    E->Wp_cap = total;
+  float* Wp = dst;
+  if (!Wp) {
+    if (total > E->Wp_cap) {
+      if (E->Wp) HIPCHECK(hipFree(E->Wp));
+      HIPCHECK(hipMalloc(&E->Wp, total * sizeof(float)));
+      E->Wp_cap = total;
+    }
+    Wp = E->Wp;
+  } else if (total > dst_cap) {
+    fail("pack_policy: packed policy larger than its buffer");
   }
-  pp = make_packed(E->shape, E->Wp, W, &total);
-  PackArgs pa{W, E->Wp, pp, E->shape, total};
+  pp = make_packed(E->shape, Wp, W, &total);
+  PackArgs pa{W, Wp, pp, E->shape, total};
   hipLaunchKernelGGL(k_pack, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, 0, pa);
   HIPCHECK(hipGetLastError());
   *out = pp;
@@ -822,14 +830,14 @@ static void poll_queue_error(EnvState* E) {
 
 static void rollout_impl(EnvState* E, int H, const float* W, const float* mean, const float* var, float* O, float* A,
                          float* LP, float* V, float* R, float* D, float* Vlast, const float* act_noise,
-                         const float* reset_noise) {
+                         const float* reset_noise, float* wp = nullptr, long wp_cap = 0) {
   poll_queue_error(E);
   if (H < 0) H = 0;   // no control step; the bootstrap value is still computed (as the reference's k_rollout)
   PackedPolicy pp;
-  pack_policy(E, W, &pp);
+  pack_policy(E, W, &pp, wp, wp_cap);
   PhysArgs pa = phys_args(E);
   pa.act = A; pa.astep = 1; pa.rstep = 1; pa.R = R; pa.D = D; pa.reset_noise = reset_noise;
-  const bool prof = E->prof_on != 0;
+  const bool prof = E->prof_on != 0 && !wp;
   for (int t = 0; t < H; ++t) {
     if (prof) prof_mark(E->ev_pol, E->n_pol);
     launch_policy(E, pp, t, H, mean, var, act_noise, O, A, LP, V, Vlast);
@@ -844,6 +852,26 @@ static void rollout_impl(EnvState* E, int H, const float* W, const float* mean, 
   HIPCHECK(hipMemcpyAsync(E->h_qerr, E->qerr, sizeof(int), hipMemcpyDeviceToHost, 0));
 }
 
+// ---- packed policy weights of g1_rollout_noalloc: a file-scope device array, so the entry point
+// allocates nothing. The widest shape g1_env_set_policy accepts (three hidden layers of 512) packs
+// into 595,488 floats; the array holds 640 Ki floats (2.5 MiB) on every GPU the library runs on,
+// until the process ends. Host code never names the array in a launch: it uses the device address
+// hipGetSymbolAddress returns, once per device, with that device current (kept in scratch_addr).
+constexpr long kScratchFloats = 640L * 1024L;
+static __device__ __align__(256) float scratch[kScratchFloats];
+constexpr int kMaxDevices = 64;
+static float* scratch_addr[kMaxDevices];
+
+static void scratch_setup() {
+  int dev = 0;
+  HIPCHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) fail("scratch_setup: device index beyond the library's table");
+  if (scratch_addr[dev]) return;
+  void* p = nullptr;
+  HIPCHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  scratch_addr[dev] = (float*)p;
+}
+
 extern "C" {
 
 int g1_env_obs_dim(void) { return kObs; }
@@ -851,6 +879,7 @@ int g1_env_act_dim(void) { return kAct; }
 
 void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
   if (N <= 0 || substeps <= 0 || pgs_iters < 0) fail("g1_env_create: invalid N/substeps/pgs_iters");
+  scratch_setup();
   EnvState* E = new EnvState();
   E->N = N; E->S = substeps; E->pgs = pgs_iters; E->seed = seed; E->mu = MF::foot_mu;
   E->shape = PolicyShape{2, {256, 256, 0, 0}, 0};
@@ -999,6 +1028,27 @@ void g1_rollout(void* h, int H, const float* W, const float* mean, const float* 
 void g1_rollout_ex(void* h, int H, const float* W, const float* mean, const float* var, float* O, float* A, float* LP,
                    float* V, float* R, float* D, float* Vlast, const float* act_noise, const float* reset_noise) {
   rollout_impl((EnvState*)h, H, W, mean, var, O, A, LP, V, R, D, Vlast, act_noise, reset_noise);
+}
+
+int g1_rollout_noalloc(void* h, int H, const float* W, const float* mean, const float* var, float* O, float* A,
+                       float* LP, float* V, float* R, float* D, float* Vlast, const float* act_noise,
+                       const float* reset_noise) {
+  EnvState* E = (EnvState*)h;
+  int dev = 0;
+  HIPCHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices || !scratch_addr[dev]) {
+    fprintf(stderr, "g1_rollout_noalloc: no env was created on the current device\n");
+    return -1;
+  }
+  long total = 0;
+  make_packed(E->shape, nullptr, nullptr, &total);
+  if (total > kScratchFloats) {
+    fprintf(stderr, "g1_rollout_noalloc: the packed policy needs %ld floats, the scratch holds %ld\n", total,
+            kScratchFloats);
+    return -1;
+  }
+  rollout_impl(E, H, W, mean, var, O, A, LP, V, R, D, Vlast, act_noise, reset_noise, scratch_addr[dev], kScratchFloats);
+  return 0;
 }
 
 void g1_env_bench_phys(void* h, int K) {

@@ -43,6 +43,7 @@ SIGNATURES = {
     "g1_env_destroy": (None, [_vp]),
     # additive
     "g1_rollout_ex": (None, [_vp, _c.c_int] + [_vp] * 12),
+    "g1_rollout_noalloc": (_c.c_int, [_vp, _c.c_int] + [_vp] * 12),
     "g1_env_set_state": (None, [_vp, _fp, _fp, _fp, _ip]),
     "g1_env_get_state": (None, [_vp, _fp, _fp, _fp, _ip]),
     "g1_env_set_policy": (_c.c_int, [_vp, _c.c_int, _ip, _c.c_int]),
