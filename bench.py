@@ -1,16 +1,33 @@
 """Benchmark of the fused rollout on one MI355X: the BASELINE metric (physics substeps/s and ms per
 fused rollout, N=8192, H=32, S=10, pgs=8, MLP 100-256-256 tanh), with the physics kernel's
-roofline fraction and the CPU oracle timed on this host beside it.
+roofline and the CPU oracle timed on this host beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3|4] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3|4] [--no-cpu] [--no-counters]
 
 A "step" is one fused rollout (one g1_rollout call: H control steps x S substeps for all N worlds)
 with the policy weights and frozen statistics already resident in HBM. Prints ONE JSON line.
+
+Roofline of k_physics (the dominant kernel): the physics runs out of registers and LDS and is
+bound by VALU issue, so `achieved` is its algorithmic FLOP rate: the reference algorithm's
+floating-point operations per world-substep by contact count (g1.cu_amd/roofline.py, counted by an
+instrumented oracle) summed over the launch's measured contact histogram, divided by the average
+launch time from HIP events on the kernel's stream; `peak` is the MI355X fp32 figure. Hardware
+counters come from rocprofv3 passes over a one-rollout run of this script, started as child
+processes before this process touches the GPU: HBM traffic per dispatch (FETCH_SIZE and
+WRITE_SIZE, each scaled by what the counter reads for a copy of known size in the same run),
+VALU busy and lane utilisation, LDS utilisation and bank-conflict share. The working-set unit of
+the reference algorithm (bytes of every per-world intermediate written and read once) is reported
+beside it as `hbm_proxy`: a workload measure, not an HBM ceiling.
 """
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -19,18 +36,16 @@ sys.path.insert(0, os.path.join(ROOT, "g1.cu_amd"))
 
 import numpy as np  # noqa: E402
 
-HBM_PEAK_GBS = 8000.0            # MI355X published HBM3E bandwidth
+import roofline as rf  # noqa: E402
+
 RTX3090_SUBSTEPS_PER_S = 4.96e6  # reference's published fused-rollout number (N=8192, H=32, S=10)
-# HBM bytes per k_physics dispatch at config 3 from rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled
-# by the same counter on a copy of known size (profiles/k_physics_config3_pmc.md)
-PHYS_TRAFFIC_BYTES = {3: 16.04e6}
-
-
-def bytes_per_world_substep(c, p):
-    """Algorithmic bytes of one world-substep with c contacts and p PGS sweeps: every per-world
-    intermediate of the reference algorithm written once and read once in fp32, the PGS matrix
-    read once per sweep (B_ws(c) = 4 [2 (3244 + 1390 c + 35 [c>0]) + 16 c^2 (1 + p)])."""
-    return 4.0 * (2.0 * (3244 + 1390 * c + 35 * (c > 0)) + 16.0 * c * c * (1 + p))
+COPY_MIB = 1024                  # copy of known size that calibrates FETCH_SIZE / WRITE_SIZE
+COUNTER_PASSES = (
+    ("fetch", ["FETCH_SIZE"]),
+    ("write", ["WRITE_SIZE"]),
+    ("sq", ["VALUBusy", "VALUUtilization", "LdsUtil", "LDSBankConflict", "SQ_INSTS_VALU", "SQ_INSTS_LDS",
+            "SQ_WAVES"]),
+)
 
 
 def cpu_baseline(cfg, threads, seed=0):
@@ -45,7 +60,8 @@ def cpu_baseline(cfg, threads, seed=0):
     qp, qv, pa, st = configs.reset_states(rng, n)
     W = configs.policy_init(rng, hidden=cfg["hidden"])
     an, rn = configs.rollout_noise(rng, H, n)
-    mean = np.zeros(100, np.float32); var = np.ones(100, np.float32)
+    mean = np.zeros(100, np.float32)
+    var = np.ones(100, np.float32)
     t0 = time.perf_counter()
     oracle.rollout(qp, qv, pa, st, W, mean, var, an, rn, H, S=S, pgs=cfg["pgs"], hidden=cfg["hidden"],
                    act=cfg["act"], threads=threads)
@@ -55,6 +71,80 @@ def cpu_baseline(cfg, threads, seed=0):
                        f"({n * H * S} world-substeps, {dt:.1f} s wall on {threads} threads)")
 
 
+# ---------------------------------------------------------------- hardware counters (rocprofv3)
+def counter_child(config):
+    """The profiled program: one copy of COPY_MIB MiB (the calibration dispatch), then one warm-up
+    and one timed rollout of the configuration."""
+    import torch
+    import configs
+    import g1env
+    n = COPY_MIB * (1 << 20) // 4
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+    cfg = configs.ROLLOUT_CONFIGS[config]
+    N, H = cfg["N"], cfg["H"]
+    W = torch.from_numpy(configs.policy_init(np.random.default_rng(1234), hidden=cfg["hidden"])).cuda()
+    mean, var = torch.zeros(100, device="cuda"), torch.ones(100, device="cuda")
+    with g1env.Env(N, substeps=cfg["S"], pgs_iters=cfg["pgs"], seed=1) as env:
+        env.set_policy(cfg["hidden"], cfg["act"])
+        env.reset()
+        traj = g1env.Trajectory(H, N)
+        for _ in range(2):
+            traj.run(env, W, mean, var)
+        torch.cuda.synchronize()
+        assert env.check() == 0
+
+
+def _read_counters(outdir):
+    rows = []
+    for path in glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path, newline="") as f:
+            rows += list(csv.DictReader(f))
+    return rows
+
+
+def measure_counters(config, timeout_s=150):
+    """Runs the counter passes on child processes; returns per-dispatch averages for k_physics and
+    the calibration copy, or None with the reason."""
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not found"
+    res = {"physics": {}, "copy": {}}
+    env = dict(os.environ, TMPDIR="/tmp")
+    for name, counters in COUNTER_PASSES:
+        outdir = tempfile.mkdtemp(prefix=f"g1bench_{name}_", dir="/tmp")
+        cmd = [exe, "--pmc", *counters, "--output-format", "csv", "-d", outdir, "-o", "p", "--",
+               sys.executable, os.path.abspath(__file__), "--counter-child", "--config", str(config)]
+        try:
+            p = subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout_s, capture_output=True, text=True)
+        except subprocess.TimeoutExpired:
+            return None, f"counter pass {name} timed out"
+        rows = _read_counters(outdir)
+        shutil.rmtree(outdir, ignore_errors=True)
+        if not rows:
+            return None, f"counter pass {name}: no output (exit {p.returncode}): {p.stderr[-300:]}"
+        for r in rows:
+            kname, cname, val = r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"])
+            key = "physics" if "k_physics" in kname else ("copy" if "copyBuffer" in kname else None)
+            if key is None:
+                continue
+            res[key].setdefault(cname, []).append(val)
+    phys = {k: float(np.mean(v)) for k, v in res["physics"].items()}
+    copy = {k: float(np.max(v)) for k, v in res["copy"].items()}
+    need = {"FETCH_SIZE", "WRITE_SIZE"}
+    if not need <= set(phys) or not need <= set(copy):
+        return None, "counter passes did not report the physics or copy dispatches"
+    kib = COPY_MIB * 1024.0
+    scale_f, scale_w = kib / copy["FETCH_SIZE"], kib / copy["WRITE_SIZE"]
+    phys["traffic_bytes"] = (phys["FETCH_SIZE"] * scale_f + phys["WRITE_SIZE"] * scale_w) * 1024.0
+    phys["fetch_scale"], phys["write_scale"] = scale_f, scale_w
+    phys["dispatches"] = len(res["physics"]["FETCH_SIZE"])
+    return phys, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -62,14 +152,22 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=3, choices=[3, 4])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-counters", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--counter-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--policy", choices=["random", "trained"], default="random",
                     help="random-init weights (the configuration's definition) or the reference's trained "
                          "checkpoint (g1.cu_amd/data/trained_policy_finish_best.npz: walking contact mix)")
     args = ap.parse_args()
+    if args.counter_child:
+        counter_child(args.config)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: the rollout shards worlds across GPUs with no exchange, "
               "and this build runs on single-GPU boxes only (--gpus 1).", file=sys.stderr)
         sys.exit(2)
+
+    # counter passes first, while this process has not touched the GPU
+    counters, counter_note = (None, "skipped (--no-counters)") if args.no_counters else measure_counters(args.config)
 
     import torch
     import configs
@@ -85,24 +183,23 @@ def main():
             sys.exit("the trained checkpoint has the config-3 policy shape (100-256-256 tanh)")
         tp = np.load(os.path.join(ROOT, "g1.cu_amd", "data", "trained_policy_finish_best.npz"))
         W = torch.from_numpy(tp["W"]).cuda()
-        mean = torch.from_numpy(tp["obs_mean"]).cuda(); var = torch.from_numpy(tp["obs_var"]).cuda()
+        mean = torch.from_numpy(tp["obs_mean"]).cuda()
+        var = torch.from_numpy(tp["obs_var"]).cuda()
     else:
         W = torch.from_numpy(configs.policy_init(rng, hidden=cfg["hidden"])).cuda()
-        mean = torch.zeros(100, device="cuda"); var = torch.ones(100, device="cuda")
+        mean = torch.zeros(100, device="cuda")
+        var = torch.ones(100, device="cuda")
     traj = g1env.Trajectory(H, N)
 
-    def rollout():
-        traj.run(env, W, mean, var)
-
     for _ in range(args.warmup):
-        rollout()
+        traj.run(env, W, mean, var)
     torch.cuda.synchronize()
     env.ncon_hist(enable=True)
     env.profile(1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        rollout()
+        traj.run(env, W, mean, var)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     pr = env.profile_read()
@@ -110,19 +207,48 @@ def main():
     hist = env.ncon_hist(enable=False)
     if env.check() != 0:
         sys.exit("physics work queue error: results undefined")
+    env.close()
     ms_rollout = wall * 1e3 / args.steps
     substeps_per_s = N * H * S / (wall / args.steps)
 
-    phys_ms, phys_n, pol_ms = pr["physics_ms"], pr["physics_launches"], pr["policy_ms"]
-    nsub = hist.sum()
-    bytes_total = sum(int(hist[c]) * bytes_per_world_substep(c, pgs) for c in range(9))
-    launches = phys_n
-    bytes_per_launch = bytes_total / max(launches, 1)
-    avg_launch_s = phys_ms / max(launches, 1) * 1e-3
-    achieved = bytes_per_launch / avg_launch_s / 1e9
-    cbar = float((hist * np.arange(9)).sum() / max(nsub, 1))
-    policy_flops = 2 * N * (H + 1) * sum(a * b for a, b in zip((100,) + tuple(cfg["hidden"]),
-                                                                 tuple(cfg["hidden"]) + (30,)))
+    launches = max(pr["physics_launches"], 1)
+    avg_launch_s = pr["physics_ms"] / launches * 1e-3
+    bytes_total, flops_total = rf.physics_work(hist, pgs, control_steps_worlds=N * H * args.steps)
+    flops_launch, bytes_launch = flops_total / launches, bytes_total / launches
+    achieved_tf = flops_launch / avg_launch_s / 1e12
+    cbar = float((hist * np.arange(9)).sum() / max(hist.sum(), 1))
+    pol_flops = 2 * N * (H + 1) * sum(a * b for a, b in zip((100,) + tuple(cfg["hidden"]), tuple(cfg["hidden"]) + (30,)))
+    pol_ms = pr["policy_ms"] / args.steps
+    pol_tf = pol_flops / (pol_ms * 1e-3) / 1e12 if pol_ms > 0 else None
+
+    roof = {"bound": "valu", "achieved": achieved_tf, "peak": rf.FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": achieved_tf / rf.FP32_PEAK_TFLOPS,
+            "traffic": counters["traffic_bytes"] if counters else None,
+            "kernel": "k_physics", "avg_launch_ms": avg_launch_s * 1e3, "algorithmic_flops_per_launch": flops_launch,
+            "mean_ncon": cbar, "frac_of_unpacked_fp32": achieved_tf / rf.FP32_UNPACKED_TFLOPS,
+            "hbm_proxy": {"unit": "GB/s", "achieved": bytes_launch / avg_launch_s / 1e9, "peak": rf.HBM_PEAK_GBS,
+                          "frac": bytes_launch / avg_launch_s / 1e9 / rf.HBM_PEAK_GBS,
+                          "algorithmic_bytes_per_launch": bytes_launch,
+                          "note": "reference-algorithm working set per world-substep, written and read once; "
+                                  "held in registers and LDS, not HBM"}}
+    if counters:
+        valu = counters.get("SQ_INSTS_VALU")
+        roof["counters"] = {
+            "source": f"rocprofv3 --pmc, one-rollout run of this script ({counters['dispatches']} k_physics dispatches)",
+            "hbm_bytes_per_dispatch": counters["traffic_bytes"],
+            "hbm_gbs": counters["traffic_bytes"] / avg_launch_s / 1e9,
+            "fetch_write_scale": [counters["fetch_scale"], counters["write_scale"]],
+            "valu_busy_frac": counters.get("VALUBusy", float("nan")) / 100.0,
+            "valu_lane_utilization": counters.get("VALUUtilization", float("nan")) / 100.0,
+            "valu_insts_per_dispatch": valu,
+            "valu_issue_frac": valu / (rf.VALU_ISSUE_PEAK * avg_launch_s) if valu else None,
+            "flops_per_valu_lane_slot": flops_launch / (valu * 64) if valu else None,
+            "lds_util_frac": counters.get("LdsUtil", float("nan")) / 100.0,
+            "lds_bank_conflict_frac": counters.get("LDSBankConflict", float("nan")) / 100.0,
+            "lds_insts_per_dispatch": counters.get("SQ_INSTS_LDS")}
+    else:
+        roof["counters"] = {"note": counter_note}
+
     out = {
         "metric": "physics substeps/sec + ms per fused rollout (N=8192, H=32, 10 substeps) on 1 GPU",
         "value": substeps_per_s,
@@ -143,15 +269,12 @@ def main():
                                f"fused rollout N={N} H={H} S={S} pgs={pgs} "
                                f"policy 100-{'-'.join(map(str, cfg['hidden']))} {'tanh' if cfg['act'] == 0 else 'ELU'}",
                    "N": N, "H": H, "substeps": S, "pgs": pgs, "ms_per_rollout": ms_rollout},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": PHYS_TRAFFIC_BYTES.get(args.config),
-                     "kernel": "k_physics", "avg_launch_ms": phys_ms / max(launches, 1),
-                     "algorithmic_bytes_per_launch": bytes_per_launch, "mean_ncon": cbar},
-        "phases": {"physics_ms_per_rollout": phys_ms / args.steps, "policy_ms_per_rollout": pol_ms / args.steps,
-                   "policy_tflops": policy_flops / (pol_ms / args.steps * 1e-3) / 1e12 if pol_ms > 0 else None,
+        "roofline": roof,
+        "phases": {"physics_ms_per_rollout": pr["physics_ms"] / args.steps, "policy_ms_per_rollout": pol_ms,
+                   "policy_tflops": pol_tf,
+                   "policy_mfma_frac": pol_tf / rf.FP32_PEAK_TFLOPS if pol_tf else None,
                    "ncon_hist": hist.tolist()},
     }
-    env.close()
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(cfg, threads)

@@ -63,6 +63,46 @@ def _load():
 
 
 _lib = None
+_flib = None
+
+COUNT_KEYS = ("add", "mul", "fma", "div", "sqrt", "cmp", "trans")
+
+
+def flops_lib():
+    """The operation-counting instantiation of the oracle (oracle/libg1flops.so)."""
+    global _flib
+    if _flib is None:
+        path = os.path.join(HERE, "libg1flops.so")
+        if not os.path.exists(path):
+            build()
+        _flib = ctypes.CDLL(path)
+        _flib.flc_substep.argtypes = [_f32p, _f32p, _f32p, _c.c_int, _c.c_float, _c.c_int,
+                                      np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")]
+        _flib.flc_substep.restype = _c.c_int
+        _flib.flc_step_overhead.argtypes = [_c.c_int, np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")]
+    return _flib
+
+
+def flops_of(counts):
+    """Floating-point operations of an operation count: add/sub, mul, div and sqrt one each, a fused
+    multiply-add two; comparisons and transcendental calls are reported apart."""
+    return counts["add"] + counts["mul"] + 2 * counts["fma"] + counts["div"] + counts["sqrt"]
+
+
+def count_substep(qpos, qvel, target, pgs=8, mu=MU_MODEL, ref_order=True):
+    """Operation counts of one env substep of one world (the reference's association by default).
+    Returns (ncon, dict of counts)."""
+    out = np.zeros(7)
+    nc = flops_lib().flc_substep(_arr(qpos, np.float32), _arr(qvel, np.float32), _arr(target, np.float32), int(pgs),
+                                 float(mu), int(ref_order), out)
+    return nc, dict(zip(COUNT_KEYS, out.astype(np.int64).tolist()))
+
+
+def count_step_overhead(ref_order=True):
+    """Operation counts of a control step's work outside its substeps (targets, reward, termination)."""
+    out = np.zeros(7)
+    flops_lib().flc_step_overhead(int(ref_order), out)
+    return dict(zip(COUNT_KEYS, out.astype(np.int64).tolist()))
 
 
 def lib():
