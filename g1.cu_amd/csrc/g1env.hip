@@ -18,6 +18,7 @@
 #include "../../include/g1env.h"
 #include "physics.h"
 #include "policy.h"
+#include "rollout.h"
 
 using namespace g1k;
 
@@ -77,9 +78,183 @@ __device__ __forceinline__ T ld_l2(const T* p) {
   return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- work-queue hand-over between waves (k_physics, k_rollout)
+// A value stored by another wave of the same launch is read from the L2 (ld_l2), the producer's
+// stores are acknowledged before its flag moves, and flags only grow. The hardware places blocks on
+// the 8 XCDs round-robin, so all waves of queue q share the L2 of XCD q mod 8 (xlocal, verified when
+// the env is created and re-checked by every wave); the L2 is then the coherence point. Without
+// xlocal the hand-over uses agent-scope release/acquire fences, which also write back and
+// invalidate the L2 (correct on any placement, much slower).
+
+// Wait until *flag >= want (wrap-safe). A wait that exceeds kSpinLimit polls sets qerr = 1 and
+// returns: every item waited for was claimed earlier by a running wave, so a wait ends unless the
+// hardware stalls; the error makes the next synchronising call exit.
+__device__ __forceinline__ void wait_flag(const unsigned* flag, unsigned want, int* qerr, int xlocal) {
+  unsigned spins = 0;
+#pragma unroll 1
+  for (;;) {
+    const unsigned f = __builtin_amdgcn_readfirstlane(ld_l2(flag));
+    if ((int)(f - want) >= 0) break;
+    if (++spins > kSpinLimit) {
+      if (threadIdx.x == 0) __hip_atomic_store(qerr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  if (xlocal) __asm__ volatile("" ::: "memory");
+  else __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// Publish the item's stores: every store acknowledged, then the flag moves to `value`.
+__device__ __forceinline__ void release_flag(unsigned* flag, unsigned value, int xlocal) {
+  __syncthreads();
+  if (xlocal) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  if (threadIdx.x == 0) __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One physics work item: world pair p (the two 32-lane groups of the wave), control step k of the
+// launch, substeps [cst[c], cst[c + 1]) of it: PD torques, world_qacc, Euler; the last chunk of a
+// control step adds the step's reward, termination and auto-reset (reference:
+// src/g1_env.cu:118-212, the k_rollout substep loop :319-325). Every input a previous item or launch
+// wrote is read from the L2 (the actions too: in k_rollout the policy items of the same launch
+// write them).
+__device__ __forceinline__ void physics_item(const PhysArgs& a, WorldLds& s, const LaneModel& L, int g, int l, int p,
+                                             int k, int c, unsigned& hcnt) {
+  const int ai = L.hinge ? L.b - 2 : 0;
+  const SolveParams P{a.pgs, a.mu, true, true};
+  const int w = 2 * p + g;
+  const bool wvalid = w < a.N;
+  const int wc = wvalid ? w : a.N - 1;   // an odd N's last group repeats world N - 1 and stores nothing
+
+  LaneState st;
+  const float* gq = a.qp + (long)wc * kNQ;
+  const float* gv = a.qv + (long)wc * kNV;
+#pragma unroll
+  for (int m = 0; m < 7; ++m) st.bq[m] = ld_l2(gq + m);
+#pragma unroll
+  for (int m = 0; m < 6; ++m) st.bqd[m] = ld_l2(gv + m);
+  st.jq = L.hinge ? ld_l2(gq + L.b + 5) : 0.f;
+  st.jqd = L.hinge ? ld_l2(gv + L.b + 4) : 0.f;
+  const int t = a.t0 + k * a.astep;
+  const float act = L.hinge ? ld_l2(a.act + ((long)t * a.N + wc) * kAct + ai) : 0.f;
+  // PD target = clamp(stand + 0.5 a) (reference: src/g1_env.cu:123-130)
+  float target = fmaf_(0.5f, act, L.qstand);
+  if (target < L.clo) target = L.clo;
+  if (target > L.chi) target = L.chi;
+  float vx_sum = 0.f, energy = 0.f;
+  if (c > 0) {
+    energy = ld_l2(a.acc + (long)wc * kGroup + l);
+    vx_sum = ld_l2(a.vxs + wc);
+  }
+  const int s0 = a.cst[c], s1 = a.cst[c + 1];
+#pragma unroll 1
+  for (int sub = s0; sub < s1; ++sub) {
+    float jtau = 0.f;
+    if (L.hinge) {
+      float pdt = fmaf_(-L.kd, st.jqd, L.kp * (target - st.jq));
+      if (pdt < L.flo) pdt = L.flo;
+      else if (pdt > L.fhi) pdt = L.fhi;
+      jtau = pdt;
+      energy += fabsf(pdt * st.jqd);
+    }
+    float bqacc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, jqacc = 0.f;
+    const int nc = world_qacc(l, s, st, jtau, P, bqacc, jqacc);
+    hcnt += (l == nc && wvalid) ? 1u : 0u;
+    integrate_lane(L, st, bqacc, jqacc, true);
+    vx_sum += st.bqd[0];
+  }
+  if (c < a.nch - 1) {
+    if (wvalid) {
+      a.acc[(long)w * kGroup + l] = energy;
+      if (l == 1) a.vxs[w] = vx_sum;
+    }
+  } else {
+    // ---- reward / termination / auto-reset (reference: src/g1_env.cu:164-211), lane 1 decides
+    float pa = L.hinge ? ld_l2(a.pa + (long)wc * kAct + ai) : 0.f;
+    int step = ld_l2(a.steps + wc);
+    unsigned rng = ld_l2(a.rng + wc);
+    const float da = L.hinge ? act - pa : 0.f;
+    float act_pen = gsum(da * da);
+    const float energy_tot = gsum(energy);
+    int d_flag = 0;
+    float r = 0.f;
+    if (l == 1) {
+      const float vx = vx_sum / (float)a.S;
+      const float height = st.bq[2];
+      const float qx = st.bq[4], qy = st.bq[5];
+      const float up = fmaf_(-2.f, fmaf_(qy, qy, qx * qx), 1.f);   // quat2mat(q)[2][2]
+      const int alive = !(height < 0.45f || up < 0.5f);
+      const float upc = up < 0.f ? 0.f : (up > 1.f ? 1.f : up);
+      float vx_c = vx > 0.8f ? 0.8f : vx;
+      if (vx_c < 0.f) vx_c = 0.f;
+      const float r_vel = 1.0f * vx_c * upc;
+      const float r_lat = -0.2f * fabsf(st.bqd[1]) - 0.05f * fabsf(st.bqd[5]);
+      const float r_up = 0.3f * upc;
+      const float r_h = -0.5f * fabsf(height - 0.78f);
+      if (act_pen > 10.f) act_pen = 10.f;
+      r = alive ? 1.0f + r_vel + r_lat + r_up + r_h - 0.005f * act_pen - 1e-4f * energy_tot : -5.0f;
+      const int won = alive && st.bq[0] >= 5.0f;
+      if (won) r += 50.0f;
+      d_flag = (!alive || won || step + 1 >= 1000) ? 1 : 0;
+    }
+    d_flag = gshfl(d_flag, 1);
+    step += 1;
+    pa = act;
+    if (d_flag) {
+      const float u = a.reset_noise ? a.reset_noise[((long)t * a.N + wc) * kAct + ai]
+                                    : rng_pm1(a.seed, wc, rng, kStreamReset, ai);
+      if (L.hinge) { st.jq = L.qstand + 0.05f * u; st.jqd = 0.f; pa = 0.f; }
+#pragma unroll
+      for (int m = 0; m < 7; ++m) st.bq[m] = MF::qpos_stand[m];
+#pragma unroll
+      for (int m = 0; m < 6; ++m) st.bqd[m] = 0.f;
+      step = 0;
+    }
+    rng += 1;
+    if (wvalid) {
+      if (l == 1) {
+        const long o = (long)(a.t0 + k * a.rstep) * a.N + w;
+        a.R[o] = r;
+        a.D[o] = (float)d_flag;
+        a.steps[w] = step;
+        a.rng[w] = rng;
+      }
+      if (L.hinge) a.pa[(long)w * kAct + ai] = pa;
+      if (a.obs && k == a.K - 1) {
+        // observation of the final state, each lane writing its own entries (same values as k_obs)
+        float* o = a.obs + (long)w * kObs;
+        if (l == 1) {
+#pragma unroll
+          for (int m = 0; m < 6; ++m) o[m] = st.bqd[m];
+          const float qw = st.bq[3], qx = st.bq[4], qy = st.bq[5], qz = st.bq[6];
+          o[6] = -(2.f * fmaf_(-qw, qy, qx * qz));
+          o[7] = -(2.f * fmaf_(qw, qx, qy * qz));
+          o[8] = -fmaf_(-2.f, fmaf_(qy, qy, qx * qx), 1.f);
+        }
+        if (L.hinge) { o[9 + ai] = st.jq; o[38 + ai] = st.jqd; o[67 + ai] = pa; }
+        if (l == 0) { o[96] = 0.8f; o[97] = 0.f; o[98] = 0.f; o[99] = 0.f; }
+      }
+    }
+  }
+  if (wvalid) {
+    float* oq = a.qp + (long)w * kNQ;
+    float* ov = a.qv + (long)w * kNV;
+    if (l == 1) {
+#pragma unroll
+      for (int m = 0; m < 7; ++m) oq[m] = st.bq[m];
+#pragma unroll
+      for (int m = 0; m < 6; ++m) ov[m] = st.bqd[m];
+    }
+    if (L.hinge) {
+      oq[L.b + 5] = st.jq;
+      ov[L.b + 4] = st.jqd;
+    }
+  }
+}
+
 // One physics launch advances every world pair (the two 32-lane groups of a wave64) by K control
-// steps of S substeps: PD torques, world_qacc, Euler, then the control step's reward, termination
-// and auto-reset (reference: src/g1_env.cu:118-212, the k_rollout substep loop :319-325).
+// steps of S substeps (physics_item).
 //
 // The work is cut into items (world pair, chunk of substeps of one control step) that
 // persistent waves claim from a queue, instead of one block per pair for the whole launch: a pair
@@ -92,14 +267,7 @@ __device__ __forceinline__ T ld_l2(const T* p) {
 // a block whose queue is empty goes on with the other queues of its XCD (q + 8, q + 16, q + 24 mod
 // 32), which evens out queues that drew more pairs with contacts. Item (p, j) needs item (p, j - 1),
 // which was claimed earlier from the same queue by a wave that is running, so a wait always ends;
-// the pair's flag counts its completed items. A wait that
-// exceeds kSpinLimit polls sets qerr and continues rather than spin on.
-// Hand-over of a pair's state between items: the hardware places blocks on the 8 XCDs
-// round-robin, so all waves of queue q share the L2 of XCD q mod 8 (xlocal, verified when the env
-// is created and re-checked by every wave). The L2 is then the coherence point: the producer waits for its
-// stores to be acknowledged by the L2 before it moves the flag, and the consumer reads the flag and
-// the state from the L2 past its L1. Without xlocal the hand-over uses agent-scope release/acquire
-// fences, which also write back and invalidate the L2 (correct on any placement, much slower).
+// the pair's flag counts its completed items.
 __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
   __shared__ WorldLds lds[2];
   const int g = group_id(), l = group_lane();
@@ -110,7 +278,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
   const int npairs = (a.N + 1) >> 1;
   const int nch = a.nch;
   // queue qc being drained: the block's own, then the other queues of its XCD (same L2, so the
-  // hand-over below holds; every item waited for was claimed earlier by a running wave)
+  // hand-over holds; every item waited for was claimed earlier by a running wave)
   int qc = q;
   unsigned nq, nitems;
   unsigned* ctr;
@@ -120,8 +288,6 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
     ctr = a.qctr + a.qpar * kQueues + qq;
   };
   set_queue(q);
-  const int ai = L.hinge ? L.b - 2 : 0;
-  const SolveParams P{a.pgs, a.mu, true, true};
   unsigned hcnt = 0;   // lane q < 9 counts substeps with q contacts
   if (a.xlocal && threadIdx.x == 0 && xcc_id() != q % kXcds)
     __hip_atomic_store(a.qerr, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -140,158 +306,162 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
     const int j = (int)(it / nq);
     const int p = qc + kQueues * (int)(it - (unsigned)j * nq);
     const int k = j / nch, c = j - k * nch;
-    if (j > 0) {
-      const unsigned want = a.fbase + (unsigned)j;
-      unsigned spins = 0;
-#pragma unroll 1
-      for (;;) {
-        const unsigned f = __builtin_amdgcn_readfirstlane(ld_l2(a.flags + p));
-        if ((int)(f - want) >= 0) break;
-        if (++spins > kSpinLimit) {
-          if (threadIdx.x == 0) __hip_atomic_store(a.qerr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-      }
-      if (a.xlocal) __asm__ volatile("" ::: "memory");
-      else __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    }
-    const int w = 2 * p + g;
-    const bool wvalid = w < a.N;
-    const int wc = wvalid ? w : a.N - 1;   // an odd N's last group repeats world N - 1 and stores nothing
-
-    LaneState st;
-    const float* gq = a.qp + (long)wc * kNQ;
-    const float* gv = a.qv + (long)wc * kNV;
-#pragma unroll
-    for (int m = 0; m < 7; ++m) st.bq[m] = ld_l2(gq + m);
-#pragma unroll
-    for (int m = 0; m < 6; ++m) st.bqd[m] = ld_l2(gv + m);
-    st.jq = L.hinge ? ld_l2(gq + L.b + 5) : 0.f;
-    st.jqd = L.hinge ? ld_l2(gv + L.b + 4) : 0.f;
-    const int t = a.t0 + k * a.astep;
-    const float act = L.hinge ? a.act[((long)t * a.N + wc) * kAct + ai] : 0.f;
-    // PD target = clamp(stand + 0.5 a) (reference: src/g1_env.cu:123-130)
-    float target = fmaf_(0.5f, act, L.qstand);
-    if (target < L.clo) target = L.clo;
-    if (target > L.chi) target = L.chi;
-    float vx_sum = 0.f, energy = 0.f;
-    if (c > 0) {
-      energy = ld_l2(a.acc + (long)wc * kGroup + l);
-      vx_sum = ld_l2(a.vxs + wc);
-    }
-    const int s0 = a.cst[c], s1 = a.cst[c + 1];
-#pragma unroll 1
-    for (int sub = s0; sub < s1; ++sub) {
-      float jtau = 0.f;
-      if (L.hinge) {
-        float pdt = fmaf_(-L.kd, st.jqd, L.kp * (target - st.jq));
-        if (pdt < L.flo) pdt = L.flo;
-        else if (pdt > L.fhi) pdt = L.fhi;
-        jtau = pdt;
-        energy += fabsf(pdt * st.jqd);
-      }
-      float bqacc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, jqacc = 0.f;
-      const int nc = world_qacc(l, s, st, jtau, P, bqacc, jqacc);
-      hcnt += (l == nc && wvalid) ? 1u : 0u;
-      integrate_lane(L, st, bqacc, jqacc, true);
-      vx_sum += st.bqd[0];
-    }
-    if (c < nch - 1) {
-      if (wvalid) {
-        a.acc[(long)w * kGroup + l] = energy;
-        if (l == 1) a.vxs[w] = vx_sum;
-      }
-    } else {
-      // ---- reward / termination / auto-reset (reference: src/g1_env.cu:164-211), lane 1 decides
-      float pa = L.hinge ? ld_l2(a.pa + (long)wc * kAct + ai) : 0.f;
-      int step = ld_l2(a.steps + wc);
-      unsigned rng = ld_l2(a.rng + wc);
-      const float da = L.hinge ? act - pa : 0.f;
-      float act_pen = gsum(da * da);
-      const float energy_tot = gsum(energy);
-      int d_flag = 0;
-      float r = 0.f;
-      if (l == 1) {
-        const float vx = vx_sum / (float)a.S;
-        const float height = st.bq[2];
-        const float qx = st.bq[4], qy = st.bq[5];
-        const float up = fmaf_(-2.f, fmaf_(qy, qy, qx * qx), 1.f);   // quat2mat(q)[2][2]
-        const int alive = !(height < 0.45f || up < 0.5f);
-        const float upc = up < 0.f ? 0.f : (up > 1.f ? 1.f : up);
-        float vx_c = vx > 0.8f ? 0.8f : vx;
-        if (vx_c < 0.f) vx_c = 0.f;
-        const float r_vel = 1.0f * vx_c * upc;
-        const float r_lat = -0.2f * fabsf(st.bqd[1]) - 0.05f * fabsf(st.bqd[5]);
-        const float r_up = 0.3f * upc;
-        const float r_h = -0.5f * fabsf(height - 0.78f);
-        if (act_pen > 10.f) act_pen = 10.f;
-        r = alive ? 1.0f + r_vel + r_lat + r_up + r_h - 0.005f * act_pen - 1e-4f * energy_tot : -5.0f;
-        const int won = alive && st.bq[0] >= 5.0f;
-        if (won) r += 50.0f;
-        d_flag = (!alive || won || step + 1 >= 1000) ? 1 : 0;
-      }
-      d_flag = gshfl(d_flag, 1);
-      step += 1;
-      pa = act;
-      if (d_flag) {
-        const float u = a.reset_noise ? a.reset_noise[((long)t * a.N + wc) * kAct + ai]
-                                      : rng_pm1(a.seed, wc, rng, kStreamReset, ai);
-        if (L.hinge) { st.jq = L.qstand + 0.05f * u; st.jqd = 0.f; pa = 0.f; }
-#pragma unroll
-        for (int m = 0; m < 7; ++m) st.bq[m] = MF::qpos_stand[m];
-#pragma unroll
-        for (int m = 0; m < 6; ++m) st.bqd[m] = 0.f;
-        step = 0;
-      }
-      rng += 1;
-      if (wvalid) {
-        if (l == 1) {
-          const long o = (long)(a.t0 + k * a.rstep) * a.N + w;
-          a.R[o] = r;
-          a.D[o] = (float)d_flag;
-          a.steps[w] = step;
-          a.rng[w] = rng;
-        }
-        if (L.hinge) a.pa[(long)w * kAct + ai] = pa;
-        if (a.obs && k == a.K - 1) {
-          // observation of the final state, each lane writing its own entries (same values as k_obs)
-          float* o = a.obs + (long)w * kObs;
-          if (l == 1) {
-#pragma unroll
-            for (int m = 0; m < 6; ++m) o[m] = st.bqd[m];
-            const float qw = st.bq[3], qx = st.bq[4], qy = st.bq[5], qz = st.bq[6];
-            o[6] = -(2.f * fmaf_(-qw, qy, qx * qz));
-            o[7] = -(2.f * fmaf_(qw, qx, qy * qz));
-            o[8] = -fmaf_(-2.f, fmaf_(qy, qy, qx * qx), 1.f);
-          }
-          if (L.hinge) { o[9 + ai] = st.jq; o[38 + ai] = st.jqd; o[67 + ai] = pa; }
-          if (l == 0) { o[96] = 0.8f; o[97] = 0.f; o[98] = 0.f; o[99] = 0.f; }
-        }
-      }
-    }
-    if (wvalid) {
-      float* oq = a.qp + (long)w * kNQ;
-      float* ov = a.qv + (long)w * kNV;
-      if (l == 1) {
-#pragma unroll
-        for (int m = 0; m < 7; ++m) oq[m] = st.bq[m];
-#pragma unroll
-        for (int m = 0; m < 6; ++m) ov[m] = st.bqd[m];
-      }
-      if (L.hinge) {
-        oq[L.b + 5] = st.jq;
-        ov[L.b + 4] = st.jqd;
-      }
-    }
-    __syncthreads();
-    // every store of the item is acknowledged before the pair's flag moves on
-    if (a.xlocal) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    else __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    if (threadIdx.x == 0)
-      __hip_atomic_store(a.flags + p, a.fbase + (unsigned)j + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (j > 0) wait_flag(a.flags + p, a.fbase + (unsigned)j, a.qerr, a.xlocal);
+    physics_item(a, s, L, g, l, p, k, c, hcnt);
+    release_flag(a.flags + p, a.fbase + (unsigned)j + 1u, a.xlocal);
   }
   if (a.ncon_hist && l < 9 && hcnt) atomicAdd(&a.ncon_hist[l], (unsigned long long)hcnt);
+}
+
+// ====================================================================== the rollout in one launch
+// k_rollout runs a whole g1_rollout: the physics items of k_physics for H control steps, and the
+// policy of every control step on 16-world tiles (policy_tile) as work items of the same queues.
+// Tile u of queue q holds the pairs q + 32 (8 u + i), i < 8, so its items stay on the queue's XCD.
+// Claim order within a queue (nq pairs, ntq tiles, nch substep chunks per control step):
+//   P(0, all tiles); then for t < H: C(t, c, all pairs) for c < nch - 1, then per tile u:
+//   [C(t, nch - 1, the tile's pairs), P(t + 1, u)]
+// where P(t, u) is the policy of step t on tile u (P(H, u): the bootstrap value) and C(t, c, p)
+// chunk c of pair p's step t. Waits: C(t, c > 0, p) on C(t, c - 1, p) (the pair's flag);
+// C(t, 0, p) on P(t, u(p)) (the tile's flag); P(t > 0, u) on C(t - 1, nch - 1, p) of its pairs. Each
+// waited-for item comes earlier in the claim order and was claimed by a running wave, so every wait
+// ends (k_physics' argument).
+struct RolloutArgs {
+  PhysArgs ph;              // K = H control steps, actions from A
+  TileArgs po;
+  unsigned* tflags;         // [kQueues * tiles per queue] policy steps completed per tile
+  unsigned tbase;           // value every tile flag holds when this launch starts
+};
+
+// LDS of a k_rollout block: the two worlds' physics scratch, or a policy tile's hidden activations
+constexpr size_t kRolloutLds = 2 * sizeof(WorldLds) > sizeof(float) * kTileW * kTileLd
+                                   ? 2 * sizeof(WorldLds) : sizeof(float) * kTileW * kTileLd;
+
+__global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
+  __shared__ __align__(16) unsigned char lds_raw[kRolloutLds];
+  WorldLds* lds = reinterpret_cast<WorldLds*>(lds_raw);
+  const PhysArgs& a = ra.ph;
+  const int g = group_id(), l = group_lane();
+  WorldLds& s = lds[g];
+  const int q = blockIdx.x % kQueues;
+  if (blockIdx.x == 0 && threadIdx.x < kQueues) a.qctr[(a.qpar ^ 1) * kQueues + threadIdx.x] = 0u;
+  const int npairs = (a.N + 1) >> 1;
+  const int nch = a.nch, H = a.K;
+  int qc = q;
+  unsigned nq = 0, ntq = 0, nfull = 0, per_step = 0, nitems = 0;
+  unsigned* ctr = nullptr;
+  auto set_queue = [&](int qq) {
+    nq = npairs > qq ? (unsigned)((npairs - qq + kQueues - 1) / kQueues) : 0u;
+    ntq = (nq + kTilePairs - 1) / kTilePairs;
+    nfull = nq / kTilePairs;
+    per_step = (unsigned)nch * nq + ntq;
+    nitems = nq ? ntq + (unsigned)H * per_step : 0u;
+    ctr = a.qctr + a.qpar * kQueues + qq;
+  };
+  set_queue(q);
+  unsigned hcnt = 0;
+  if (a.xlocal && threadIdx.x == 0 && xcc_id() != q % kXcds)
+    __hip_atomic_store(a.qerr, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float* scratch_lds = reinterpret_cast<float*>(lds_raw);
+
+#pragma unroll 1
+  for (;;) {
+    unsigned mine = 0;
+    if (threadIdx.x == 0) mine = atomicAdd(ctr, 1u);
+    const unsigned it = __builtin_amdgcn_readfirstlane(mine);
+    if (it >= nitems) {
+      qc = qc + kXcds < kQueues ? qc + kXcds : qc + kXcds - kQueues;
+      if (qc == q) break;
+      set_queue(qc);
+      continue;
+    }
+    // ---- decode: policy item (t, u) or physics item (t, c, m)
+    int t, u = -1, c = 0, m = 0;
+    if (it < ntq) {
+      t = 0; u = (int)it;
+    } else {
+      const unsigned r = it - ntq;
+      t = (int)(r / per_step);
+      const unsigned rr = r - (unsigned)t * per_step;
+      const unsigned early = (unsigned)(nch - 1) * nq;
+      if (rr < early) {
+        c = (int)(rr / nq); m = (int)(rr - (unsigned)c * nq);
+      } else {
+        const unsigned r2 = rr - early;
+        unsigned uu, o, np;
+        if (r2 < (kTilePairs + 1) * nfull) { uu = r2 / (kTilePairs + 1); o = r2 - uu * (kTilePairs + 1); np = kTilePairs; }
+        else { uu = nfull; o = r2 - (kTilePairs + 1) * nfull; np = nq - kTilePairs * nfull; }
+        if (o < np) { c = nch - 1; m = (int)(kTilePairs * uu + o); }
+        else { u = (int)uu; t += 1; }
+      }
+    }
+    if (u >= 0) {
+      // ---- policy of step t on tile u
+      const int tile = qc + kQueues * u;
+      const int np = (int)min((unsigned)kTilePairs, nq - kTilePairs * (unsigned)u);
+      if (t > 0) {
+#pragma unroll 1
+        for (int i = 0; i < np; ++i)
+          wait_flag(a.flags + qc + kQueues * (kTilePairs * u + i), a.fbase + (unsigned)(t * nch), a.qerr, a.xlocal);
+      }
+      const int jw = threadIdx.x & 15;
+      const int w = tile_world(qc, u, jw, kQueues);
+      const bool valid = (jw >> 1) < np && w < a.N;
+      policy_tile(ra.po, a.qp, a.qv, a.pa, a.rng, a.seed, a.N, t, w, valid, scratch_lds,
+                  [](const auto* ptr) { return ld_l2(ptr); });
+      release_flag(ra.tflags + tile, ra.tbase + (unsigned)t + 1u, a.xlocal);
+    } else {
+      const int p = qc + kQueues * m;
+      const int jj = t * nch + c;
+      if (c > 0) wait_flag(a.flags + p, a.fbase + (unsigned)jj, a.qerr, a.xlocal);
+      else wait_flag(ra.tflags + qc + kQueues * (m / kTilePairs), ra.tbase + (unsigned)t + 1u, a.qerr, a.xlocal);
+      // the lane's model constants, formed here (opaque lane index) rather than held across items
+      int lo = l;
+      __asm__ volatile("" : "+v"(lo));
+      const LaneModel L = lane_model(lo);
+      physics_item(a, s, L, g, l, p, t, c, hcnt);
+      release_flag(a.flags + p, a.fbase + (unsigned)jj + 1u, a.xlocal);
+    }
+  }
+  if (a.ncon_hist && l < 9 && hcnt) atomicAdd(&a.ncon_hist[l], (unsigned long long)hcnt);
+}
+
+// Pack torch-order weights (W0, b0, W1, b1, Wmu, bmu, Wv, bv, log_std) into the tile layout.
+struct TilePackArgs {
+  const float* W; float* Wt; TileLayout tl; int h0, h1;
+};
+__global__ void k_pack_tiles(TilePackArgs a) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const TileLayout& T = a.tl;
+  if (idx >= T.total) return;
+  const long oW0 = 0, ob0 = oW0 + (long)a.h0 * kObs, oW1 = ob0 + a.h0, ob1 = oW1 + (long)a.h1 * a.h0,
+             oWmu = ob1 + a.h1, obmu = oWmu + (long)kAct * a.h1, oWv = obmu + kAct, obv = oWv + a.h1, ols = obv + 1;
+  float v = 0.f;
+  if (idx >= T.ls_off) {
+    const int i = (int)(idx - T.ls_off);
+    v = i < kAct ? a.W[ols + i] : 0.f;
+  } else {
+    int Ly = 0;
+    while (Ly < 2 && idx >= T.woff[Ly + 1]) ++Ly;
+    const int kin = Ly == 0 ? kObs : (Ly == 1 ? a.h0 : a.h1);
+    if (idx >= T.boff[Ly]) {
+      const int row = (int)(idx - T.boff[Ly]);
+      if (Ly == 0) v = row < a.h0 ? a.W[ob0 + row] : 0.f;
+      else if (Ly == 1) v = row < a.h1 ? a.W[ob1 + row] : 0.f;
+      else v = row < kAct ? a.W[obmu + row] : (row == kAct ? a.W[obv] : 0.f);
+    } else {
+      const long rel = idx - T.woff[Ly];
+      const int e = (int)(rel & 3), lane = (int)((rel >> 2) & 63);
+      const long rq = rel >> 8;
+      const int qd = (int)(rq % T.nQ[Ly]), ot = (int)(rq / T.nQ[Ly]);
+      const int row = 16 * ot + (lane & 15), k = tile_kappa(Ly, 4 * qd + e, lane >> 4);
+      if (k < kin) {
+        if (Ly == 0) v = row < a.h0 ? a.W[oW0 + (long)row * kObs + k] : 0.f;
+        else if (Ly == 1) v = row < a.h1 ? a.W[oW1 + (long)row * a.h0 + k] : 0.f;
+        else v = row < kAct ? a.W[oWmu + (long)row * a.h1 + k] : (row == kAct ? a.W[oWv + k] : 0.f);
+      }
+    }
+  }
+  a.Wt[idx] = v;
 }
 
 // XCD of each block of a grid shaped like k_physics' (placement check of the work queue)
@@ -646,6 +816,12 @@ struct EnvState {
   int pgrid;        // persistent grid: resident blocks of k_physics, a multiple of kQueues
   int xlocal;       // blocks land on XCD blockIdx % kXcds (measured at creation)
   int fences;       // 1: hand over state with agent-scope fences even where xlocal holds
+  // one-launch rollout (k_rollout): policy tiles' flags, their completed-step count, packed weights
+  int fused;        // 1: g1_rollout runs k_rollout when the policy shape allows it
+  unsigned* tflags;
+  unsigned tdone;
+  float* Wt;
+  long Wt_cap;
   int* h_qerr;      // pinned copy of qerr, refreshed asynchronously after every rollout
   // per-launch HIP events of the rollout's physics / policy kernels (null stream)
   int prof_on;
@@ -828,11 +1004,70 @@ static void poll_queue_error(EnvState* E) {
   check_queue_error(*(volatile int*)E->h_qerr);
 }
 
+// The one-launch rollout covers policies of two hidden layers of at most 256 units each (multiples of
+// 16); other shapes take the split form (policy and physics launches per control step).
+static bool fused_shape(const PolicyShape& sh) {
+  return sh.nl == 2 && sh.hid[0] % 16 == 0 && sh.hid[1] % 16 == 0 && sh.hid[0] <= kTileMaxHidden &&
+         sh.hid[1] <= kTileMaxHidden;
+}
+
+static int tiles_per_queue(int N) {
+  const int npairs = (N + 1) / 2;
+  const int nq = (npairs + kQueues - 1) / kQueues;
+  return (nq + kTilePairs - 1) / kTilePairs;
+}
+
+// The whole rollout as one k_rollout launch on the null stream; wp (capacity wp_cap floats) takes
+// the tile-packed weights instead of the env's own buffer.
+static void rollout_fused(EnvState* E, int H, const float* W, const float* mean, const float* var, float* O, float* A,
+                          float* LP, float* V, float* R, float* D, float* Vlast, const float* act_noise,
+                          const float* reset_noise, float* wp, long wp_cap) {
+  const TileLayout tl = tile_layout(E->shape.hid[0], E->shape.hid[1], E->shape.act);
+  float* Wt = wp;
+  if (!Wt) {
+    if (tl.total > E->Wt_cap) {
+      if (E->Wt) HIPCHECK(hipFree(E->Wt));
+      HIPCHECK(hipMalloc(&E->Wt, tl.total * sizeof(float)));
+      E->Wt_cap = tl.total;
+    }
+    Wt = E->Wt;
+  } else if (tl.total > wp_cap) {
+    fail("rollout: tile-packed policy larger than its buffer");
+  }
+  TilePackArgs pk{W, Wt, tl, E->shape.hid[0], E->shape.hid[1]};
+  hipLaunchKernelGGL(k_pack_tiles, dim3((unsigned)((tl.total + 255) / 256)), dim3(256), 0, 0, pk);
+  HIPCHECK(hipGetLastError());
+  RolloutArgs ra{};
+  ra.ph = phys_args(E);
+  PhysArgs& a = ra.ph;
+  a.K = H; a.act = A; a.t0 = 0; a.astep = 1; a.rstep = 1; a.R = R; a.D = D; a.reset_noise = reset_noise;
+  chunk_schedule(a, E->pgrid);
+  a.fbase = E->qdone;
+  a.qpar = E->qpar;
+  a.xlocal = E->xlocal && !E->fences;
+  ra.po = TileArgs{Wt, tl, mean, var, act_noise, O, A, LP, V, Vlast, H};
+  ra.tflags = E->tflags;
+  ra.tbase = E->tdone;
+  const bool prof = E->prof_on != 0 && !wp;
+  if (prof) prof_mark(E->ev_phys, E->n_phys);
+  hipLaunchKernelGGL(k_rollout, dim3((unsigned)E->pgrid), dim3(kPhysThreads), 0, 0, ra);
+  HIPCHECK(hipGetLastError());
+  if (prof) prof_mark(E->ev_phys, E->n_phys);
+  E->qdone += (unsigned)(H * a.nch);
+  E->tdone += (unsigned)H + 1u;
+  E->qpar ^= 1;
+  HIPCHECK(hipMemcpyAsync(E->h_qerr, E->qerr, sizeof(int), hipMemcpyDeviceToHost, 0));
+}
+
 static void rollout_impl(EnvState* E, int H, const float* W, const float* mean, const float* var, float* O, float* A,
                          float* LP, float* V, float* R, float* D, float* Vlast, const float* act_noise,
                          const float* reset_noise, float* wp = nullptr, long wp_cap = 0) {
   poll_queue_error(E);
   if (H < 0) H = 0;   // no control step; the bootstrap value is still computed (as the reference's k_rollout)
+  if (E->fused && fused_shape(E->shape)) {
+    rollout_fused(E, H, W, mean, var, O, A, LP, V, R, D, Vlast, act_noise, reset_noise, wp, wp_cap);
+    return;
+  }
   PackedPolicy pp;
   pack_policy(E, W, &pp, wp, wp_cap);
   PhysArgs pa = phys_args(E);
@@ -903,6 +1138,10 @@ void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
   HIPCHECK(hipMemset(E->qctr, 0, 2 * kQueues * sizeof(unsigned)));
   HIPCHECK(hipMemset(E->qerr, 0, sizeof(int)));
   E->qdone = 0; E->qpar = 0;
+  HIPCHECK(hipMalloc(&E->tflags, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
+  HIPCHECK(hipMemset(E->tflags, 0, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
+  E->tdone = 0;
+  E->fused = 1;
   {
     // persistent grid: every resident block of k_physics, in whole rounds of the kQueues queues,
     // and no more blocks than there are pairs (rounded up to the queues)
@@ -951,7 +1190,7 @@ void g1_env_destroy(void* h) {
   check_queue(E);
   void* bufs[] = {E->qp,       E->qv,      E->pa,        E->steps,   E->rng,  E->dact,
                   E->zero_act, E->bench_r, E->bench_d,   E->ncon_hist, E->Wp,  E->dout,
-                  E->qflags,   E->qctr,    E->qerr,      E->qacc_e,  E->qacc_vx};
+                  E->qflags,   E->qctr,    E->qerr,      E->qacc_e,  E->qacc_vx, E->tflags, E->Wt};
   for (void* b : bufs)
     if (b) HIPCHECK(hipFree(b));
   if (E->h_act) HIPCHECK(hipHostFree(E->h_act));
@@ -1181,6 +1420,13 @@ int g1_env_check(void* h) {
   int err = 0;
   HIPCHECK(hipMemcpy(&err, E->qerr, sizeof(int), hipMemcpyDeviceToHost));
   return err;
+}
+
+int g1_env_set_fused(void* h, int on) {
+  EnvState* E = (EnvState*)h;
+  if (on != 0 && on != 1) return -1;
+  E->fused = on;
+  return (on && !fused_shape(E->shape)) ? 1 : 0;
 }
 
 int g1_env_set_handover(void* h, int fences) {

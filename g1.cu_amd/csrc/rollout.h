@@ -1,0 +1,246 @@
+// rollout.h -- the policy of one 16-world tile on one wave, for the single-launch rollout (k_rollout).
+//
+// The persistent physics kernel also runs the policy: when the 8 world pairs of a tile have
+// finished control step t, one wave computes observation, normalisation, MLP, sampling and
+// log-probability for the tile's 16 worlds, and the pairs' next physics items start from its
+// actions. The MLP runs on v_mfma_f32_16x16x4f32 with the weights as the A operand and the
+// activations as the B operand: lane l holds world j = l % 16 throughout, as input feature group
+// g = l / 16 for a B operand and as output rows 4g..4g+3 of a 16-row tile in the accumulator
+// (D[4 (l / 16) + v][l % 16] in register v). A layer's accumulator registers are therefore the
+// next layer's B operands without any data movement, provided the next layer's K dimension is
+// taken in that order: k-step s of a layer after the first reads input neuron
+// kappa(s, g) = 16 (s / 4) + 4 g + s % 4 (the first layer reads observation feature 4 s + g). The
+// weights are packed to match (k_pack_tiles), so each lane's operands of four k-steps are one
+// float4 load and the 64 lanes of one load read one contiguous 1 KB line.
+//
+// Reference: obs src/g1_env.cu:46-81; normalise/clamp :298-302; MLP :219-239 (the AC of
+// scripts/ppo.py:85-99, packing scripts/ppo_fused.py:35-44); sampling + log-prob :308-318.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "policy.h"
+
+namespace g1k {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTilePairs = 8;                  // world pairs per policy tile (one queue's pairs)
+constexpr int kTileW = 2 * kTilePairs;         // 16 worlds: the N dimension of the 16x16x4 MFMA
+constexpr int kTileMaxHidden = 256;            // widest hidden layer of the one-launch rollout
+constexpr int kTileMaxT = kTileMaxHidden / 16; // 16-row output tiles of the widest layer
+constexpr int kObsSteps = 28;                  // k-steps of the first layer: 100 features, padded to 112
+constexpr int kHeadT = 2;                      // head rows: mu 0..28, value 29, 30..31 zero
+
+// Packed layout of a two-hidden-layer policy for the tile MLP (floats, offsets into one buffer):
+// layer L's weights as [T][s / 4][lane][s % 4] (T: 16-row output tile, s: k-step), then its bias in
+// natural row order padded to whole tiles; the log standard deviation last (29 values + 3 zeros).
+struct TileLayout {
+  int nT[3];        // output tiles of layer 0, layer 1, head
+  int nQ[3];        // k-step quads of layer 0, layer 1, head (= input width / 16 after layer 0)
+  long woff[3], boff[3];
+  long ls_off;
+  long total;
+  int act;          // 0 tanh, 1 ELU
+};
+
+__host__ __device__ inline TileLayout tile_layout(int h0, int h1, int act) {
+  TileLayout t{};
+  t.nT[0] = h0 / 16; t.nT[1] = h1 / 16; t.nT[2] = kHeadT;
+  t.nQ[0] = kObsSteps / 4; t.nQ[1] = h0 / 16; t.nQ[2] = h1 / 16;
+  long off = 0;
+  for (int L = 0; L < 3; ++L) {
+    t.woff[L] = off;
+    off += (long)t.nT[L] * t.nQ[L] * 64 * 4;
+    t.boff[L] = off;
+    off += (long)t.nT[L] * 16;
+  }
+  t.ls_off = off;
+  t.total = off + 32;
+  t.act = act;
+  return t;
+}
+
+// Input feature read by k-step s, lane group g of layer L.
+__host__ __device__ __forceinline__ int tile_kappa(int L, int s, int g) {
+  return L == 0 ? 4 * s + g : 16 * (s >> 2) + 4 * g + (s & 3);
+}
+
+struct TileArgs {
+  const float* Wt;          // packed (TileLayout)
+  TileLayout tl;
+  const float* mean;        // [100] frozen observation statistics
+  const float* var;
+  const float* act_noise;   // [H][N][29] or null (Philox)
+  float* O; float* A; float* LP; float* V; float* Vlast;
+  int H;
+};
+
+// The 16 worlds of tile u of queue q: pairs p = q + 32 (8 u + i), i < 8, worlds 2p and 2p + 1;
+// world slot j holds pair i = j / 2, world 2p + (j & 1).
+__device__ __forceinline__ int tile_world(int q, int u, int j, int queues) {
+  const int p = q + queues * (kTilePairs * u + (j >> 1));
+  return 2 * p + (j & 1);
+}
+
+__device__ __forceinline__ f32x4 mfma4(f32x4 w, const float* x, f32x4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w.x, x[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w.y, x[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w.z, x[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w.w, x[3], acc, 0, 0, 0);
+  return acc;
+}
+
+template <class LoadT>
+__device__ __forceinline__ float obs_of(LoadT ld, const float* qp, const float* qv, const float* pa, float qw, float qx,
+                                        float qy, float qz, int i) {
+  if (i < 6) return ld(qv + i);
+  if (i < 9) {
+    const float r = (i == 6)   ? 2.f * __builtin_fmaf(-qw, qy, qx * qz)
+                    : (i == 7) ? 2.f * __builtin_fmaf(qw, qx, qy * qz)
+                               : __builtin_fmaf(-2.f, __builtin_fmaf(qy, qy, qx * qx), 1.f);
+    return -r;
+  }
+  if (i < 38) return ld(qp + 7 + (i - 9));
+  if (i < 67) return ld(qv + 6 + (i - 38));
+  if (i < 96) return ld(pa + i - 67);
+  return i == 96 ? 0.8f : 0.f;
+}
+
+constexpr int kTileLd = kTileMaxHidden + 4;   // LDS row pitch of the hidden activations (floats)
+
+// Policy of control step t (t == H: the bootstrap value only) for the tile's worlds w_j, given by
+// the caller (valid: w_j < N). State is read with `ld` (from the L2: other waves of the launch
+// wrote it). hid: LDS scratch of kTileW x kTileLd floats (the hidden activations, world-major;
+// the log-prob terms reuse it).
+template <class LoadT>
+__device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos, const float* qvel, const float* pact,
+                                            const unsigned* rngc, unsigned long long seed, int N, int t, int w,
+                                            bool valid, float* hid, LoadT ld) {
+  // the lane index goes through an opaque asm so that nothing derived from it is hoisted out of the
+  // caller's item loop (where it would stay live beside the physics items' registers)
+  int lane = threadIdx.x & 63;
+  __asm__ volatile("" : "+v"(lane));
+  const int j = lane & 15, g = lane >> 4;
+  const TileLayout& T = a.tl;
+  const int wc = valid ? w : N - 1;
+  const float* qp = qpos + (long)wc * kNQ;
+  const float* qv = qvel + (long)wc * kNV;
+  const float* pa = pact + (long)wc * kAct;
+  const float qw = ld(qp + 3), qx = ld(qp + 4), qy = ld(qp + 5), qz = ld(qp + 6);
+
+  // ---- observation (raw to O, reference: src/g1_env.cu:69-81) and frozen normalisation
+  // (:298-302): lane (j, g) forms features 4 s + g of its world, the first layer's B operands
+  float x[kObsSteps];
+#pragma unroll
+  for (int s = 0; s < kObsSteps; ++s) {
+    const int k = 4 * s + g;
+    float z = 0.f;
+    if (k < kObs) {
+      const float o = obs_of(ld, qp, qv, pa, qw, qx, qy, qz, k);
+      if (valid && t < a.H) a.O[((long)t * N + w) * kObs + k] = o;
+      const float dv = sqrtf(a.var[k] + 1e-8f);
+      z = div_rn(o - a.mean[k], dv, rcp_rn(dv));
+      if (z < -10.f) z = -10.f; else if (z > 10.f) z = 10.f;
+    }
+    x[s] = z;
+  }
+
+  // ---- layer 0, one 16-row output tile at a time: rows 16 T + 4 g + v of world j go to
+  // hid[j][16 T + 4 g + v] (the order in which the next layer's k-steps read them)
+  const float4* W0 = reinterpret_cast<const float4*>(a.Wt + T.woff[0]) + lane;
+  float* hrow = hid + j * kTileLd + 4 * g;
+#pragma unroll 1
+  for (int ot = 0; ot < T.nT[0]; ++ot) {
+    const float4 bv = *reinterpret_cast<const float4*>(a.Wt + T.boff[0] + 16 * ot + 4 * g);
+    f32x4 acc = {bv.x, bv.y, bv.z, bv.w};
+    float4 wv[kObsSteps / 4];
+#pragma unroll
+    for (int qd = 0; qd < kObsSteps / 4; ++qd) wv[qd] = W0[((long)ot * T.nQ[0] + qd) * 64];
+#pragma unroll
+    for (int qd = 0; qd < kObsSteps / 4; ++qd) acc = mfma4(f32x4{wv[qd].x, wv[qd].y, wv[qd].z, wv[qd].w}, x + 4 * qd, acc);
+    *reinterpret_cast<float4*>(hrow + 16 * ot) =
+        float4{act_fn(acc[0], T.act), act_fn(acc[1], T.act), act_fn(acc[2], T.act), act_fn(acc[3], T.act)};
+  }
+  __syncthreads();
+
+  // ---- layer 1 tile by tile (B operands from hid), each tile's activations fed into the head
+  const float4* W1 = reinterpret_cast<const float4*>(a.Wt + T.woff[1]) + lane;
+  const float4* Wh = reinterpret_cast<const float4*>(a.Wt + T.woff[2]) + lane;
+  f32x4 hd[kHeadT];
+#pragma unroll
+  for (int ht = 0; ht < kHeadT; ++ht) {
+    const float4 bv = *reinterpret_cast<const float4*>(a.Wt + T.boff[2] + 16 * ht + 4 * g);
+    hd[ht] = f32x4{bv.x, bv.y, bv.z, bv.w};
+  }
+#pragma unroll 1
+  for (int ot = 0; ot < T.nT[1]; ++ot) {
+    const float4 bv = *reinterpret_cast<const float4*>(a.Wt + T.boff[1] + 16 * ot + 4 * g);
+    f32x4 acc = {bv.x, bv.y, bv.z, bv.w};
+    const float4* wrow = W1 + (long)ot * T.nQ[1] * 64;
+#pragma unroll 4
+    for (int qd = 0; qd < T.nQ[1]; ++qd) {
+      const float4 wv = wrow[(long)qd * 64];
+      const float4 hv = *reinterpret_cast<const float4*>(hrow + 16 * qd);
+      const float xb[4] = {hv.x, hv.y, hv.z, hv.w};
+      acc = mfma4(f32x4{wv.x, wv.y, wv.z, wv.w}, xb, acc);
+    }
+    const float h2[4] = {act_fn(acc[0], T.act), act_fn(acc[1], T.act), act_fn(acc[2], T.act), act_fn(acc[3], T.act)};
+#pragma unroll
+    for (int ht = 0; ht < kHeadT; ++ht) {
+      const float4 wv = Wh[((long)ht * T.nQ[2] + ot) * 64];
+      hd[ht] = mfma4(f32x4{wv.x, wv.y, wv.z, wv.w}, h2, hd[ht]);
+    }
+  }
+  __syncthreads();   // hid is free again (the log-prob terms below reuse it)
+  float* lds = hid;
+
+  // ---- value (head row 29: tile 1, rows 4 g + v with g = 3, v = 1)
+  if (g == 3 && valid) {
+    if (t == a.H) a.Vlast[w] = hd[1][1];
+    else a.V[(long)t * N + w] = hd[1][1];
+  }
+  if (t == a.H) return;
+
+  // ---- sampling + log-prob (reference: src/g1_env.cu:308-318): lane g owns actions 4g..4g+3 and
+  // 16+4g..16+4g+3, i.e. the action pairs 2g, 2g+1, 8+2g, 9+2g; both Box-Muller normals of one
+  // Philox counter go to the actions of one pair. The log-prob terms go through LDS so that one
+  // lane sums each world's 29 terms in action order.
+  const float LOG2PI = 1.8378770664093453f;
+  const float* ls = a.Wt + T.ls_off;
+  const unsigned rng = valid ? ld(rngc + wc) : 0u;
+  const long ab = ((long)t * N + w) * kAct;
+#pragma unroll
+  for (int ht = 0; ht < kHeadT; ++ht) {
+#pragma unroll
+    for (int hp = 0; hp < 2; ++hp) {
+      const int i0 = 16 * ht + 4 * g + 2 * hp;   // actions i0, i0 + 1
+      if (i0 < kAct) {
+        float nz[2];
+        if (a.act_noise) {
+          nz[0] = valid ? a.act_noise[ab + i0] : 0.f;
+          nz[1] = (valid && i0 + 1 < kAct) ? a.act_noise[ab + i0 + 1] : 0.f;
+        } else {
+          rng_normal2(seed, wc, rng, kStreamAction, i0 >> 1, nz[0], nz[1]);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int i = i0 + e;
+          if (i < kAct) {
+            const float lsi = ls[i];
+            if (valid) a.A[ab + i] = hd[ht][2 * hp + e] + expf(lsi) * nz[e];
+            lds[j * 32 + i] = -0.5f * nz[e] * nz[e] - lsi - 0.5f * LOG2PI;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (g == 0 && valid) {
+    float lpsum = 0.f;
+    for (int i = 0; i < kAct; ++i) lpsum += lds[j * 32 + i];
+    a.LP[(long)t * N + w] = lpsum;
+  }
+  __syncthreads();
+}
+
+}  // namespace g1k

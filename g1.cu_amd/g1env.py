@@ -54,6 +54,7 @@ SIGNATURES = {
     "g1_env_profile_read": (None, [_vp, _c.POINTER(_c.c_double)]),
     "g1_env_check": (_c.c_int, [_vp]),
     "g1_env_set_handover": (_c.c_int, [_vp, _c.c_int]),
+    "g1_env_set_fused": (_c.c_int, [_vp, _c.c_int]),
     "g1_probe_qacc": (None, [_c.c_int, _vp, _vp, _vp, _c.c_int, _c.c_int, _c.c_int, _c.c_float, _vp, _vp]),
     "g1_probe_substep": (None, [_c.c_int, _vp, _vp, _vp, _c.c_int, _c.c_int, _c.c_float, _vp, _vp]),
     "g1_probe_policy": (_c.c_int, [_c.c_int, _c.c_int, _ip, _c.c_int, _vp, _vp, _vp, _vp]),
@@ -176,6 +177,14 @@ class Env:
     def set_handover(self, fences):
         if lib.g1_env_set_handover(self.h, int(fences)) != 0:
             raise RuntimeError("hand-over mode unavailable on this placement")
+
+    def set_fused(self, on):
+        """One persistent launch per rollout (True, the default) or per-step launches (False).
+        Returns whether the one-launch form applies to the current policy shape."""
+        rc = lib.g1_env_set_fused(self.h, int(bool(on)))
+        if rc < 0:
+            raise ValueError("invalid rollout form")
+        return bool(on) and rc == 0
 
     def ncon_hist(self, enable=True):
         out = (_c.c_ulonglong * 9)()

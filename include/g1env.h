@@ -113,6 +113,13 @@ int g1_env_check(void* h);
  * slower). Returns 0, or -1 when the mode is unavailable. */
 int g1_env_set_handover(void* h, int fences);
 
+/* Rollout form: on = 1 (the default) runs g1_rollout as one persistent launch that interleaves the
+ * policy of 16-world tiles with the physics work items; on = 0 launches the policy and the physics
+ * once per control step. The one-launch form covers policies of two hidden layers of at most 256
+ * units (multiples of 16); other shapes always take the per-step form. Returns 0, 1 when on = 1 but
+ * the current policy shape takes the per-step form, or -1 for an invalid argument. */
+int g1_env_set_fused(void* h, int on);
+
 /* Parity probes running the same device code as the rollout on caller states (all DEVICE,
  * asynchronous): n worlds, qpos [n*36], qvel [n*35], qacc out [n*35], ncon out [n].
  * g1_probe_qacc: tau [n*35] on the hinge dofs; damped folds dt*kd into the factor (the env's

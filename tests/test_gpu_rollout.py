@@ -175,15 +175,17 @@ def test_rollout_teacher_forced_config4_slice(g1, orc):
     _assert_rows(rows)
 
 
-@pytest.mark.parametrize("fences", [0, 1])
-def test_rollout_matches_oracle_free_run(g1, orc, fences):
+@pytest.mark.parametrize("fences,fused", [(0, True), (1, True), (0, False), (1, False)])
+def test_rollout_matches_oracle_free_run(g1, orc, fences, fused):
     """A short rollout (N=96, H=3) with no teacher forcing: every output equals the oracle's own
-    rollout within the per-step bound, through the L2 state hand-over (fences=0) and through the
+    rollout within the per-step bound, in both rollout forms (one persistent launch, or policy and
+    physics launches per control step), through the L2 state hand-over (fences=0) and through the
     agent-scope fence hand-over that the work queue falls back to off the round-robin placement."""
     N, H = 96, 3
     qp, qv, pa, steps, W, mean, var, an, rn = _setup(N, H, 11)
     with g1.Env(N, substeps=10, pgs_iters=8, seed=1) as env:
         env.set_handover(fences)
+        assert env.set_fused(fused) == fused
         env.set_state(qp, qv, pa, steps)
         out = _rollout(g1, env, W, mean, var, H, an, rn)
         g = env.get_state()
