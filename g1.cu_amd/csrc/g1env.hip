@@ -315,21 +315,24 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
 
 // ====================================================================== the rollout in one launch
 // k_rollout runs a whole g1_rollout: the physics items of k_physics for H control steps, and the
-// policy of every control step on 16-world tiles (policy_tile) as work items of the same queues.
-// Tile u of queue q holds the pairs q + 32 (8 u + i), i < 8, so its items stay on the queue's XCD.
+// policy of every control step on 16-world tiles (policy_tile). Tile u of queue q holds the pairs
+// q + 32 (8 u + i), i < 8, so all its work stays on the queue's XCD.
 // Claim order within a queue (nq pairs, ntq tiles, nch substep chunks per control step):
-//   P(0, all tiles); then for t < H: C(t, c, all pairs) for c < nch - 1, then per tile u:
-//   [C(t, nch - 1, the tile's pairs), P(t + 1, u)]
-// where P(t, u) is the policy of step t on tile u (P(H, u): the bootstrap value) and C(t, c, p)
-// chunk c of pair p's step t. Waits: C(t, c > 0, p) on C(t, c - 1, p) (the pair's flag);
-// C(t, 0, p) on P(t, u(p)) (the tile's flag); P(t > 0, u) on C(t - 1, nch - 1, p) of its pairs. Each
-// waited-for item comes earlier in the claim order and was claimed by a running wave, so every wait
-// ends (k_physics' argument).
+//   P(0, all tiles), then C(t, c, all pairs) for t < H, c < nch,
+// where P(0, u) is the policy of step 0 on tile u and C(t, c, p) chunk c of pair p's step t. The
+// policy of a later step is not claimed: the wave that completes a tile's last pair of step t (the
+// tile's completion count, raised by every pair's last chunk after its release, reaches the tile's
+// pair count; that wave clears it) runs P(t + 1, u) at once, so no wave waits for a tile to complete;
+// P(H, u) computes the bootstrap value. Waits: C(t, c > 0, p) on C(t, c - 1, p) (the pair's flag,
+// claimed earlier); C(t, 0, p) on P(t, u(p)) (the tile's flag), which either was claimed earlier or
+// runs in the wave that completed the tile's step t - 1, a running wave. So every wait ends.
 struct RolloutArgs {
   PhysArgs ph;              // K = H control steps, actions from A
   TileArgs po;
   unsigned* tflags;         // [kQueues * tiles per queue] policy steps completed per tile
   unsigned tbase;           // value every tile flag holds when this launch starts
+  unsigned* tcount;         // [kQueues * tiles per queue] pairs of a tile done with the current step
+                            // (zero between launches)
 };
 
 // LDS of a k_rollout block: the two worlds' physics scratch, or a policy tile's hidden activations
@@ -347,14 +350,12 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
   const int npairs = (a.N + 1) >> 1;
   const int nch = a.nch, H = a.K;
   int qc = q;
-  unsigned nq = 0, ntq = 0, nfull = 0, per_step = 0, nitems = 0;
+  unsigned nq = 0, ntq = 0, nitems = 0;
   unsigned* ctr = nullptr;
   auto set_queue = [&](int qq) {
     nq = npairs > qq ? (unsigned)((npairs - qq + kQueues - 1) / kQueues) : 0u;
     ntq = (nq + kTilePairs - 1) / kTilePairs;
-    nfull = nq / kTilePairs;
-    per_step = (unsigned)nch * nq + ntq;
-    nitems = nq ? ntq + (unsigned)H * per_step : 0u;
+    nitems = nq ? ntq + (unsigned)(H * nch) * nq : 0u;
     ctr = a.qctr + a.qpar * kQueues + qq;
   };
   set_queue(q);
@@ -362,6 +363,15 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
   if (a.xlocal && threadIdx.x == 0 && xcc_id() != q % kXcds)
     __hip_atomic_store(a.qerr, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   float* scratch_lds = reinterpret_cast<float*>(lds_raw);
+  // policy of step t on tile u of queue qq (its np pairs complete through step t - 1)
+  auto policy = [&](int qq, int u, int np, int t) {
+    const int jw = threadIdx.x & 15;
+    const int w = tile_world(qq, u, jw, kQueues);
+    const bool valid = (jw >> 1) < np && w < a.N;
+    policy_tile(ra.po, a.qp, a.qv, a.pa, a.rng, a.seed, a.N, t, w, valid, scratch_lds,
+                [](const auto* ptr) { return ld_l2(ptr); });
+    release_flag(ra.tflags + qq + kQueues * u, ra.tbase + (unsigned)t + 1u, a.xlocal);
+  };
 
 #pragma unroll 1
   for (;;) {
@@ -374,52 +384,41 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
       set_queue(qc);
       continue;
     }
-    // ---- decode: policy item (t, u) or physics item (t, c, m)
-    int t, u = -1, c = 0, m = 0;
     if (it < ntq) {
-      t = 0; u = (int)it;
-    } else {
-      const unsigned r = it - ntq;
-      t = (int)(r / per_step);
-      const unsigned rr = r - (unsigned)t * per_step;
-      const unsigned early = (unsigned)(nch - 1) * nq;
-      if (rr < early) {
-        c = (int)(rr / nq); m = (int)(rr - (unsigned)c * nq);
-      } else {
-        const unsigned r2 = rr - early;
-        unsigned uu, o, np;
-        if (r2 < (kTilePairs + 1) * nfull) { uu = r2 / (kTilePairs + 1); o = r2 - uu * (kTilePairs + 1); np = kTilePairs; }
-        else { uu = nfull; o = r2 - (kTilePairs + 1) * nfull; np = nq - kTilePairs * nfull; }
-        if (o < np) { c = nch - 1; m = (int)(kTilePairs * uu + o); }
-        else { u = (int)uu; t += 1; }
-      }
+      const int u = (int)it;
+      policy(qc, u, (int)min((unsigned)kTilePairs, nq - kTilePairs * it), 0);
+      continue;
     }
-    if (u >= 0) {
-      // ---- policy of step t on tile u
-      const int tile = qc + kQueues * u;
-      const int np = (int)min((unsigned)kTilePairs, nq - kTilePairs * (unsigned)u);
-      if (t > 0) {
-#pragma unroll 1
-        for (int i = 0; i < np; ++i)
-          wait_flag(a.flags + qc + kQueues * (kTilePairs * u + i), a.fbase + (unsigned)(t * nch), a.qerr, a.xlocal);
-      }
-      const int jw = threadIdx.x & 15;
-      const int w = tile_world(qc, u, jw, kQueues);
-      const bool valid = (jw >> 1) < np && w < a.N;
-      policy_tile(ra.po, a.qp, a.qv, a.pa, a.rng, a.seed, a.N, t, w, valid, scratch_lds,
-                  [](const auto* ptr) { return ld_l2(ptr); });
-      release_flag(ra.tflags + tile, ra.tbase + (unsigned)t + 1u, a.xlocal);
-    } else {
-      const int p = qc + kQueues * m;
-      const int jj = t * nch + c;
-      if (c > 0) wait_flag(a.flags + p, a.fbase + (unsigned)jj, a.qerr, a.xlocal);
-      else wait_flag(ra.tflags + qc + kQueues * (m / kTilePairs), ra.tbase + (unsigned)t + 1u, a.qerr, a.xlocal);
+    const unsigned r = it - ntq;
+    const int jj = (int)(r / nq), m = (int)(r - (unsigned)jj * nq);
+    const int t = jj / nch, c = jj - t * nch;
+    const int p = qc + kQueues * m;
+    const int u = m / kTilePairs;
+    if (c > 0) wait_flag(a.flags + p, a.fbase + (unsigned)jj, a.qerr, a.xlocal);
+    else wait_flag(ra.tflags + qc + kQueues * u, ra.tbase + (unsigned)t + 1u, a.qerr, a.xlocal);
+    {
       // the lane's model constants, formed here (opaque lane index) rather than held across items
       int lo = l;
       __asm__ volatile("" : "+v"(lo));
       const LaneModel L = lane_model(lo);
       physics_item(a, s, L, g, l, p, t, c, hcnt);
-      release_flag(a.flags + p, a.fbase + (unsigned)jj + 1u, a.xlocal);
+    }
+    release_flag(a.flags + p, a.fbase + (unsigned)jj + 1u, a.xlocal);
+    if (c == nch - 1) {
+      // this pair's step t is complete: count it for the tile; the wave completing the tile runs
+      // the tile's policy of step t + 1
+      const int np = (int)min((unsigned)kTilePairs, nq - kTilePairs * (unsigned)u);
+      unsigned old = 0;
+      if (threadIdx.x == 0)
+        old = __hip_atomic_fetch_add(ra.tcount + qc + kQueues * u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      old = __builtin_amdgcn_readfirstlane(old);
+      if (old + 1u == (unsigned)np) {
+        // no pair of the tile counts again before this policy's flag release: clear the count here
+        if (threadIdx.x == 0)
+          __hip_atomic_store(ra.tcount + qc + kQueues * u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!a.xlocal) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        policy(qc, u, np, t + 1);
+      }
     }
   }
   if (a.ncon_hist && l < 9 && hcnt) atomicAdd(&a.ncon_hist[l], (unsigned long long)hcnt);
@@ -819,6 +818,7 @@ struct EnvState {
   // one-launch rollout (k_rollout): policy tiles' flags, their completed-step count, packed weights
   int fused;        // 1: g1_rollout runs k_rollout when the policy shape allows it
   unsigned* tflags;
+  unsigned* tcount;
   unsigned tdone;
   float* Wt;
   long Wt_cap;
@@ -1048,6 +1048,7 @@ static void rollout_fused(EnvState* E, int H, const float* W, const float* mean,
   ra.po = TileArgs{Wt, tl, mean, var, act_noise, O, A, LP, V, Vlast, H};
   ra.tflags = E->tflags;
   ra.tbase = E->tdone;
+  ra.tcount = E->tcount;
   const bool prof = E->prof_on != 0 && !wp;
   if (prof) prof_mark(E->ev_phys, E->n_phys);
   hipLaunchKernelGGL(k_rollout, dim3((unsigned)E->pgrid), dim3(kPhysThreads), 0, 0, ra);
@@ -1140,6 +1141,8 @@ void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
   E->qdone = 0; E->qpar = 0;
   HIPCHECK(hipMalloc(&E->tflags, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
   HIPCHECK(hipMemset(E->tflags, 0, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
+  HIPCHECK(hipMalloc(&E->tcount, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
+  HIPCHECK(hipMemset(E->tcount, 0, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
   E->tdone = 0;
   E->fused = 1;
   {
@@ -1190,7 +1193,7 @@ void g1_env_destroy(void* h) {
   check_queue(E);
   void* bufs[] = {E->qp,       E->qv,      E->pa,        E->steps,   E->rng,  E->dact,
                   E->zero_act, E->bench_r, E->bench_d,   E->ncon_hist, E->Wp,  E->dout,
-                  E->qflags,   E->qctr,    E->qerr,      E->qacc_e,  E->qacc_vx, E->tflags, E->Wt};
+                  E->qflags,   E->qctr,    E->qerr,      E->qacc_e,  E->qacc_vx, E->tflags, E->tcount, E->Wt};
   for (void* b : bufs)
     if (b) HIPCHECK(hipFree(b));
   if (E->h_act) HIPCHECK(hipHostFree(E->h_act));
