@@ -336,8 +336,8 @@ struct RolloutArgs {
 };
 
 // LDS of a k_rollout block: the two worlds' physics scratch, or a policy tile's hidden activations
-constexpr size_t kRolloutLds = 2 * sizeof(WorldLds) > sizeof(float) * kTileW * kTileLd
-                                   ? 2 * sizeof(WorldLds) : sizeof(float) * kTileW * kTileLd;
+constexpr size_t kRolloutLds = 2 * sizeof(WorldLds) > sizeof(float) * kTileLds
+                                   ? 2 * sizeof(WorldLds) : sizeof(float) * kTileLds;
 
 __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
   __shared__ __align__(16) unsigned char lds_raw[kRolloutLds];

@@ -36,7 +36,8 @@ constexpr int kHeadT = 2;                      // head rows: mu 0..28, value 29,
 // natural row order padded to whole tiles; the log standard deviation last (29 values + 3 zeros).
 struct TileLayout {
   int nT[3];        // output tiles of layer 0, layer 1, head
-  int nQ[3];        // k-step quads of layer 0, layer 1, head (= input width / 16 after layer 0)
+  int nQ[3];        // k-step quads of layer 0, layer 1 (input width / 16 rounded up to a multiple
+                    // of 4; the padding holds zero weights), head (input width / 16)
   long woff[3], boff[3];
   long ls_off;
   long total;
@@ -46,7 +47,7 @@ struct TileLayout {
 __host__ __device__ inline TileLayout tile_layout(int h0, int h1, int act) {
   TileLayout t{};
   t.nT[0] = h0 / 16; t.nT[1] = h1 / 16; t.nT[2] = kHeadT;
-  t.nQ[0] = kObsSteps / 4; t.nQ[1] = h0 / 16; t.nQ[2] = h1 / 16;
+  t.nQ[0] = kObsSteps / 4; t.nQ[1] = 4 * ((h0 + 63) / 64); t.nQ[2] = h1 / 16;
   long off = 0;
   for (int L = 0; L < 3; ++L) {
     t.woff[L] = off;
@@ -107,11 +108,12 @@ __device__ __forceinline__ float obs_of(LoadT ld, const float* qp, const float* 
 }
 
 constexpr int kTileLd = kTileMaxHidden + 4;   // LDS row pitch of the hidden activations (floats)
+constexpr int kTileLds = kTileW * kTileLd + kTileMaxHidden;   // LDS floats of one tile's policy
 
 // Policy of control step t (t == H: the bootstrap value only) for the tile's worlds w_j, given by
 // the caller (valid: w_j < N). State is read with `ld` (from the L2: other waves of the launch
-// wrote it). hid: LDS scratch of kTileW x kTileLd floats (the hidden activations, world-major;
-// the log-prob terms reuse it).
+// wrote it). hid: LDS scratch of kTileLds floats: the hidden activations (kTileW x kTileLd,
+// world-major; the log-prob terms reuse them), then the second layer's bias.
 template <class LoadT>
 __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos, const float* qvel, const float* pact,
                                             const unsigned* rngc, unsigned long long seed, int N, int t, int w,
@@ -146,24 +148,62 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
   }
 
   // ---- layer 0, one 16-row output tile at a time: rows 16 T + 4 g + v of world j go to
-  // hid[j][16 T + 4 g + v] (the order in which the next layer's k-steps read them)
+  // hid[j][16 T + 4 g + v] (the order in which the next layer's k-steps read them). The weights and
+  // bias of tile T + 1 are loaded while tile T's MFMAs run (two register sets, used alternately).
   const float4* W0 = reinterpret_cast<const float4*>(a.Wt + T.woff[0]) + lane;
+  const float* B0 = a.Wt + T.boff[0] + 4 * g;
   float* hrow = hid + j * kTileLd + 4 * g;
-#pragma unroll 1
-  for (int ot = 0; ot < T.nT[0]; ++ot) {
-    const float4 bv = *reinterpret_cast<const float4*>(a.Wt + T.boff[0] + 16 * ot + 4 * g);
-    f32x4 acc = {bv.x, bv.y, bv.z, bv.w};
-    float4 wv[kObsSteps / 4];
-#pragma unroll
-    for (int qd = 0; qd < kObsSteps / 4; ++qd) wv[qd] = W0[((long)ot * T.nQ[0] + qd) * 64];
-#pragma unroll
-    for (int qd = 0; qd < kObsSteps / 4; ++qd) acc = mfma4(f32x4{wv[qd].x, wv[qd].y, wv[qd].z, wv[qd].w}, x + 4 * qd, acc);
-    *reinterpret_cast<float4*>(hrow + 16 * ot) =
-        float4{act_fn(acc[0], T.act), act_fn(acc[1], T.act), act_fn(acc[2], T.act), act_fn(acc[3], T.act)};
+  float* hb = hid + kTileW * kTileLd;
+  {
+    // the second layer's bias to LDS (read there once per output tile)
+    const int nb = 16 * T.nT[1];
+    if (4 * lane < nb) *reinterpret_cast<float4*>(hb + 4 * lane) = *reinterpret_cast<const float4*>(a.Wt + T.boff[1] + 4 * lane);
   }
+  const int nT0 = T.nT[0];
+  // (Every load below is issued on every path, the last tile's reloaded past the end, so that the
+  // number of loads in flight is the same on all paths and the waits count only older loads.)
+  float4 w0[2][kObsSteps / 4], b0[2];
+  // (the preloads are kept in use order: a wait for the first operand then counts the rest as newer)
+#pragma unroll
+  for (int qd = 0; qd < kObsSteps / 4; ++qd) {
+    w0[0][qd] = W0[(long)qd * 64];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  b0[0] = *reinterpret_cast<const float4*>(B0);
+#pragma unroll 1
+  for (int ot0 = 0; ot0 < nT0; ot0 += 2) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int ot = ot0 + r;
+      {
+        const int on = ot + 1 < nT0 ? ot + 1 : nT0 - 1;
+#pragma unroll
+        for (int qd = 0; qd < kObsSteps / 4; ++qd) w0[r ^ 1][qd] = W0[((long)on * (kObsSteps / 4) + qd) * 64];
+        b0[r ^ 1] = *reinterpret_cast<const float4*>(B0 + 16 * on);
+      }
+      if (ot < nT0) {
+        f32x4 acc = {b0[r].x, b0[r].y, b0[r].z, b0[r].w};
+#pragma unroll
+        for (int qd = 0; qd < kObsSteps / 4; ++qd)
+          acc = mfma4(f32x4{w0[r][qd].x, w0[r][qd].y, w0[r][qd].z, w0[r][qd].w}, x + 4 * qd, acc);
+        *reinterpret_cast<float4*>(hrow + 16 * ot) =
+            float4{act_fn(acc[0], T.act), act_fn(acc[1], T.act), act_fn(acc[2], T.act), act_fn(acc[3], T.act)};
+      }
+    }
+  }
+  // layer 1's k dimension is padded to whole 4-quad blocks: zero activations there (zero weights)
+#pragma unroll 1
+  for (int ot = nT0; ot < T.nQ[1]; ++ot) *reinterpret_cast<float4*>(hrow + 16 * ot) = float4{0.f, 0.f, 0.f, 0.f};
   __syncthreads();
 
-  // ---- layer 1 tile by tile (B operands from hid), each tile's activations fed into the head
+  // ---- layer 1 tile by tile (B operands from hid), each tile's activations fed into the head.
+  // Its weights are read in storage order (tile ot, k-quad qd) as blocks of 4 k-quads, kRing
+  // blocks ahead of the MFMAs that use them; each block's slot also carries the head weights of the
+  // block's tile (the same lines again for the tile's other blocks), so that every load is issued on
+  // every path.
+  constexpr int kRing = 4;
+  const int nQB = T.nQ[1] >> 2;            // 4-quad blocks per tile
+  const int nB = T.nT[1] * nQB;            // blocks of the layer
   const float4* W1 = reinterpret_cast<const float4*>(a.Wt + T.woff[1]) + lane;
   const float4* Wh = reinterpret_cast<const float4*>(a.Wt + T.woff[2]) + lane;
   f32x4 hd[kHeadT];
@@ -172,23 +212,62 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
     const float4 bv = *reinterpret_cast<const float4*>(a.Wt + T.boff[2] + 16 * ht + 4 * g);
     hd[ht] = f32x4{bv.x, bv.y, bv.z, bv.w};
   }
-#pragma unroll 1
-  for (int ot = 0; ot < T.nT[1]; ++ot) {
-    const float4 bv = *reinterpret_cast<const float4*>(a.Wt + T.boff[1] + 16 * ot + 4 * g);
-    f32x4 acc = {bv.x, bv.y, bv.z, bv.w};
-    const float4* wrow = W1 + (long)ot * T.nQ[1] * 64;
-#pragma unroll 4
-    for (int qd = 0; qd < T.nQ[1]; ++qd) {
-      const float4 wv = wrow[(long)qd * 64];
-      const float4 hv = *reinterpret_cast<const float4*>(hrow + 16 * qd);
-      const float xb[4] = {hv.x, hv.y, hv.z, hv.w};
-      acc = mfma4(f32x4{wv.x, wv.y, wv.z, wv.w}, xb, acc);
-    }
-    const float h2[4] = {act_fn(acc[0], T.act), act_fn(acc[1], T.act), act_fn(acc[2], T.act), act_fn(acc[3], T.act)};
+  float4 wr[kRing][4], whr[kRing][kHeadT];
+  int lt = 0, lq = 0;                      // tile and block within the tile of the next block loaded
 #pragma unroll
-    for (int ht = 0; ht < kHeadT; ++ht) {
-      const float4 wv = Wh[((long)ht * T.nQ[2] + ot) * 64];
-      hd[ht] = mfma4(f32x4{wv.x, wv.y, wv.z, wv.w}, h2, hd[ht]);
+  for (int r = 0; r < kRing; ++r) {
+    const int bl = lt * nQB + lq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wr[r][i] = W1[(long)(4 * bl + i) * 64];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int ht = 0; ht < kHeadT; ++ht) whr[r][ht] = Wh[((long)ht * T.nQ[2] + lt) * 64];
+    __builtin_amdgcn_sched_barrier(0);
+    if (bl + 1 < nB && ++lq == nQB) { lq = 0; ++lt; }
+  }
+  f32x4 acc;
+  {
+    const float4 bv = *reinterpret_cast<const float4*>(hb + 4 * g);
+    acc = f32x4{bv.x, bv.y, bv.z, bv.w};
+  }
+  int ot = 0, qb = 0;
+#pragma unroll 1
+  for (int b0 = 0; b0 < nB; b0 += kRing) {
+#pragma unroll
+    for (int r = 0; r < kRing; ++r) {
+      const int b = b0 + r;
+      if (b < nB) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 hv = *reinterpret_cast<const float4*>(hrow + 16 * (4 * qb + i));
+          const float xb[4] = {hv.x, hv.y, hv.z, hv.w};
+          acc = mfma4(f32x4{wr[r][i].x, wr[r][i].y, wr[r][i].z, wr[r][i].w}, xb, acc);
+        }
+        if (++qb == nQB) {
+          // tile ot done: its activations are the head's k-quad ot
+          const float h2[4] = {act_fn(acc[0], T.act), act_fn(acc[1], T.act), act_fn(acc[2], T.act),
+                               act_fn(acc[3], T.act)};
+#pragma unroll
+          for (int ht = 0; ht < kHeadT; ++ht)
+            hd[ht] = mfma4(f32x4{whr[r][ht].x, whr[r][ht].y, whr[r][ht].z, whr[r][ht].w}, h2, hd[ht]);
+          qb = 0;
+          ++ot;
+          if (ot < T.nT[1]) {
+            const float4 bv = *reinterpret_cast<const float4*>(hb + 16 * ot + 4 * g);
+            acc = f32x4{bv.x, bv.y, bv.z, bv.w};
+          }
+        }
+      }
+      // refill the slot in place (no register copy of a value still in flight), on every path; past
+      // the last block the last block is loaded again
+      const int bl = lt * nQB + lq;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wr[r][i] = W1[(long)(4 * bl + i) * 64];
+#pragma unroll
+      for (int ht = 0; ht < kHeadT; ++ht) whr[r][ht] = Wh[((long)ht * T.nQ[2] + lt) * 64];
+      if (bl + 1 < nB && ++lq == nQB) { lq = 0; ++lt; }
     }
   }
   __syncthreads();   // hid is free again (the log-prob terms below reuse it)
