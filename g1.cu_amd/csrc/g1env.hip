@@ -426,7 +426,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
 
 // Pack torch-order weights (W0, b0, W1, b1, Wmu, bmu, Wv, bv, log_std) into the tile layout.
 struct TilePackArgs {
-  const float* W; float* Wt; TileLayout tl; int h0, h1;
+  const float* W; const float* mean; const float* var; float* Wt; TileLayout tl; int h0, h1;
 };
 __global__ void k_pack_tiles(TilePackArgs a) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -435,7 +435,17 @@ __global__ void k_pack_tiles(TilePackArgs a) {
   const long oW0 = 0, ob0 = oW0 + (long)a.h0 * kObs, oW1 = ob0 + a.h0, ob1 = oW1 + (long)a.h1 * a.h0,
              oWmu = ob1 + a.h1, obmu = oWmu + (long)kAct * a.h1, oWv = obmu + kAct, obv = oWv + a.h1, ols = obv + 1;
   float v = 0.f;
-  if (idx >= T.ls_off) {
+  if (idx >= T.nrm_off) {
+    // normalisation constants of feature 4 s + g at [c][g][s] (the divisor as the split policy's)
+    const int rel = (int)(idx - T.nrm_off), c = rel / (4 * kObsSteps), r = rel - c * 4 * kObsSteps;
+    const int g = r / kObsSteps, k = 4 * (r - g * kObsSteps) + g;
+    if (k < kObs) {
+      const float dv = sqrtf(a.var[k] + 1e-8f);
+      v = c == 0 ? a.mean[k] : (c == 1 ? dv : rcp_rn(dv));
+    } else {
+      v = c == 0 ? 0.f : 1.f;
+    }
+  } else if (idx >= T.ls_off) {
     const int i = (int)(idx - T.ls_off);
     v = i < kAct ? a.W[ols + i] : 0.f;
   } else {
@@ -1034,7 +1044,7 @@ static void rollout_fused(EnvState* E, int H, const float* W, const float* mean,
   } else if (tl.total > wp_cap) {
     fail("rollout: tile-packed policy larger than its buffer");
   }
-  TilePackArgs pk{W, Wt, tl, E->shape.hid[0], E->shape.hid[1]};
+  TilePackArgs pk{W, mean, var, Wt, tl, E->shape.hid[0], E->shape.hid[1]};
   hipLaunchKernelGGL(k_pack_tiles, dim3((unsigned)((tl.total + 255) / 256)), dim3(256), 0, 0, pk);
   HIPCHECK(hipGetLastError());
   RolloutArgs ra{};
@@ -1045,7 +1055,7 @@ static void rollout_fused(EnvState* E, int H, const float* W, const float* mean,
   a.fbase = E->qdone;
   a.qpar = E->qpar;
   a.xlocal = E->xlocal && !E->fences;
-  ra.po = TileArgs{Wt, tl, mean, var, act_noise, O, A, LP, V, Vlast, H};
+  ra.po = TileArgs{Wt, tl, act_noise, O, A, LP, V, Vlast, H};
   ra.tflags = E->tflags;
   ra.tbase = E->tdone;
   ra.tcount = E->tcount;

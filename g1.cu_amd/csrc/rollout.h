@@ -33,13 +33,16 @@ constexpr int kHeadT = 2;                      // head rows: mu 0..28, value 29,
 
 // Packed layout of a two-hidden-layer policy for the tile MLP (floats, offsets into one buffer):
 // layer L's weights as [T][s / 4][lane][s % 4] (T: 16-row output tile, s: k-step), then its bias in
-// natural row order padded to whole tiles; the log standard deviation last (29 values + 3 zeros).
+// natural row order padded to whole tiles; the log standard deviation (29 values + 3 zeros); last
+// the observation normalisation as [3][g][s] for feature 4 s + g: mean, d = RN(sqrt(var + 1e-8))
+// and RN(1 / d) (features past 100: 0, 1, 1), so that lane group g reads its own as float4s.
 struct TileLayout {
   int nT[3];        // output tiles of layer 0, layer 1, head
   int nQ[3];        // k-step quads of layer 0, layer 1 (input width / 16 rounded up to a multiple
                     // of 4; the padding holds zero weights), head (input width / 16)
   long woff[3], boff[3];
   long ls_off;
+  long nrm_off;
   long total;
   int act;          // 0 tanh, 1 ELU
 };
@@ -56,7 +59,8 @@ __host__ __device__ inline TileLayout tile_layout(int h0, int h1, int act) {
     off += (long)t.nT[L] * 16;
   }
   t.ls_off = off;
-  t.total = off + 32;
+  t.nrm_off = off + 32;
+  t.total = t.nrm_off + 3 * 4 * kObsSteps;
   t.act = act;
   return t;
 }
@@ -69,8 +73,6 @@ __host__ __device__ __forceinline__ int tile_kappa(int L, int s, int g) {
 struct TileArgs {
   const float* Wt;          // packed (TileLayout)
   TileLayout tl;
-  const float* mean;        // [100] frozen observation statistics
-  const float* var;
   const float* act_noise;   // [H][N][29] or null (Philox)
   float* O; float* A; float* LP; float* V; float* Vlast;
   int H;
@@ -91,29 +93,38 @@ __device__ __forceinline__ f32x4 mfma4(f32x4 w, const float* x, f32x4 acc) {
   return acc;
 }
 
-template <class LoadT>
-__device__ __forceinline__ float obs_of(LoadT ld, const float* qp, const float* qv, const float* pa, float qw, float qx,
-                                        float qy, float qz, int i) {
-  if (i < 6) return ld(qv + i);
-  if (i < 9) {
+constexpr int kObsLoads = 25;   // k-steps of the first layer that read a state value (4 s + g < 100)
+
+// Observation feature i (reference: src/g1_env.cu:69-81): base angular and linear velocity (qvel
+// 0..5), gravity in the base frame (from the base quaternion), joint positions (qpos 7..35), joint
+// velocities (qvel 6..34), previous action, the command (0.8) and three zeros. obs_src gives the
+// state value feature i copies (a valid address for the others, whose value obs_value forms).
+__device__ __forceinline__ const float* obs_src(const float* qp, const float* qv, const float* pa, int i) {
+  const float* p = qv;
+  p = i < 6 ? qv + i : p;
+  p = (i >= 9 && i < 38) ? qp + (i - 2) : p;
+  p = (i >= 38 && i < 67) ? qv + (i - 32) : p;
+  p = (i >= 67 && i < 96) ? pa + (i - 67) : p;
+  return p;
+}
+__device__ __forceinline__ float obs_value(float raw, float qw, float qx, float qy, float qz, int i) {
+  if (i >= 6 && i < 9) {
     const float r = (i == 6)   ? 2.f * __builtin_fmaf(-qw, qy, qx * qz)
                     : (i == 7) ? 2.f * __builtin_fmaf(qw, qx, qy * qz)
                                : __builtin_fmaf(-2.f, __builtin_fmaf(qy, qy, qx * qx), 1.f);
     return -r;
   }
-  if (i < 38) return ld(qp + 7 + (i - 9));
-  if (i < 67) return ld(qv + 6 + (i - 38));
-  if (i < 96) return ld(pa + i - 67);
-  return i == 96 ? 0.8f : 0.f;
+  if (i >= 96) return i == 96 ? 0.8f : 0.f;
+  return raw;
 }
 
 constexpr int kTileLd = kTileMaxHidden + 4;   // LDS row pitch of the hidden activations (floats)
-constexpr int kTileLds = kTileW * kTileLd + kTileMaxHidden;   // LDS floats of one tile's policy
+constexpr int kTileLds = kTileW * kTileLd + 2 * kTileMaxHidden;   // LDS floats of one tile's policy
 
 // Policy of control step t (t == H: the bootstrap value only) for the tile's worlds w_j, given by
 // the caller (valid: w_j < N). State is read with `ld` (from the L2: other waves of the launch
 // wrote it). hid: LDS scratch of kTileLds floats: the hidden activations (kTileW x kTileLd,
-// world-major; the log-prob terms reuse them), then the second layer's bias.
+// world-major; the log-prob terms reuse them), then the two layers' biases.
 template <class LoadT>
 __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos, const float* qvel, const float* pact,
                                             const unsigned* rngc, unsigned long long seed, int N, int t, int w,
@@ -128,61 +139,80 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
   const float* qp = qpos + (long)wc * kNQ;
   const float* qv = qvel + (long)wc * kNV;
   const float* pa = pact + (long)wc * kAct;
-  const float qw = ld(qp + 3), qx = ld(qp + 4), qy = ld(qp + 5), qz = ld(qp + 6);
 
   // ---- observation (raw to O, reference: src/g1_env.cu:69-81) and frozen normalisation
-  // (:298-302): lane (j, g) forms features 4 s + g of its world, the first layer's B operands
+  // (:298-302): lane (j, g) forms features 4 s + g of its world, the first layer's B operands.
+  // Every state value is loaded first (one load per feature, all in flight together), then the
+  // normalisation constants.
+  const float qw = ld(qp + 3), qx = ld(qp + 4), qy = ld(qp + 5), qz = ld(qp + 6);
+  float raw[kObsLoads];
+#pragma unroll
+  for (int s = 0; s < kObsLoads; ++s) raw[s] = ld(obs_src(qp, qv, pa, 4 * s + g));
+  const float4* NC = reinterpret_cast<const float4*>(a.Wt + T.nrm_off + kObsSteps * g);
+  float4 nmean[kObsSteps / 4], ndiv[kObsSteps / 4], nrcp[kObsSteps / 4];
+#pragma unroll
+  for (int q = 0; q < kObsSteps / 4; ++q) {
+    nmean[q] = NC[q];
+    ndiv[q] = NC[q + kObsSteps];
+    nrcp[q] = NC[q + 2 * kObsSteps];
+  }
   float x[kObsSteps];
 #pragma unroll
   for (int s = 0; s < kObsSteps; ++s) {
     const int k = 4 * s + g;
     float z = 0.f;
-    if (k < kObs) {
-      const float o = obs_of(ld, qp, qv, pa, qw, qx, qy, qz, k);
+    if (s < kObsLoads) {
+      const float o = obs_value(raw[s], qw, qx, qy, qz, k);
       if (valid && t < a.H) a.O[((long)t * N + w) * kObs + k] = o;
-      const float dv = sqrtf(a.var[k] + 1e-8f);
-      z = div_rn(o - a.mean[k], dv, rcp_rn(dv));
+      const float m = (&nmean[s >> 2].x)[s & 3], d = (&ndiv[s >> 2].x)[s & 3], y = (&nrcp[s >> 2].x)[s & 3];
+      z = div_rn(o - m, d, y);
       if (z < -10.f) z = -10.f; else if (z > 10.f) z = 10.f;
     }
     x[s] = z;
   }
 
   // ---- layer 0, one 16-row output tile at a time: rows 16 T + 4 g + v of world j go to
-  // hid[j][16 T + 4 g + v] (the order in which the next layer's k-steps read them). The weights and
-  // bias of tile T + 1 are loaded while tile T's MFMAs run (two register sets, used alternately).
+  // hid[j][16 T + 4 g + v] (the order in which the next layer's k-steps read them). The weights of
+  // tile T + 2 are loaded while tile T's MFMAs run (three register sets in turn); both layers'
+  // biases are read from LDS.
   const float4* W0 = reinterpret_cast<const float4*>(a.Wt + T.woff[0]) + lane;
-  const float* B0 = a.Wt + T.boff[0] + 4 * g;
   float* hrow = hid + j * kTileLd + 4 * g;
-  float* hb = hid + kTileW * kTileLd;
+  float* hb0 = hid + kTileW * kTileLd;
+  float* hb1 = hb0 + kTileMaxHidden;
   {
-    // the second layer's bias to LDS (read there once per output tile)
-    const int nb = 16 * T.nT[1];
-    if (4 * lane < nb) *reinterpret_cast<float4*>(hb + 4 * lane) = *reinterpret_cast<const float4*>(a.Wt + T.boff[1] + 4 * lane);
+    const int n0 = 16 * T.nT[0], n1 = 16 * T.nT[1];
+    if (4 * lane < n0) *reinterpret_cast<float4*>(hb0 + 4 * lane) = *reinterpret_cast<const float4*>(a.Wt + T.boff[0] + 4 * lane);
+    if (4 * lane < n1) *reinterpret_cast<float4*>(hb1 + 4 * lane) = *reinterpret_cast<const float4*>(a.Wt + T.boff[1] + 4 * lane);
   }
   const int nT0 = T.nT[0];
-  // (Every load below is issued on every path, the last tile's reloaded past the end, so that the
-  // number of loads in flight is the same on all paths and the waits count only older loads.)
-  float4 w0[2][kObsSteps / 4], b0[2];
-  // (the preloads are kept in use order: a wait for the first operand then counts the rest as newer)
+  // (Every load below is issued on every path, the last tile's reloaded past the end, and the
+  // preloads keep their use order, so that the number of loads in flight is the same on all paths
+  // and a wait counts only older loads.)
+  constexpr int kRing0 = 3;
+  float4 w0[kRing0][kObsSteps / 4];
 #pragma unroll
-  for (int qd = 0; qd < kObsSteps / 4; ++qd) {
-    w0[0][qd] = W0[(long)qd * 64];
-    __builtin_amdgcn_sched_barrier(0);
+  for (int r = 0; r < kRing0 - 1; ++r) {
+    const int on = r < nT0 ? r : nT0 - 1;
+#pragma unroll
+    for (int qd = 0; qd < kObsSteps / 4; ++qd) {
+      w0[r][qd] = W0[((long)on * (kObsSteps / 4) + qd) * 64];
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
-  b0[0] = *reinterpret_cast<const float4*>(B0);
+  __syncthreads();   // the biases are in LDS
 #pragma unroll 1
-  for (int ot0 = 0; ot0 < nT0; ot0 += 2) {
+  for (int ot0 = 0; ot0 < nT0; ot0 += kRing0) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < kRing0; ++r) {
       const int ot = ot0 + r;
       {
-        const int on = ot + 1 < nT0 ? ot + 1 : nT0 - 1;
+        const int on = ot + kRing0 - 1 < nT0 ? ot + kRing0 - 1 : nT0 - 1;
 #pragma unroll
-        for (int qd = 0; qd < kObsSteps / 4; ++qd) w0[r ^ 1][qd] = W0[((long)on * (kObsSteps / 4) + qd) * 64];
-        b0[r ^ 1] = *reinterpret_cast<const float4*>(B0 + 16 * on);
+        for (int qd = 0; qd < kObsSteps / 4; ++qd) w0[(r + kRing0 - 1) % kRing0][qd] = W0[((long)on * (kObsSteps / 4) + qd) * 64];
       }
       if (ot < nT0) {
-        f32x4 acc = {b0[r].x, b0[r].y, b0[r].z, b0[r].w};
+        const float4 bv = *reinterpret_cast<const float4*>(hb0 + 16 * ot + 4 * g);
+        f32x4 acc = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
         for (int qd = 0; qd < kObsSteps / 4; ++qd)
           acc = mfma4(f32x4{w0[r][qd].x, w0[r][qd].y, w0[r][qd].z, w0[r][qd].w}, x + 4 * qd, acc);
@@ -229,20 +259,28 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
   }
   f32x4 acc;
   {
-    const float4 bv = *reinterpret_cast<const float4*>(hb + 4 * g);
+    const float4 bv = *reinterpret_cast<const float4*>(hb1 + 4 * g);
     acc = f32x4{bv.x, bv.y, bv.z, bv.w};
   }
+  // the B operands (hid) of block b are read from LDS during block b - 1
+  float4 hv[2][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hv[0][i] = *reinterpret_cast<const float4*>(hrow + 16 * i);
   int ot = 0, qb = 0;
 #pragma unroll 1
   for (int b0 = 0; b0 < nB; b0 += kRing) {
 #pragma unroll
     for (int r = 0; r < kRing; ++r) {
       const int b = b0 + r;
+      {
+        const int qn = qb + 1 == nQB ? 0 : qb + 1;   // the next block's k-quads within its tile
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hv[(r + 1) & 1][i] = *reinterpret_cast<const float4*>(hrow + 16 * (4 * qn + i));
+      }
       if (b < nB) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float4 hv = *reinterpret_cast<const float4*>(hrow + 16 * (4 * qb + i));
-          const float xb[4] = {hv.x, hv.y, hv.z, hv.w};
+          const float xb[4] = {hv[r & 1][i].x, hv[r & 1][i].y, hv[r & 1][i].z, hv[r & 1][i].w};
           acc = mfma4(f32x4{wr[r][i].x, wr[r][i].y, wr[r][i].z, wr[r][i].w}, xb, acc);
         }
         if (++qb == nQB) {
@@ -255,7 +293,7 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
           qb = 0;
           ++ot;
           if (ot < T.nT[1]) {
-            const float4 bv = *reinterpret_cast<const float4*>(hb + 16 * ot + 4 * g);
+            const float4 bv = *reinterpret_cast<const float4*>(hb1 + 16 * ot + 4 * g);
             acc = f32x4{bv.x, bv.y, bv.z, bv.w};
           }
         }

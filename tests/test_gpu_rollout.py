@@ -175,6 +175,28 @@ def test_rollout_teacher_forced_config4_slice(g1, orc):
     _assert_rows(rows)
 
 
+@pytest.mark.parametrize("hidden,act", [((48, 32), 1), ((80, 144), 0)])
+def test_rollout_teacher_forced_one_launch_shapes(g1, orc, hidden, act):
+    """The one-launch rollout's policy tile on two-layer shapes other than 256-256: a first layer
+    that is not a whole number of 4-quad blocks (48, 80: the k dimension padded with zero weights),
+    second layers of 2 and 9 output tiles (fewer tiles than ring slots, and a block count that is not
+    a multiple of the ring), ELU and tanh. N=512, 4 control steps against the oracle."""
+    import configs
+    N, H = 512, 4
+    rng = np.random.default_rng(61)
+    qp, qv, pa, steps = configs.reset_states(rng, N)
+    W = configs.policy_init(rng, hidden=hidden)
+    mean = rng.normal(0, 0.1, 100).astype(np.float32)
+    var = rng.uniform(0.5, 2.0, 100).astype(np.float32)
+    with g1.Env(N, substeps=10, pgs_iters=8, seed=1) as env:
+        env.set_policy(hidden, act)
+        assert env.policy_params() == W.size
+        assert env.set_fused(True)          # the shape runs in the one-launch form
+        env.set_state(qp, qv, pa, steps)
+        rows = _teacher_forced_run(g1, orc, env, N, H, W, mean, var, hidden, act, seed=62)
+    _assert_rows(rows)
+
+
 @pytest.mark.parametrize("fences,fused", [(0, True), (1, True), (0, False), (1, False)])
 def test_rollout_matches_oracle_free_run(g1, orc, fences, fused):
     """A short rollout (N=96, H=3) with no teacher forcing: every output equals the oracle's own
