@@ -368,8 +368,9 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
     const int jw = threadIdx.x & 15;
     const int w = tile_world(qq, u, jw, kQueues);
     const bool valid = (jw >> 1) < np && w < a.N;
-    policy_tile(ra.po, a.qp, a.qv, a.pa, a.rng, a.seed, a.N, t, w, valid, scratch_lds,
-                [](const auto* ptr) { return ld_l2(ptr); });
+    const auto ld = [](const auto* ptr) { return ld_l2(ptr); };
+    if (ra.po.tl.act == 0) policy_tile<0>(ra.po, a.qp, a.qv, a.pa, a.rng, a.seed, a.N, t, w, valid, scratch_lds, ld);
+    else policy_tile<1>(ra.po, a.qp, a.qv, a.pa, a.rng, a.seed, a.N, t, w, valid, scratch_lds, ld);
     release_flag(ra.tflags + qq + kQueues * u, ra.tbase + (unsigned)t + 1u, a.xlocal);
   };
 
@@ -384,11 +385,12 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
       set_queue(qc);
       continue;
     }
+    // the policy this wave runs after its item, if any (one call site: one copy of its code)
+    int pol_u = -1, pol_np = 0, pol_t = 0;
     if (it < ntq) {
-      const int u = (int)it;
-      policy(qc, u, (int)min((unsigned)kTilePairs, nq - kTilePairs * it), 0);
-      continue;
-    }
+      pol_u = (int)it;
+      pol_np = (int)min((unsigned)kTilePairs, nq - kTilePairs * it);
+    } else {
     const unsigned r = it - ntq;
     const int jj = (int)(r / nq), m = (int)(r - (unsigned)jj * nq);
     const int t = jj / nch, c = jj - t * nch;
@@ -417,9 +419,11 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
         if (threadIdx.x == 0)
           __hip_atomic_store(ra.tcount + qc + kQueues * u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (!a.xlocal) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        policy(qc, u, np, t + 1);
+        pol_u = u; pol_np = np; pol_t = t + 1;
       }
     }
+    }
+    if (pol_u >= 0) policy(qc, pol_u, pol_np, pol_t);
   }
   if (a.ncon_hist && l < 9 && hcnt) atomicAdd(&a.ncon_hist[l], (unsigned long long)hcnt);
 }
@@ -1017,8 +1021,7 @@ static void poll_queue_error(EnvState* E) {
 // The one-launch rollout covers policies of two hidden layers of at most 256 units each (multiples of
 // 16); other shapes take the split form (policy and physics launches per control step).
 static bool fused_shape(const PolicyShape& sh) {
-  return sh.nl == 2 && sh.hid[0] % 16 == 0 && sh.hid[1] % 16 == 0 && sh.hid[0] <= kTileMaxHidden &&
-         sh.hid[1] <= kTileMaxHidden;
+  return sh.nl == 2 && sh.hid[0] <= kTileMaxHidden && sh.hid[1] <= kTileMaxHidden;
 }
 
 static int tiles_per_queue(int N) {
@@ -1032,7 +1035,7 @@ static int tiles_per_queue(int N) {
 static void rollout_fused(EnvState* E, int H, const float* W, const float* mean, const float* var, float* O, float* A,
                           float* LP, float* V, float* R, float* D, float* Vlast, const float* act_noise,
                           const float* reset_noise, float* wp, long wp_cap) {
-  const TileLayout tl = tile_layout(E->shape.hid[0], E->shape.hid[1], E->shape.act);
+  const TileLayout tl = tile_layout(E->shape.act);
   float* Wt = wp;
   if (!Wt) {
     if (tl.total > E->Wt_cap) {

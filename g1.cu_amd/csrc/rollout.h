@@ -38,8 +38,7 @@ constexpr int kHeadT = 2;                      // head rows: mu 0..28, value 29,
 // and RN(1 / d) (features past 100: 0, 1, 1), so that lane group g reads its own as float4s.
 struct TileLayout {
   int nT[3];        // output tiles of layer 0, layer 1, head
-  int nQ[3];        // k-step quads of layer 0, layer 1 (input width / 16 rounded up to a multiple
-                    // of 4; the padding holds zero weights), head (input width / 16)
+  int nQ[3];        // k-step quads of layer 0, layer 1, head
   long woff[3], boff[3];
   long ls_off;
   long nrm_off;
@@ -47,10 +46,12 @@ struct TileLayout {
   int act;          // 0 tanh, 1 ELU
 };
 
-__host__ __device__ inline TileLayout tile_layout(int h0, int h1, int act) {
+// Every layer is laid out at the widest shape (256-256): rows past a layer's width and k-steps past
+// its input width hold zeros.
+__host__ __device__ inline TileLayout tile_layout(int act) {
   TileLayout t{};
-  t.nT[0] = h0 / 16; t.nT[1] = h1 / 16; t.nT[2] = kHeadT;
-  t.nQ[0] = kObsSteps / 4; t.nQ[1] = 4 * ((h0 + 63) / 64); t.nQ[2] = h1 / 16;
+  t.nT[0] = kTileMaxT; t.nT[1] = kTileMaxT; t.nT[2] = kHeadT;
+  t.nQ[0] = kObsSteps / 4; t.nQ[1] = kTileMaxT; t.nQ[2] = kTileMaxT;
   long off = 0;
   for (int L = 0; L < 3; ++L) {
     t.woff[L] = off;
@@ -93,6 +94,30 @@ __device__ __forceinline__ f32x4 mfma4(f32x4 w, const float* x, f32x4 acc) {
   return acc;
 }
 
+// Hidden-layer activations of the tile MLP, branch-free so that they issue between the MFMAs of
+// the next output tile. tanh: below |x| = 1/8 the odd series to x^7 (truncation < 2e-10), above it
+// 1 - 2 / (e^{2|x|} + 1) with the hardware exp2 (absolute error ~1e-7, no cancellation); the sign
+// restored. ELU: x for x > 0, else e^x - 1, below |x| = 1/8 by the series to x^5 (truncation
+// < 6e-9). The first layer's K sums over 256 such values, so the outputs stay far inside the policy
+// outputs' 1e-5 bound. ACT: 0 tanh, 1 ELU.
+template <int ACT>
+__device__ __forceinline__ float act_tile(float x) {
+  const float a = __builtin_fabsf(x);
+  if (ACT == 0) {
+    const float a2 = a * a;
+    const float ser = __builtin_fmaf(a * a2, __builtin_fmaf(a2, __builtin_fmaf(a2, -17.f / 315.f, 2.f / 15.f), -1.f / 3.f), a);
+    const float e = __builtin_amdgcn_exp2f(a * 2.8853900817779268f);   // e^{2a}
+    const float big = 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
+    const float r = a < 0.125f ? ser : big;
+    return __builtin_copysignf(r, x);
+  } else {
+    const float ser = x * __builtin_fmaf(x, __builtin_fmaf(x, __builtin_fmaf(x, __builtin_fmaf(x, 1.f / 120.f, 1.f / 24.f), 1.f / 6.f), 0.5f), 1.f);
+    const float em1 = __builtin_amdgcn_exp2f(x * 1.4426950408889634f) - 1.f;
+    const float neg = a < 0.125f ? ser : em1;
+    return x > 0.f ? x : neg;
+  }
+}
+
 constexpr int kObsLoads = 25;   // k-steps of the first layer that read a state value (4 s + g < 100)
 
 // Observation feature i (reference: src/g1_env.cu:69-81): base angular and linear velocity (qvel
@@ -118,14 +143,13 @@ __device__ __forceinline__ float obs_value(float raw, float qw, float qx, float 
   return raw;
 }
 
-constexpr int kTileLd = kTileMaxHidden + 4;   // LDS row pitch of the hidden activations (floats)
-constexpr int kTileLds = kTileW * kTileLd + 2 * kTileMaxHidden;   // LDS floats of one tile's policy
+constexpr int kTileLds = kTileW * 32 + 2 * kTileMaxHidden;   // LDS floats of one tile's policy
 
 // Policy of control step t (t == H: the bootstrap value only) for the tile's worlds w_j, given by
 // the caller (valid: w_j < N). State is read with `ld` (from the L2: other waves of the launch
-// wrote it). hid: LDS scratch of kTileLds floats: the hidden activations (kTileW x kTileLd,
-// world-major; the log-prob terms reuse them), then the two layers' biases.
-template <class LoadT>
+// wrote it). hid: LDS scratch of kTileLds floats: the log-prob terms (kTileW x 32), then the two
+// layers' biases.
+template <int ACT, class LoadT>
 __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos, const float* qvel, const float* pact,
                                             const unsigned* rngc, unsigned long long seed, int N, int t, int w,
                                             bool valid, float* hid, LoadT ld) {
@@ -171,144 +195,91 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
     x[s] = z;
   }
 
-  // ---- layer 0, one 16-row output tile at a time: rows 16 T + 4 g + v of world j go to
-  // hid[j][16 T + 4 g + v] (the order in which the next layer's k-steps read them). The weights of
-  // tile T + 2 are loaded while tile T's MFMAs run (three register sets in turn); both layers'
-  // biases are read from LDS.
-  const float4* W0 = reinterpret_cast<const float4*>(a.Wt + T.woff[0]) + lane;
-  float* hrow = hid + j * kTileLd + 4 * g;
-  float* hb0 = hid + kTileW * kTileLd;
+  // ---- the MLP, on the fixed 256-256 shape (narrower layers are padded with zero weights and
+  // biases, whose rows give act(0) = 0 and add exact zeros downstream). Layer 0 runs in 16 output
+  // tiles, fully unrolled: tile T's activations (rows 16 T + 4 g + v of world j in lane (j, g),
+  // register v) are the second layer's B operands of k-quad T as they stand, so the hidden
+  // activations never leave the registers. Weights stream from the L2 through register slots ahead
+  // of their MFMAs, every load on every path (waits then count only older loads); the biases are
+  // read from LDS.
+  float* hb0 = hid + kTileW * 32;
   float* hb1 = hb0 + kTileMaxHidden;
-  {
-    const int n0 = 16 * T.nT[0], n1 = 16 * T.nT[1];
-    if (4 * lane < n0) *reinterpret_cast<float4*>(hb0 + 4 * lane) = *reinterpret_cast<const float4*>(a.Wt + T.boff[0] + 4 * lane);
-    if (4 * lane < n1) *reinterpret_cast<float4*>(hb1 + 4 * lane) = *reinterpret_cast<const float4*>(a.Wt + T.boff[1] + 4 * lane);
-  }
-  const int nT0 = T.nT[0];
-  // (Every load below is issued on every path, the last tile's reloaded past the end, and the
-  // preloads keep their use order, so that the number of loads in flight is the same on all paths
-  // and a wait counts only older loads.)
-  constexpr int kRing0 = 3;
-  float4 w0[kRing0][kObsSteps / 4];
+  *reinterpret_cast<float4*>(hb0 + 4 * lane) = *reinterpret_cast<const float4*>(a.Wt + T.boff[0] + 4 * lane);
+  *reinterpret_cast<float4*>(hb1 + 4 * lane) = *reinterpret_cast<const float4*>(a.Wt + T.boff[1] + 4 * lane);
+  constexpr int kQ0 = kObsSteps / 4;            // k-quads per output tile of layer 0
+  constexpr int kQ0All = kTileMaxT * kQ0;        // layer 0's k-quads in storage order
+  constexpr int kRing0 = 8, kAhead0 = kQ0;       // quad slots; a quad is loaded one tile ahead
+  const float4* W0 = reinterpret_cast<const float4*>(a.Wt + T.woff[0]);
+  float4 w0[kRing0];
 #pragma unroll
-  for (int r = 0; r < kRing0 - 1; ++r) {
-    const int on = r < nT0 ? r : nT0 - 1;
-#pragma unroll
-    for (int qd = 0; qd < kObsSteps / 4; ++qd) {
-      w0[r][qd] = W0[((long)on * (kObsSteps / 4) + qd) * 64];
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  for (int gq = 0; gq < kAhead0; ++gq) {
+    w0[gq % kRing0] = W0[gq * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
   }
   __syncthreads();   // the biases are in LDS
-#pragma unroll 1
-  for (int ot0 = 0; ot0 < nT0; ot0 += kRing0) {
+  f32x4 h[kTileMaxT];
 #pragma unroll
-    for (int r = 0; r < kRing0; ++r) {
-      const int ot = ot0 + r;
-      {
-        const int on = ot + kRing0 - 1 < nT0 ? ot + kRing0 - 1 : nT0 - 1;
+  for (int ot = 0; ot < kTileMaxT; ++ot) {
+    const float4 bv = *reinterpret_cast<const float4*>(hb0 + 16 * ot + 4 * g);
+    f32x4 acc = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-        for (int qd = 0; qd < kObsSteps / 4; ++qd) w0[(r + kRing0 - 1) % kRing0][qd] = W0[((long)on * (kObsSteps / 4) + qd) * 64];
-      }
-      if (ot < nT0) {
-        const float4 bv = *reinterpret_cast<const float4*>(hb0 + 16 * ot + 4 * g);
-        f32x4 acc = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-        for (int qd = 0; qd < kObsSteps / 4; ++qd)
-          acc = mfma4(f32x4{w0[r][qd].x, w0[r][qd].y, w0[r][qd].z, w0[r][qd].w}, x + 4 * qd, acc);
-        *reinterpret_cast<float4*>(hrow + 16 * ot) =
-            float4{act_fn(acc[0], T.act), act_fn(acc[1], T.act), act_fn(acc[2], T.act), act_fn(acc[3], T.act)};
-      }
+    for (int qd = 0; qd < kQ0; ++qd) {
+      const int gq = ot * kQ0 + qd;
+      if (gq + kAhead0 < kQ0All) w0[(gq + kAhead0) % kRing0] = W0[(gq + kAhead0) * 64 + lane];
+      const float4 wq = w0[gq % kRing0];
+      acc = mfma4(f32x4{wq.x, wq.y, wq.z, wq.w}, x + 4 * qd, acc);
+      __builtin_amdgcn_sched_barrier(0);   // each refill issued ahead of its quad's MFMAs, as written
     }
+    h[ot] = f32x4{act_tile<ACT>(acc[0]), act_tile<ACT>(acc[1]), act_tile<ACT>(acc[2]), act_tile<ACT>(acc[3])};
+    __builtin_amdgcn_sched_barrier(0);   // keep each tile's loads and MFMAs within the tile
   }
-  // layer 1's k dimension is padded to whole 4-quad blocks: zero activations there (zero weights)
-#pragma unroll 1
-  for (int ot = nT0; ot < T.nQ[1]; ++ot) *reinterpret_cast<float4*>(hrow + 16 * ot) = float4{0.f, 0.f, 0.f, 0.f};
-  __syncthreads();
 
-  // ---- layer 1 tile by tile (B operands from hid), each tile's activations fed into the head.
-  // Its weights are read in storage order (tile ot, k-quad qd) as blocks of 4 k-quads, kRing
-  // blocks ahead of the MFMAs that use them; each block's slot also carries the head weights of the
-  // block's tile (the same lines again for the tile's other blocks), so that every load is issued on
-  // every path.
-  constexpr int kRing = 4;
-  const int nQB = T.nQ[1] >> 2;            // 4-quad blocks per tile
-  const int nB = T.nT[1] * nQB;            // blocks of the layer
-  const float4* W1 = reinterpret_cast<const float4*>(a.Wt + T.woff[1]) + lane;
-  const float4* Wh = reinterpret_cast<const float4*>(a.Wt + T.woff[2]) + lane;
+  // ---- layer 1 tile by tile, each tile's activations fed into the head as its k-quad; the weights
+  // in 4-quad blocks through two slots, each refilled with the block after next as soon as its
+  // block's MFMAs are issued
+  const float4* W1 = reinterpret_cast<const float4*>(a.Wt + T.woff[1]);
+  const float4* Wh = reinterpret_cast<const float4*>(a.Wt + T.woff[2]);
   f32x4 hd[kHeadT];
 #pragma unroll
   for (int ht = 0; ht < kHeadT; ++ht) {
     const float4 bv = *reinterpret_cast<const float4*>(a.Wt + T.boff[2] + 16 * ht + 4 * g);
     hd[ht] = f32x4{bv.x, bv.y, bv.z, bv.w};
   }
-  float4 wr[kRing][4], whr[kRing][kHeadT];
-  int lt = 0, lq = 0;                      // tile and block within the tile of the next block loaded
+  float4 wr[2][4];
 #pragma unroll
-  for (int r = 0; r < kRing; ++r) {
-    const int bl = lt * nQB + lq;
+  for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      wr[r][i] = W1[(long)(4 * bl + i) * 64];
+      wr[qb][i] = W1[(4 * qb + i) * 64 + lane];
       __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int ht = 0; ht < kHeadT; ++ht) whr[r][ht] = Wh[((long)ht * T.nQ[2] + lt) * 64];
-    __builtin_amdgcn_sched_barrier(0);
-    if (bl + 1 < nB && ++lq == nQB) { lq = 0; ++lt; }
-  }
-  f32x4 acc;
-  {
-    const float4 bv = *reinterpret_cast<const float4*>(hb1 + 4 * g);
-    acc = f32x4{bv.x, bv.y, bv.z, bv.w};
-  }
-  // the B operands (hid) of block b are read from LDS during block b - 1
-  float4 hv[2][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) hv[0][i] = *reinterpret_cast<const float4*>(hrow + 16 * i);
-  int ot = 0, qb = 0;
 #pragma unroll 1
-  for (int b0 = 0; b0 < nB; b0 += kRing) {
+  for (int ot = 0; ot < kTileMaxT; ++ot) {
+    const int on = ot + 1 < kTileMaxT ? ot + 1 : ot;   // the last tile reloads itself
+    float4 wh[kHeadT];
 #pragma unroll
-    for (int r = 0; r < kRing; ++r) {
-      const int b = b0 + r;
-      {
-        const int qn = qb + 1 == nQB ? 0 : qb + 1;   // the next block's k-quads within its tile
+    for (int ht = 0; ht < kHeadT; ++ht) wh[ht] = Wh[(ht * kTileMaxT + ot) * 64 + lane];
+    const float4 bv = *reinterpret_cast<const float4*>(hb1 + 16 * ot + 4 * g);
+    f32x4 acc = {bv.x, bv.y, bv.z, bv.w};
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) hv[(r + 1) & 1][i] = *reinterpret_cast<const float4*>(hrow + 16 * (4 * qn + i));
+    for (int qb = 0; qb < 4; ++qb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 hq = h[4 * qb + i];
+        const float xb[4] = {hq[0], hq[1], hq[2], hq[3]};
+        acc = mfma4(f32x4{wr[qb & 1][i].x, wr[qb & 1][i].y, wr[qb & 1][i].z, wr[qb & 1][i].w}, xb, acc);
       }
-      if (b < nB) {
+      // block qb + 2 of this tile, or block qb - 2 of the next
+      const int nb = qb < 2 ? 4 * ot + qb + 2 : 4 * on + qb - 2;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float xb[4] = {hv[r & 1][i].x, hv[r & 1][i].y, hv[r & 1][i].z, hv[r & 1][i].w};
-          acc = mfma4(f32x4{wr[r][i].x, wr[r][i].y, wr[r][i].z, wr[r][i].w}, xb, acc);
-        }
-        if (++qb == nQB) {
-          // tile ot done: its activations are the head's k-quad ot
-          const float h2[4] = {act_fn(acc[0], T.act), act_fn(acc[1], T.act), act_fn(acc[2], T.act),
-                               act_fn(acc[3], T.act)};
-#pragma unroll
-          for (int ht = 0; ht < kHeadT; ++ht)
-            hd[ht] = mfma4(f32x4{whr[r][ht].x, whr[r][ht].y, whr[r][ht].z, whr[r][ht].w}, h2, hd[ht]);
-          qb = 0;
-          ++ot;
-          if (ot < T.nT[1]) {
-            const float4 bv = *reinterpret_cast<const float4*>(hb1 + 16 * ot + 4 * g);
-            acc = f32x4{bv.x, bv.y, bv.z, bv.w};
-          }
-        }
-      }
-      // refill the slot in place (no register copy of a value still in flight), on every path; past
-      // the last block the last block is loaded again
-      const int bl = lt * nQB + lq;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wr[r][i] = W1[(long)(4 * bl + i) * 64];
-#pragma unroll
-      for (int ht = 0; ht < kHeadT; ++ht) whr[r][ht] = Wh[((long)ht * T.nQ[2] + lt) * 64];
-      if (bl + 1 < nB && ++lq == nQB) { lq = 0; ++lt; }
+      for (int i = 0; i < 4; ++i) wr[qb & 1][i] = W1[(4 * nb + i) * 64 + lane];
+      __builtin_amdgcn_sched_barrier(0);   // the refill issued here, a block ahead of its use
     }
+    const float h2[4] = {act_tile<ACT>(acc[0]), act_tile<ACT>(acc[1]), act_tile<ACT>(acc[2]), act_tile<ACT>(acc[3])};
+#pragma unroll
+    for (int ht = 0; ht < kHeadT; ++ht) hd[ht] = mfma4(f32x4{wh[ht].x, wh[ht].y, wh[ht].z, wh[ht].w}, h2, hd[ht]);
   }
-  __syncthreads();   // hid is free again (the log-prob terms below reuse it)
   float* lds = hid;
 
   // ---- value (head row 29: tile 1, rows 4 g + v with g = 3, v = 1)

@@ -116,7 +116,8 @@ int g1_env_set_handover(void* h, int fences);
 /* Rollout form: on = 1 (the default) runs g1_rollout as one persistent launch that interleaves the
  * policy of 16-world tiles with the physics work items; on = 0 launches the policy and the physics
  * once per control step. The one-launch form covers policies of two hidden layers of at most 256
- * units (multiples of 16); other shapes always take the per-step form. Returns 0, 1 when on = 1 but
+ * units each (run at 256-256 with zero padding); other shapes always take the per-step form.
+ * Returns 0, 1 when on = 1 but
  * the current policy shape takes the per-step form, or -1 for an invalid argument. */
 int g1_env_set_fused(void* h, int on);
 

@@ -175,12 +175,11 @@ def test_rollout_teacher_forced_config4_slice(g1, orc):
     _assert_rows(rows)
 
 
-@pytest.mark.parametrize("hidden,act", [((48, 32), 1), ((80, 144), 0)])
+@pytest.mark.parametrize("hidden,act", [((48, 32), 1), ((80, 144), 0), ((100, 60), 0), ((256, 17), 1)])
 def test_rollout_teacher_forced_one_launch_shapes(g1, orc, hidden, act):
-    """The one-launch rollout's policy tile on two-layer shapes other than 256-256: a first layer
-    that is not a whole number of 4-quad blocks (48, 80: the k dimension padded with zero weights),
-    second layers of 2 and 9 output tiles (fewer tiles than ring slots, and a block count that is not
-    a multiple of the ring), ELU and tanh. N=512, 4 control steps against the oracle."""
+    """The one-launch rollout's policy tile on two-layer shapes other than 256-256, which it runs at
+    256-256 with zero padding: widths that are and are not multiples of 16, ELU and tanh. N=512,
+    4 control steps against the oracle."""
     import configs
     N, H = 512, 4
     rng = np.random.default_rng(61)
