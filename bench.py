@@ -1,5 +1,5 @@
 """Benchmark of the fused rollout on one MI355X: the BASELINE metric (physics substeps/s and ms per
-fused rollout, N=8192, H=32, S=10, pgs=8, MLP 100-256-256 tanh), with the physics kernel's
+fused rollout, N=8192, H=32, S=10, pgs=8, MLP 100-256-256 tanh), with the dominant kernel's
 roofline and the CPU oracle timed on this host beside it.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3|4] [--no-cpu] [--no-counters]
@@ -7,11 +7,14 @@ roofline and the CPU oracle timed on this host beside it.
 A "step" is one fused rollout (one g1_rollout call: H control steps x S substeps for all N worlds)
 with the policy weights and frozen statistics already resident in HBM. Prints ONE JSON line.
 
-Roofline of k_physics (the dominant kernel): the physics runs out of registers and LDS and is
-bound by VALU issue, so `achieved` is its algorithmic FLOP rate: the reference algorithm's
-floating-point operations per world-substep by contact count (g1.cu_amd/roofline.py, counted by an
-instrumented oracle) summed over the launch's measured contact histogram, divided by the average
-launch time from HIP events on the kernel's stream; `peak` is the MI355X fp32 figure. Hardware
+The dominant kernel is k_rollout (the whole rollout in one launch: physics work items and the
+policy of 16-world tiles) when the policy shape runs in one launch (two hidden layers of at most
+256, config 3), else k_physics (config 4's three-layer policy takes per-step launches). The physics
+runs out of registers and LDS and is bound by VALU issue, so `achieved` is the launch's algorithmic
+FLOP rate: the reference algorithm's floating-point operations per world-substep by contact count
+(g1.cu_amd/roofline.py, counted by an instrumented oracle) summed over the launch's measured contact
+histogram, plus (k_rollout) the policy MLP's multiply-adds, divided by the average launch time from
+HIP events on the kernel's stream; `peak` is the MI355X fp32 figure. Hardware
 counters come from rocprofv3 passes over a one-rollout run of this script, started as child
 processes before this process touches the GPU: HBM traffic per dispatch (FETCH_SIZE and
 WRITE_SIZE, each scaled by what the counter reads for a copy of known size in the same run),
@@ -74,7 +77,7 @@ def cpu_baseline(cfg, threads, seed=0):
 # ---------------------------------------------------------------- hardware counters (rocprofv3)
 def counter_child(config):
     """The profiled program: one copy of COPY_MIB MiB (the calibration dispatch), then one warm-up
-    and one timed rollout of the configuration."""
+    and one timed rollout of the configuration (in the library's default rollout form)."""
     import torch
     import configs
     import g1env
@@ -106,8 +109,8 @@ def _read_counters(outdir):
     return rows
 
 
-def measure_counters(config, timeout_s=150):
-    """Runs the counter passes on child processes; returns per-dispatch averages for k_physics and
+def measure_counters(config, kernel, timeout_s=150):
+    """Runs the counter passes on child processes; returns per-dispatch averages for `kernel` and
     the calibration copy, or None with the reason."""
     exe = shutil.which("rocprofv3")
     if exe is None:
@@ -128,7 +131,7 @@ def measure_counters(config, timeout_s=150):
             return None, f"counter pass {name}: no output (exit {p.returncode}): {p.stderr[-300:]}"
         for r in rows:
             kname, cname, val = r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"])
-            key = "physics" if "k_physics" in kname else ("copy" if "copyBuffer" in kname else None)
+            key = "physics" if kernel in kname else ("copy" if "copyBuffer" in kname else None)
             if key is None:
                 continue
             res[key].setdefault(cname, []).append(val)
@@ -166,17 +169,23 @@ def main():
               "and this build runs on single-GPU boxes only (--gpus 1).", file=sys.stderr)
         sys.exit(2)
 
+    import configs
+    cfg = configs.ROLLOUT_CONFIGS[args.config]
+    # the library runs a two-hidden-layer policy of at most 256 units as one launch (k_rollout)
+    one_launch = len(cfg["hidden"]) == 2 and max(cfg["hidden"]) <= 256
+    kernel = "k_rollout" if one_launch else "k_physics"
     # counter passes first, while this process has not touched the GPU
-    counters, counter_note = (None, "skipped (--no-counters)") if args.no_counters else measure_counters(args.config)
+    counters, counter_note = ((None, "skipped (--no-counters)") if args.no_counters
+                              else measure_counters(args.config, kernel))
 
     import torch
-    import configs
     import g1env
-    cfg = configs.ROLLOUT_CONFIGS[args.config]
     N, H, S, pgs = cfg["N"], cfg["H"], cfg["S"], cfg["pgs"]
     rng = np.random.default_rng(1234)
     env = g1env.Env(N, substeps=S, pgs_iters=pgs, seed=1)
     env.set_policy(cfg["hidden"], cfg["act"])
+    if env.set_fused(True) != one_launch:
+        sys.exit("rollout form differs from the one this script expects")
     env.reset()
     if args.policy == "trained":
         if args.config != 3:
@@ -214,17 +223,21 @@ def main():
     launches = max(pr["physics_launches"], 1)
     avg_launch_s = pr["physics_ms"] / launches * 1e-3
     bytes_total, flops_total = rf.physics_work(hist, pgs, control_steps_worlds=N * H * args.steps)
-    flops_launch, bytes_launch = flops_total / launches, bytes_total / launches
-    achieved_tf = flops_launch / avg_launch_s / 1e12
+    phys_flops_launch, bytes_launch = flops_total / launches, bytes_total / launches
     cbar = float((hist * np.arange(9)).sum() / max(hist.sum(), 1))
+    # policy MLP multiply-adds per rollout: H steps plus the bootstrap value (fp32, MFMA)
     pol_flops = 2 * N * (H + 1) * sum(a * b for a, b in zip((100,) + tuple(cfg["hidden"]), tuple(cfg["hidden"]) + (30,)))
+    mlp_flops_launch = pol_flops * args.steps / launches if one_launch else 0.0
+    flops_launch = phys_flops_launch + mlp_flops_launch
+    achieved_tf = flops_launch / avg_launch_s / 1e12
     pol_ms = pr["policy_ms"] / args.steps
     pol_tf = pol_flops / (pol_ms * 1e-3) / 1e12 if pol_ms > 0 else None
 
     roof = {"bound": "valu", "achieved": achieved_tf, "peak": rf.FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": achieved_tf / rf.FP32_PEAK_TFLOPS,
             "traffic": counters["traffic_bytes"] if counters else None,
-            "kernel": "k_physics", "avg_launch_ms": avg_launch_s * 1e3, "algorithmic_flops_per_launch": flops_launch,
+            "kernel": kernel, "avg_launch_ms": avg_launch_s * 1e3, "algorithmic_flops_per_launch": flops_launch,
+            "physics_flops_per_launch": phys_flops_launch, "mlp_flops_per_launch": mlp_flops_launch,
             "mean_ncon": cbar, "frac_of_unpacked_fp32": achieved_tf / rf.FP32_UNPACKED_TFLOPS,
             "hbm_proxy": {"unit": "GB/s", "achieved": bytes_launch / avg_launch_s / 1e9, "peak": rf.HBM_PEAK_GBS,
                           "frac": bytes_launch / avg_launch_s / 1e9 / rf.HBM_PEAK_GBS,
@@ -234,7 +247,7 @@ def main():
     if counters:
         valu = counters.get("SQ_INSTS_VALU")
         roof["counters"] = {
-            "source": f"rocprofv3 --pmc, one-rollout run of this script ({counters['dispatches']} k_physics dispatches)",
+            "source": f"rocprofv3 --pmc, one-rollout run of this script ({counters['dispatches']} {kernel} dispatches)",
             "hbm_bytes_per_dispatch": counters["traffic_bytes"],
             "hbm_gbs": counters["traffic_bytes"] / avg_launch_s / 1e9,
             "fetch_write_scale": [counters["fetch_scale"], counters["write_scale"]],
@@ -242,7 +255,7 @@ def main():
             "valu_lane_utilization": counters.get("VALUUtilization", float("nan")) / 100.0,
             "valu_insts_per_dispatch": valu,
             "valu_issue_frac": valu / (rf.VALU_ISSUE_PEAK * avg_launch_s) if valu else None,
-            "flops_per_valu_lane_slot": flops_launch / (valu * 64) if valu else None,
+            "physics_flops_per_valu_lane_slot": phys_flops_launch / (valu * 64) if valu else None,
             "lds_util_frac": counters.get("LdsUtil", float("nan")) / 100.0,
             "lds_bank_conflict_frac": counters.get("LDSBankConflict", float("nan")) / 100.0,
             "lds_insts_per_dispatch": counters.get("SQ_INSTS_LDS")}
@@ -270,10 +283,12 @@ def main():
                                f"policy 100-{'-'.join(map(str, cfg['hidden']))} {'tanh' if cfg['act'] == 0 else 'ELU'}",
                    "N": N, "H": H, "substeps": S, "pgs": pgs, "ms_per_rollout": ms_rollout},
         "roofline": roof,
-        "phases": {"physics_ms_per_rollout": pr["physics_ms"] / args.steps, "policy_ms_per_rollout": pol_ms,
-                   "policy_tflops": pol_tf,
-                   "policy_mfma_frac": pol_tf / rf.FP32_PEAK_TFLOPS if pol_tf else None,
-                   "ncon_hist": hist.tolist()},
+        "phases": ({"rollout_launch_ms": pr["physics_ms"] / args.steps,
+                    "note": "physics and policy share one k_rollout launch per rollout"} if one_launch else
+                   {"physics_ms_per_rollout": pr["physics_ms"] / args.steps, "policy_ms_per_rollout": pol_ms,
+                    "policy_tflops": pol_tf,
+                    "policy_mfma_frac": pol_tf / rf.FP32_PEAK_TFLOPS if pol_tf else None}),
+        "ncon_hist": hist.tolist(),
     }
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)

@@ -1,5 +1,5 @@
 """Algorithmic work units of the physics and the MI355X peaks they are priced against, used by
-bench.py and scripts/bench_configs.py.
+bench.py and tests/bench_configs.py.
 
 Two units per world-substep with c foot contacts and p PGS sweeps:
 

@@ -1,7 +1,10 @@
 """Measurements of the benchmark configurations other than the headline rollout, GPU and CPU side by
 side (the headline config-3 rollout is bench.py's; config 4 is `bench.py --config 4`).
 
-    python g1.cu_amd/scripts/bench_configs.py [--cpu-threads T] [--skip-cpu]
+    python tests/bench_configs.py [--cpu-threads T] [--skip-cpu]
+
+A measurement harness beside the test suite (it checks the GPU against the CPU oracle), not part of
+the library.
 
 config 0  qacc of 256 perturbed single-world states (no contact, plain factor): fp64 CPU oracle time
           per state (1 thread) and the GPU's fp32 relerr against it.
@@ -26,9 +29,9 @@ import sys
 import time
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ROOT = os.path.dirname(os.path.dirname(HERE))
-sys.path.insert(0, HERE)
-sys.path.insert(0, os.path.dirname(HERE))
+ROOT = os.path.dirname(HERE)
+sys.path.insert(0, os.path.join(ROOT, "g1.cu_amd", "scripts"))
+sys.path.insert(0, os.path.join(ROOT, "g1.cu_amd"))
 
 import numpy as np  # noqa: E402
 
