@@ -126,6 +126,47 @@ def test_config1_dynamics_teacher_forced_and_drift(g1, orc):
     assert np.isfinite(gq).all() and dq_.max() <= 1e-4
 
 
+@pytest.mark.timeout(600)
+def test_config1_full_workload_teacher_forced(g1, orc):
+    """Config 1 at its full size: N=8192 worlds, 1000 substeps with tau resampled every 10 (100
+    draws), no contact, plain factor, the env's velocity guard, on the GPU's own running state. At
+    10 sampled segments the first substep runs as its own launch over all worlds, and 1024 sampled
+    worlds are compared with the oracle's substep from the same pre-substep state: qacc, qvel and
+    qpos bit for bit. The 1000-substep run stays finite."""
+    import torch
+    import configs
+    N, seg, nseg = 8192, 10, 100
+    rng = np.random.default_rng(17)
+    qp, qv = configs.perturbed_states(N, rng)
+    dq, dv = _dev(qp.astype(np.float32)), _dev(qv.astype(np.float32))
+    qa = torch.zeros(N, 35, device="cuda")
+    nc = torch.zeros(N, dtype=torch.int32, device="cuda")
+    sel = np.sort(rng.choice(N, 1024, replace=False))
+    check = {0, 11, 23, 37, 50, 64, 77, 88, 95, 99}
+
+    def run(dt_, nsub):
+        g1.lib.g1_dynamics_bench(N, g1.dev_ptr(dq), g1.dev_ptr(dv), g1.dev_ptr(dt_), nsub, 0, 0, 1, 8, 0.6,
+                                  g1.dev_ptr(qa), g1.dev_ptr(nc))
+
+    for k in range(nseg):
+        tau = configs.random_torque(N, rng).astype(np.float32)
+        dt_ = _dev(tau)
+        if k in check:
+            torch.cuda.synchronize()
+            q0, v0 = dq.cpu().numpy()[sel], dv.cpu().numpy()[sel]
+            run(dt_, 1)
+            torch.cuda.synchronize()
+            oq, ov, oa, _ = orc.dynamics(q0, v0, tau[sel], nsub=1, guard=True, threads=8)
+            gq, gv, ga = dq.cpu().numpy()[sel], dv.cpu().numpy()[sel], qa.cpu().numpy()[sel]
+            assert np.array_equal(ga, oa) and np.array_equal(gv, ov) and np.array_equal(gq, oq), k
+            run(dt_, seg - 1)
+        else:
+            run(dt_, seg)
+    torch.cuda.synchronize()
+    assert np.isfinite(dq.cpu().numpy()).all() and np.isfinite(dv.cpu().numpy()).all()
+    print(f"config1 N={N}: 1000 substeps; {len(check)} sampled substeps x {sel.size} worlds bit-identical")
+
+
 def test_smooth_qacc_vs_mujoco(g1, ref_traj):
     sel = ref_traj["sel"]
     prev = np.maximum(sel - 1, 0)
