@@ -61,6 +61,8 @@ struct PhysArgs {
   int xlocal;                      // queue q's waves all run on XCD q (checked at env creation)
   int nch;                         // work items (substep chunks) per pair and control step:
   int cst[kMaxChunks + 1];         //   chunk c = substeps [cst[c], cst[c + 1]), cst[nch] = S
+  int nchl;                        // the same for the launch's last control step (k = K - 1)
+  int cstl[kMaxChunks + 1];
 };
 
 constexpr int kPhysThreads = 64;   // one wave64 = two 32-lane world groups
@@ -147,7 +149,9 @@ __device__ __forceinline__ void physics_item(const PhysArgs& a, WorldLds& s, con
     energy = ld_l2(a.acc + (long)wc * kGroup + l);
     vx_sum = ld_l2(a.vxs + wc);
   }
-  const int s0 = a.cst[c], s1 = a.cst[c + 1];
+  const bool lastk = k == a.K - 1;   // the launch's last control step has a chunk table of its own
+  const int nck = lastk ? a.nchl : a.nch;
+  const int s0 = lastk ? a.cstl[c] : a.cst[c], s1 = lastk ? a.cstl[c + 1] : a.cst[c + 1];
 #pragma unroll 1
   for (int sub = s0; sub < s1; ++sub) {
     float jtau = 0.f;
@@ -164,7 +168,7 @@ __device__ __forceinline__ void physics_item(const PhysArgs& a, WorldLds& s, con
     integrate_lane(L, st, bqacc, jqacc, true);
     vx_sum += st.bqd[0];
   }
-  if (c < a.nch - 1) {
+  if (c < nck - 1) {
     if (wvalid) {
       a.acc[(long)w * kGroup + l] = energy;
       if (l == 1) a.vxs[w] = vx_sum;
@@ -317,8 +321,9 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
 // k_rollout runs a whole g1_rollout: the physics items of k_physics for H control steps, and the
 // policy of every control step on 16-world tiles (policy_tile). Tile u of queue q holds the pairs
 // q + 32 (8 u + i), i < 8, so all its work stays on the queue's XCD.
-// Claim order within a queue (nq pairs, ntq tiles, nch substep chunks per control step):
-//   P(0, all tiles), then C(t, c, all pairs) for t < H, c < nch,
+// Claim order within a queue (nq pairs, ntq tiles, nch substep chunks per control step, nchl in
+// the last one):
+//   P(0, all tiles), then C(t, c, all pairs) for t < H, c < (t < H - 1 ? nch : nchl),
 // where P(0, u) is the policy of step 0 on tile u and C(t, c, p) chunk c of pair p's step t. The
 // policy of a later step is not claimed: the wave that completes a tile's last pair of step t (the
 // tile's completion count, raised by every pair's last chunk after its release, reaches the tile's
@@ -335,7 +340,7 @@ struct RolloutArgs {
                             // (zero between launches)
 };
 
-// LDS of a k_rollout block: the two worlds' physics scratch, or a policy tile's hidden activations
+// LDS of a k_rollout block: the two worlds' physics scratch, or a policy tile's scratch
 constexpr size_t kRolloutLds = 2 * sizeof(WorldLds) > sizeof(float) * kTileLds
                                    ? 2 * sizeof(WorldLds) : sizeof(float) * kTileLds;
 
@@ -355,7 +360,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
   auto set_queue = [&](int qq) {
     nq = npairs > qq ? (unsigned)((npairs - qq + kQueues - 1) / kQueues) : 0u;
     ntq = (nq + kTilePairs - 1) / kTilePairs;
-    nitems = nq ? ntq + (unsigned)(H * nch) * nq : 0u;
+    nitems = nq ? ntq + (H > 0 ? (unsigned)((H - 1) * nch + a.nchl) * nq : 0u) : 0u;
     ctr = a.qctr + a.qpar * kQueues + qq;
   };
   set_queue(q);
@@ -391,9 +396,18 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
       pol_u = (int)it;
       pol_np = (int)min((unsigned)kTilePairs, nq - kTilePairs * it);
     } else {
-    const unsigned r = it - ntq;
-    const int jj = (int)(r / nq), m = (int)(r - (unsigned)jj * nq);
-    const int t = jj / nch, c = jj - t * nch;
+    // chunk index jj of the pair within the launch (its flag counts completed chunks)
+    const unsigned r = it - ntq, nreg = (unsigned)((H - 1) * nch) * nq;
+    int jj, m, t, c;
+    if (r < nreg) {
+      jj = (int)(r / nq); m = (int)(r - (unsigned)jj * nq);
+      t = jj / nch; c = jj - t * nch;
+    } else {
+      const unsigned rl = r - nreg;
+      c = (int)(rl / nq); m = (int)(rl - (unsigned)c * nq);
+      t = H - 1; jj = (H - 1) * nch + c;
+    }
+    const int nck = t == H - 1 ? a.nchl : nch;
     const int p = qc + kQueues * m;
     const int u = m / kTilePairs;
     if (c > 0) wait_flag(a.flags + p, a.fbase + (unsigned)jj, a.qerr, a.xlocal);
@@ -406,7 +420,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
       physics_item(a, s, L, g, l, p, t, c, hcnt);
     }
     release_flag(a.flags + p, a.fbase + (unsigned)jj + 1u, a.xlocal);
-    if (c == nch - 1) {
+    if (c == nck - 1) {
       // this pair's step t is complete: count it for the tile; the wave completing the tile runs
       // the tile's policy of step t + 1
       const int np = (int)min((unsigned)kTilePairs, nq - kTilePairs * (unsigned)u);
@@ -957,28 +971,40 @@ static PhysArgs phys_args(EnvState* E) {
 //   2,2,2,2,1,1 0.444; 4,4,2 0.446; 4,3,2,1 0.448; 2 x 5 0.437; 3,3,3,1 0.457; 5,5 0.466.
 // * 32 pairs per wave (config 4, N = 131072): 6,4 5.81 ms; 5,5 5.83; 10 5.83; 4,3,3 5.86;
 //   2 x 5 5.98; 2,2,2,2,1,1 6.02.
-static void chunk_schedule(PhysArgs& a, int pgrid) {
+// In the one-launch rollout (one_launch) the policy items keep the waves busy across control
+// steps, and a whole control step per item does best (config 3, ms per rollout, every step cut the
+// same way): 10 12.82; 6,4 12.87-12.91; 5,5 12.88; 7,3 12.91; 4,3,3 13.01; 2,2,2,2,2 13.56.
+static void chunk_schedule(PhysArgs& a, int pgrid, bool one_launch = false) {
   const int S = a.S;
-  int n = 0, s0 = 0;
-  auto add = [&](int len) { a.cst[n++] = s0; s0 += len; };
+  // kind 0: one item; 1: 60% then the rest; 2: three-substep items (longer for S > 46, within
+  // kMaxChunks) while more than four substeps remain, then two, a single one last
+  auto build = [&](int kind, int* cst) {
+    int n = 0, s0 = 0;
+    auto add = [&](int len) { cst[n++] = s0; s0 += len; };
+    if (kind == 0) {
+      add(S);
+    } else if (kind == 1) {
+      const int first = (3 * S + 4) / 5;
+      add(first);
+      if (S > first) add(S - first);
+    } else {
+      const int big = std::max(3, (S - 4 + kMaxChunks - 3) / (kMaxChunks - 2));
+      while (S - s0 > 4) add(std::min(big, S - s0 - 2));
+      while (s0 < S) add(S - s0 >= 2 ? 2 : 1);
+    }
+    cst[n] = S;
+    if (n < 1 || n > kMaxChunks || s0 != S) fail("physics launch: bad substep chunk schedule");
+    for (int c = 0; c < n; ++c)
+      if (cst[c + 1] <= cst[c]) fail("physics launch: bad substep chunk schedule");
+    return n;
+  };
   const double work_per_wave = (double)((a.N + 1) / 2) * a.K / pgrid;   // pair-control-steps
-  if (work_per_wave >= 8.0) {
-    // two items: 60% of the substeps, then the rest
-    const int first = (3 * S + 4) / 5;
-    add(first);
-    if (S > first) add(S - first);
-  } else {
-    // three-substep items (longer for S > 46, within kMaxChunks) while more than four substeps
-    // remain, then two, a single one last
-    const int big = std::max(3, (S - 4 + kMaxChunks - 3) / (kMaxChunks - 2));
-    while (S - s0 > 4) add(std::min(big, S - s0 - 2));
-    while (s0 < S) add(S - s0 >= 2 ? 2 : 1);
-  }
-  a.cst[n] = S;
-  a.nch = n;
-  if (n < 1 || n > kMaxChunks || s0 != S) fail("physics launch: bad substep chunk schedule");
-  for (int c = 0; c < n; ++c)
-    if (a.cst[c + 1] <= a.cst[c]) fail("physics launch: bad substep chunk schedule");
+  const bool big = work_per_wave >= 8.0;
+  a.nch = build(one_launch && big ? 0 : (big ? 1 : 2), a.cst);
+  // the one-launch rollout ends its last control step in two items, which shortens the launch's
+  // drain (config 3, ms per rollout, same-box A/B: last step as 6,4 12.80; 3,3,2,2 12.80;
+  // 2,2,2,2,1,1 12.83; ten single substeps 12.86; one item 12.84-12.87)
+  a.nchl = build(big ? 1 : 2, a.cstl);
 }
 
 // Enqueue one physics launch on the null stream; the queue state (flag base, counter row) advances
@@ -1018,8 +1044,9 @@ static void poll_queue_error(EnvState* E) {
   check_queue_error(*(volatile int*)E->h_qerr);
 }
 
-// The one-launch rollout covers policies of two hidden layers of at most 256 units each (multiples of
-// 16); other shapes take the split form (policy and physics launches per control step).
+// The one-launch rollout covers policies of two hidden layers of at most 256 units each (run at
+// 256-256 with zero padding); other shapes take the split form (policy and physics launches per
+// control step).
 static bool fused_shape(const PolicyShape& sh) {
   return sh.nl == 2 && sh.hid[0] <= kTileMaxHidden && sh.hid[1] <= kTileMaxHidden;
 }
@@ -1054,7 +1081,7 @@ static void rollout_fused(EnvState* E, int H, const float* W, const float* mean,
   ra.ph = phys_args(E);
   PhysArgs& a = ra.ph;
   a.K = H; a.act = A; a.t0 = 0; a.astep = 1; a.rstep = 1; a.R = R; a.D = D; a.reset_noise = reset_noise;
-  chunk_schedule(a, E->pgrid);
+  chunk_schedule(a, E->pgrid, true);
   a.fbase = E->qdone;
   a.qpar = E->qpar;
   a.xlocal = E->xlocal && !E->fences;
@@ -1067,7 +1094,7 @@ static void rollout_fused(EnvState* E, int H, const float* W, const float* mean,
   hipLaunchKernelGGL(k_rollout, dim3((unsigned)E->pgrid), dim3(kPhysThreads), 0, 0, ra);
   HIPCHECK(hipGetLastError());
   if (prof) prof_mark(E->ev_phys, E->n_phys);
-  E->qdone += (unsigned)(H * a.nch);
+  E->qdone += H > 0 ? (unsigned)((H - 1) * a.nch + a.nchl) : 0u;
   E->tdone += (unsigned)H + 1u;
   E->qpar ^= 1;
   HIPCHECK(hipMemcpyAsync(E->h_qerr, E->qerr, sizeof(int), hipMemcpyDeviceToHost, 0));

@@ -196,6 +196,32 @@ def test_rollout_teacher_forced_one_launch_shapes(g1, orc, hidden, act):
     _assert_rows(rows)
 
 
+def test_one_launch_rollout_equals_step_by_step(g1):
+    """The one-launch rollout cuts a control step into work items by the work per wave: at N=8192
+    and H=8 every step but the last is one item and the last two (6 and 4 substeps); a launch per
+    control step (H=1) cuts each step into 3,3,2,2. Item boundaries only hand a pair's state over
+    and the policy tiles are the same, so one H=8 launch equals eight H=1 launches bit for bit:
+    every trajectory output, the bootstrap value and the final state (with timeouts and auto-resets
+    inside the horizon)."""
+    N, H = 8192, 8
+    qp, qv, pa, steps, W, mean, var, an, rn = _setup(N, H, 71)
+    steps[::7] = 993 + np.arange(steps[::7].size) % 7   # timeouts and auto-resets inside the horizon
+    with g1.Env(N, substeps=10, pgs_iters=8, seed=1) as env:
+        env.set_state(qp, qv, pa, steps)
+        one = _rollout(g1, env, W, mean, var, H, an, rn)
+        end_one = env.get_state()
+        env.set_state(qp, qv, pa, steps)
+        parts = [_rollout(g1, env, W, mean, var, 1, an[t:t + 1], rn[t:t + 1]) for t in range(H)]
+        end_steps = env.get_state()
+    for f in ("O", "A", "LP", "V", "R", "D"):
+        step_by_step = np.concatenate([q[f] for q in parts], 0)
+        assert np.array_equal(one[f].view(np.uint32), step_by_step.view(np.uint32)), f
+    assert np.array_equal(one["Vlast"].view(np.uint32), parts[-1]["Vlast"].view(np.uint32))
+    for a, b in zip(end_one, end_steps):
+        assert np.array_equal(a, b)
+    assert one["D"].sum() > 0
+
+
 @pytest.mark.parametrize("fences,fused", [(0, True), (1, True), (0, False), (1, False)])
 def test_rollout_matches_oracle_free_run(g1, orc, fences, fused):
     """A short rollout (N=96, H=3) with no teacher forcing: every output equals the oracle's own
