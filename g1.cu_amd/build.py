@@ -10,13 +10,12 @@ import subprocess
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-SRC = os.path.join(HERE, "csrc", "g1env.hip")
 OUT_DIR = os.path.join(HERE, "build")
 OUT = os.path.join(OUT_DIR, "libg1env.so")
 ARCH = os.environ.get("G1_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     # no packed-FP32 VALU forms (v_pk_*_f32): some of their forms have produced silently wrong
     # results on this GPU pool; hipcc's host pass warns that it does not know the feature
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -30,13 +29,30 @@ FLAGS = [
 ]
 
 
+# translation units and their own flags: the one-launch rollout kernel is scheduled ILP-first
+# (config 3 rollout 12.83 -> 12.77 ms); the same scheduler makes k_physics and k_policy slower
+# (config 4 rollout 233.5 -> 240.8 ms), so they keep the default one
+SOURCES = (
+    ("g1env.hip", []),
+    ("rollout_kernel.hip", ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]),
+)
+
+
 def build(verbose=False):
     os.makedirs(OUT_DIR, exist_ok=True)
-    cmd = ["hipcc", *FLAGS, SRC, "-o", OUT + ".tmp"]
-    if verbose:
-        cmd.append("-Rpass-analysis=kernel-resource-usage")
-        print(" ".join(cmd), flush=True)
+    objs = []
+    for name, extra in SOURCES:
+        obj = os.path.join(OUT_DIR, os.path.splitext(name)[0] + ".o")
+        cmd = ["hipcc", *FLAGS, *extra, "-c", os.path.join(HERE, "csrc", name), "-o", obj]
+        if verbose:
+            cmd.append("-Rpass-analysis=kernel-resource-usage")
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        objs.append(obj)
+    cmd = ["hipcc", f"--offload-arch={ARCH}", "-fPIC", "-shared", *objs, "-o", OUT + ".tmp"]
     subprocess.run(cmd, check=True)
+    for obj in objs:
+        os.remove(obj)
     os.replace(OUT + ".tmp", OUT)
     return OUT
 
