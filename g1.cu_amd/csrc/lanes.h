@@ -59,11 +59,20 @@ __device__ __forceinline__ int wave_max(int v) {
   return __builtin_amdgcn_readfirstlane(v > o ? v : o);
 }
 
-// Value of lane I of this lane's aligned 8-lane chain (ds_swizzle bit mode within 32 lanes:
-// and_mask 0x18 keeps the chain bits, or_mask selects lane I).
+// Value of lane I of this lane's aligned 8-lane chain. (Two DPP moves instead of one ds_swizzle:
+// the factor's chain levels wait on these broadcasts, and the swizzle's LDS round trip made config 3
+// 0.8% slower.)
 template <int I>
 __device__ __forceinline__ float chain_bcast(float v) {
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (I << 5)));
+  static_assert(I >= 0 && I < 8, "lane of the chain");
+  // quad_perm [i, i, i, i] (i = I mod 4) gives every quad its lane i; then the quad that does not
+  // hold lane I takes the other quad's value (row_shr:4 into banks 1 and 3, or row_shl:4 into
+  // banks 0 and 2): two DPP moves, VALU latency instead of an LDS round trip
+  constexpr int i = I & 3;
+  const int x = __builtin_amdgcn_update_dpp(0, __float_as_int(v), i | (i << 2) | (i << 4) | (i << 6), 0xF, 0xF, false);
+  const int y = I < 4 ? __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xA, false)
+                      : __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0x5, false);
+  return __int_as_float(y);
 }
 
 // 8-bit contact mask of this group from a wave ballot
