@@ -504,15 +504,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const int k = rowc < 3 ? rowc : rowc - 3, k1 = k == 2 ? 0 : k + 1, k2 = k == 0 ? 2 : k - 1;
     const bool isv = rowc >= 3;
     const int so = isv ? 3 : 0;
-    const int base8 = 8 * grp;
     float pc = 0.f, pac = 0.f;   // component rowc of the current body's v and a
 #pragma unroll
     for (int r = 2; r <= kMaxDepth; ++r) {
       const bool act = r >= c_lo && r <= c_hi;
       const int b = chain_body(r);
       // parent's components: the chain's previous level, or from LDS at a chain's first body
-      float X1 = gshfl(pc, base8 + k1), X2 = gshfl(pc, base8 + k2);            // w_p[k+1], w_p[k+2]
-      float Y1 = gshfl(pc, base8 + 3 + k1), Y2 = gshfl(pc, base8 + 3 + k2);    // v_p[k+1], v_p[k+2]
+      float X1, X2, Y1, Y2;   // w_p[k+1], w_p[k+2], v_p[k+1], v_p[k+2]
+      chain_rot3(pc, X1, X2, Y1, Y2);
       float P = pc, PA = pac;
       if (r == 2 || r == 5) {
         const bool start = (r == c_lo);
