@@ -187,9 +187,9 @@ __device__ __forceinline__ float dot6(const float* a, const float* b) {
 }
 
 // Scheduling pin for the unrolled tree traversals: forces the six carried values through a
-// (no-op) volatile asm so each body's arithmetic completes before the next body's LDS reads are
-// issued. Without it the unrolled code hoists every body's loads up front and runs out of
-// registers.
+// (no-op) volatile asm, which no LDS access crosses. Without it the unrolled code hoists every
+// body's loads up front and runs out of registers; the traversals issue the next body's reads
+// before the pin, so one body's reads are in flight while the current body computes.
 #define G1_PIN6(v) __asm__ volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5])::"memory")
 
 // MuJoCo solimp impedance sigmoid (reference: src/contact.cuh:97-109)
@@ -914,31 +914,43 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     float u[kNBody];
 #pragma unroll
     for (int b = 14; b < kNBody; ++b) u[b] = 0.f;
-    float carR[6], carL[6], c8[6], c2[6];
-    auto up = [&](int b, float (&car)[6], float (&croot)[6]) {
-      const int d = b + 4;
+    // Each body's LDS operands are read one body ahead (`nxt`) so their latency overlaps the
+    // current body's arithmetic; the pin keeps the reads from running further ahead.
+    // (only plain loads: a value used before the pin would make it wait for them)
+    struct UpIn { float S[6], U[6], iD, e; };
+    auto ld_up = [&](int b, UpIn& f) {
+#pragma unroll
+      for (int k = 0; k < 6; ++k) { f.S[k] = s.u.fac.S[b + 4][k]; f.U[k] = s.u.fac.U[b][k]; }
+      f.iD = s.u.fac.invD[b];
+      f.e = eb[b < 8 ? 7 - b : 13 - b];   // xrhs(b + 4) before its select
+    };
+    constexpr int kUpOrder[12] = {13, 7, 12, 6, 11, 5, 10, 4, 9, 3, 8, 2};
+    float car[2][6] = {}, croot[2][6];   // [0] right leg (13..8), [1] left leg (7..2)
+    UpIn cur, nxt;
+    ld_up(kUpOrder[0], cur);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      const int b = kUpOrder[i], g = i & 1;
+      if (i + 1 < 12) ld_up(kUpOrder[i + 1], nxt);
       float pb[6];
 #pragma unroll
-      for (int k = 0; k < 6; ++k) pb[k] = body_nchild[b] == 0 ? 0.f : car[k];
-      const float* Sd = s.u.fac.S[d];
-      const float* Ub = s.u.fac.U[b];
-      const float ub = xrhs(d) - dot6(Sd, pb);
+      for (int k = 0; k < 6; ++k) pb[k] = body_nchild[b] == 0 ? 0.f : car[g][k];
+      const bool own = basis && (b < 8 ? !right : right);
+      const float ub = (own ? cur.e : 0.f) - dot6(cur.S, pb);
       u[b] = ub;
-      const float ud = ub * s.u.fac.invD[b];
+      const float ud = ub * cur.iD;
 #pragma unroll
       for (int k = 0; k < 6; ++k) {
-        const float c = fmaf_(Ub[k], ud, pb[k]);
-        if (body_parent[b] == 1) croot[k] = c;
-        else car[k] = c;
+        const float c = fmaf_(cur.U[k], ud, pb[k]);
+        if (body_parent[b] == 1) croot[g][k] = c;
+        else car[g][k] = c;
       }
-      G1_PIN6(car);
+      G1_PIN6(car[g]);
       __asm__ volatile("" : "+v"(u[b]));
-    };
-#pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      up(13 - i, carR, c8);
-      up(7 - i, carL, c2);
+      if (i + 1 < 12) cur = nxt;
     }
+    const float (&c8)[6] = croot[0];
+    const float (&c2)[6] = croot[1];
     float p1[6];
     const bool smooth = j == 0;
 #pragma unroll
@@ -986,45 +998,35 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
     G1_PIN6(a1);
     // root -> leaf over five independent chains, walked interleaved: legs and waist from the
-    // pelvis (2.., 8.., 14..16), then both arms from the torso (17.., 24..)
+    // pelvis (2.., 8.., 14..16), then both arms from the torso (17.., 24..); operands read one
+    // body ahead as in the leaf -> root pass
     static_assert(body_parent[14] == 1 && body_parent[17] == 16 && body_parent[24] == 16, "chains");
-    auto down = [&](int b, const float (&ap)[6], float (&ac)[6]) {
-      const int d = b + 4;
-      const float* Ub = s.u.fac.U[b];
-      const float* Sd = s.u.fac.S[d];
-      const float ub = smooth ? s.u.fac.us[b] : u[b];
-      const float q = (ub - dot6(Ub, ap)) * s.u.fac.invD[b];
-      if (wr) ycol[d] = q;
+    struct DnIn { float U[6], S[6], iD, us; };
+    auto ld_dn = [&](int b, DnIn& f) {
 #pragma unroll
-      for (int k = 0; k < 6; ++k) ac[k] = fmaf_(Sd[k], q, ap[k]);
-      G1_PIN6(ac);
+      for (int k = 0; k < 6; ++k) { f.U[k] = s.u.fac.U[b][k]; f.S[k] = s.u.fac.S[b + 4][k]; }
+      f.iD = s.u.fac.invD[b];
+      f.us = s.u.fac.us[b];
     };
-    float aL[6], aR[6], aW[6], tmp[6];
-    down(2, a1, aL); down(8, a1, aR); down(14, a1, aW);
+    constexpr int kDownOrder[29] = {2, 8, 14, 3, 9, 15, 4, 10, 16, 5, 11, 6, 12, 7, 13,
+                                    17, 24, 18, 25, 19, 26, 20, 27, 21, 28, 22, 29, 23, 30};
+    float acc[5][6];   // left leg, right leg, waist (the torso 16 at its end), left arm, right arm
+    DnIn dc, dn;
+    ld_dn(kDownOrder[0], dc);
 #pragma unroll
-    for (int i = 1; i < 6; ++i) {
+    for (int i = 0; i < 29; ++i) {
+      const int b = kDownOrder[i];
+      const int ch = b < 8 ? 0 : b < 14 ? 1 : b < 17 ? 2 : b < 24 ? 3 : 4;
+      if (i + 1 < 29) ld_dn(kDownOrder[i + 1], dn);
+      float ap[6];
 #pragma unroll
-      for (int k = 0; k < 6; ++k) tmp[k] = aL[k];
-      down(2 + i, tmp, aL);
+      for (int k = 0; k < 6; ++k) ap[k] = body_parent[b] == 1 ? a1[k] : body_parent[b] == 16 ? acc[2][k] : acc[ch][k];
+      const float q = ((smooth ? dc.us : u[b]) - dot6(dc.U, ap)) * dc.iD;
+      if (wr) ycol[b + 4] = q;
 #pragma unroll
-      for (int k = 0; k < 6; ++k) tmp[k] = aR[k];
-      down(8 + i, tmp, aR);
-      if (i < 3) {
-#pragma unroll
-        for (int k = 0; k < 6; ++k) tmp[k] = aW[k];
-        down(14 + i, tmp, aW);
-      }
-    }
-    float aLA[6], aRA[6];
-    down(17, aW, aLA); down(24, aW, aRA);   // aW is the torso (16) now
-#pragma unroll
-    for (int i = 1; i < 7; ++i) {
-#pragma unroll
-      for (int k = 0; k < 6; ++k) tmp[k] = aLA[k];
-      down(17 + i, tmp, aLA);
-#pragma unroll
-      for (int k = 0; k < 6; ++k) tmp[k] = aRA[k];
-      down(24 + i, tmp, aRA);
+      for (int k = 0; k < 6; ++k) acc[ch][k] = fmaf_(dc.S[k], q, ap[k]);
+      G1_PIN6(acc[ch]);
+      if (i + 1 < 29) dc = dn;
     }
   }
   __syncthreads();
