@@ -820,22 +820,44 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
   }
   // ---------------- smooth solve root -> leaf (reference: src/aba_factor.cuh:156-164)
+  // In the factor's chain layout: the four chains walk root -> leaf in lock-step over depth, every
+  // lane of a chain carrying the whole 6-vector acceleration (the per-body operations of the
+  // lane-per-body form, redundantly on the chain's lanes), so a level has no cross-lane exchange;
+  // the chains start from the pelvis (lane 1), the right arm from the torso (chain 2, depth 4).
+  // A chain's values outside its depth range are never stored, and the right arm's are replaced
+  // at its first level. Each level's LDS operands are read one level ahead.
   if (ncon_max == 0) {
-    float Uk[6];
+    float a[6];
 #pragma unroll
-    for (int k = 0; k < 6; ++k) Uk[k] = s.u.fac.U[L.b][k];
-    const float usk = s.u.fac.us[L.b], iDk = s.u.fac.invD[L.b];
+    for (int k = 0; k < 6; ++k) a[k] = gshfl(a6[k], 1);
+    float U[6], S[6], us, iD;
+    auto ld = [&](int r) {
+      const int b = chain_body(r);
+#pragma unroll
+      for (int k = 0; k < 6; ++k) { U[k] = s.u.fac.U[b][k]; S[k] = s.u.fac.S[b + 4][k]; }
+      us = s.u.fac.us[b];
+      iD = s.u.fac.invD[b];
+    };
+    ld(2);
 #pragma unroll
     for (int r = 2; r <= kMaxDepth; ++r) {
-      float ap[6];
+      if (r == kTorsoDepth + 1) {
+        float at[6];
 #pragma unroll
-      for (int k = 0; k < 6; ++k) ap[k] = gshfl(a6[k], L.par);
-      if (L.depth == r) {
-        const float q = (usk - dot6(Uk, ap)) * iDk;
+        for (int k = 0; k < 6; ++k) at[k] = gshfl(a[k], 16 + crow);
+        if (grp == 3) {
 #pragma unroll
-        for (int k = 0; k < 6; ++k) a6[k] = fmaf_(S6[k], q, ap[k]);
-        s.Mm[0][L.b + 4] = q;
+          for (int k = 0; k < 6; ++k) a[k] = at[k];
+        }
       }
+      const float Uc[6] = {U[0], U[1], U[2], U[3], U[4], U[5]};
+      const float Sc[6] = {S[0], S[1], S[2], S[3], S[4], S[5]};
+      const float usc = us, iDc = iD;
+      if (r < kMaxDepth) ld(r + 1);
+      const float q = (usc - dot6(Uc, a)) * iDc;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) a[k] = fmaf_(Sc[k], q, a[k]);
+      if (r >= c_lo && r <= c_hi && crow == 0) s.Mm[0][chain_body(r) + 4] = q;
     }
   }
 
