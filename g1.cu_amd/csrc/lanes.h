@@ -69,19 +69,21 @@ __device__ __forceinline__ float chain_bcast(float v) {
   // hold lane I takes the other quad's value (row_shr:4 into banks 1 and 3, or row_shl:4 into
   // banks 0 and 2): two DPP moves, VALU latency instead of an LDS round trip
   constexpr int i = I & 3;
-  const int x = __builtin_amdgcn_update_dpp(0, __float_as_int(v), i | (i << 2) | (i << 4) | (i << 6), 0xF, 0xF, false);
+  // (mov_dpp: no old value to materialise; every quad_perm source lane exists)
+  const int x = __builtin_amdgcn_mov_dpp(__float_as_int(v), i | (i << 2) | (i << 4) | (i << 6), 0xF, 0xF, true);
   const int y = I < 4 ? __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xA, false)
                       : __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0x5, false);
   return __int_as_float(y);
 }
 
-// DPP moves within 16-lane rows (identical in every row)
+// DPP moves within 16-lane rows (identical in every row); mov_dpp with bound_ctrl: lanes whose
+// source lies outside the row read 0, and no old value has to be materialised
 template <int A, int B, int C, int D>
 __device__ __forceinline__ float quad_perm(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), A | (B << 2) | (C << 4) | (D << 6), 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), A | (B << 2) | (C << 4) | (D << 6), 0xF, 0xF, true));
 }
 __device__ __forceinline__ float row_shl3(float v) {   // lane i <- lane i + 3 of its row
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x103, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x103, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float shr3_upper_quads(float x) {   // lanes 4..7 of each 8 <- lanes 1..4
   return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x113, 0xF, 0xA, false));

@@ -748,19 +748,29 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   __syncthreads();   // I^A of the pelvis and the hinge factor complete in LDS
   if (l < 6) {
     // column l of U6 = I^A S_base: translation l < 3 picks column 3 + l of I^A, rotation l >= 3
-    // is I^A's angular columns times R1 col (l - 3) (structural zeros skipped, see sbase_dot)
-    const int lt = l < 3 ? l : 0;
-    const float* Sc = s.u.fac.S[l < 3 ? 3 : l];   // (translation lanes: any stored row, unused)
+    // is I^A's angular columns times R1 col (l - 3) (structural zeros skipped, see sbase_dot).
+    // The packed I^A and the rows S[3..5] are read whole (the same addresses on every lane) and
+    // the lane's column is selected in registers.
+    float IA[21], S3[3][3];
+#pragma unroll
+    for (int i = 0; i < 21; ++i) IA[i] = s.u.fac.IA1[i];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+      for (int i = 0; i < 3; ++i) S3[k][i] = s.u.fac.S[3 + k][i];
+    float Sc[3];   // row S[l] of a rotation lane (translation lanes: unused)
+#pragma unroll
+    for (int i = 0; i < 3; ++i) Sc[i] = l == 4 ? S3[1][i] : (l == 5 ? S3[2][i] : S3[0][i]);
     float U6c[6];
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
-      const float rot = fmaf_(s.u.fac.IA1[symidx(i, 2)], Sc[2],
-                              fmaf_(s.u.fac.IA1[symidx(i, 1)], Sc[1], s.u.fac.IA1[symidx(i, 0)] * Sc[0]));
-      U6c[i] = l < 3 ? s.u.fac.IA1[symidx(i, 3 + lt)] : rot;
+      const float rot = fmaf_(IA[symidx(i, 2)], Sc[2], fmaf_(IA[symidx(i, 1)], Sc[1], IA[symidx(i, 0)] * Sc[0]));
+      const float tr = l == 0 ? IA[symidx(i, 3)] : (l == 1 ? IA[symidx(i, 4)] : IA[symidx(i, 5)]);
+      U6c[i] = l < 3 ? tr : rot;
     }
     // D = S_base' U6 (+ armature and dt*damping, both 0 on the free joint)
 #pragma unroll
-    for (int k = 0; k < 6; ++k) s.u.fac.Dm[k * 6 + l] = sbase_dot(k, s.u.fac.S[k], U6c);
+    for (int k = 0; k < 6; ++k) s.u.fac.Dm[k * 6 + l] = sbase_dot(k, S3[k < 3 ? 0 : k - 3], U6c);
   }
   __syncthreads();
   float a6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -869,6 +879,9 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const int legbase = s.con_leg[c] ? 12 : 6;
     const V3 r = vsub(V3{s.con[c][0], s.con[c][1], s.con[c][2]}, p);
     float v0 = 0.f, v1 = 0.f, v2 = 0.f;
+    // the rows are stored after the loop: stores between the reads would keep each dof's reads
+    // from issuing before the previous dof's stores
+    float E[3][kContactDofs];
 #pragma unroll
     for (int k = 0; k < kContactDofs; ++k) {
       // ancestor dofs walked foot -> root: leg hinges (foot first), then the free base 0..5
@@ -886,10 +899,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         jc = cross(V3{s.u.fac.S[a][0], s.u.fac.S[a][1], s.u.fac.S[a][2]}, r);
       }
       const float e0 = jc.z, e1 = mu * jc.y, e2 = -mu * jc.x;
-      s.Eb[c][0][k] = e0; s.Eb[c][1][k] = e1; s.Eb[c][2][k] = e2;
+      E[0][k] = e0; E[1][k] = e1; E[2][k] = e2;
       const float qd = s.qvel[a];
       v0 = fmaf_(e0, qd, v0); v1 = fmaf_(e1, qd, v1); v2 = fmaf_(e2, qd, v2);
     }
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int k = 0; k < kContactDofs; ++k) s.Eb[c][a][k] = E[a][k];
     const float dmax = MF::foot_solimp[1], tc = MF::foot_solref[0], dr = MF::foot_solref[1];
     const float bcoef = 2.f / (dmax * tc);
     const float kcoef = 1.f / (dmax * dmax * tc * tc * dr * dr);
