@@ -504,11 +504,29 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const int k = rowc < 3 ? rowc : rowc - 3, k1 = k == 2 ? 0 : k + 1, k2 = k == 0 ? 2 : k - 1;
     const bool isv = rowc >= 3;
     const int so = isv ? 3 : 0;
+    // per-lane base pointers: depth r's operands sit at a constant offset from them, and the next
+    // level's are read before this level's stores (which the compiler cannot tell apart from them)
+    const float* const Sl = &s.u.fac.S[c_off + 4][0];
+    const float* const pS0 = Sl + rowc;
+    const float* const pS1 = Sl + so + k1;
+    const float* const pS2 = Sl + so + k2;
+    const float* const pS3 = Sl + k1;
+    const float* const pS4 = Sl + k2;
+    const float* const pq = &s.qvel[c_off + 4];
+    float* const pV = V6 + 6 * c_off + crow;
+    float* const pA = A6 + 6 * c_off + crow;
+    float nS[5], nq;
+    auto ld = [&](int r) {
+      nS[0] = pS0[6 * r]; nS[1] = pS1[6 * r]; nS[2] = pS2[6 * r]; nS[3] = pS3[6 * r]; nS[4] = pS4[6 * r];
+      nq = pq[r];
+    };
+    ld(2);
     float pc = 0.f, pac = 0.f;   // component rowc of the current body's v and a
 #pragma unroll
     for (int r = 2; r <= kMaxDepth; ++r) {
       const bool act = r >= c_lo && r <= c_hi;
-      const int b = chain_body(r);
+      const float Sr = nS[0], Sw1 = nS[1], Sw2 = nS[2], Sv1 = nS[3], Sv2 = nS[4], qd = nq;
+      if (r < kMaxDepth) ld(r + 1);
       // parent's components: the chain's previous level, or from LDS at a chain's first body
       float X1, X2, Y1, Y2;   // w_p[k+1], w_p[k+2], v_p[k+1], v_p[k+2]
       chain_rot3(pc, X1, X2, Y1, Y2);
@@ -522,18 +540,16 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
           P = pv6[rowc]; PA = A6[6 * pb + rowc];
         }
       }
-      const float* Sb = s.u.fac.S[b + 4];
-      const float qd = s.qvel[b + 4];
-      const float vn = fmaf_(Sb[rowc], qd, P);
-      const float t1 = fmaf_(-X2, Sb[so + k1], X1 * Sb[so + k2]);   // (w_p x s_w)_k, or (w_p x s_v)_k
-      const float t2 = fmaf_(-Y2, Sb[k1], Y1 * Sb[k2]);             // (v_p x s_w)_k
+      const float vn = fmaf_(Sr, qd, P);
+      const float t1 = fmaf_(-X2, Sw1, X1 * Sw2);   // (w_p x s_w)_k, or (w_p x s_v)_k
+      const float t2 = fmaf_(-Y2, Sv1, Y1 * Sv2);   // (v_p x s_w)_k
       const float sd = isv ? t1 + t2 : t1;
       const float an = fmaf_(sd, qd, PA);
       // a chain's values outside its depth range are never read (its first body takes the parent
       // from LDS, its results are stored only while active), so no select keeps them
       pc = vn;
       pac = an;
-      if (act && crow < 6) { V6[6 * b + crow] = pc; A6[6 * b + crow] = pac; }
+      if (act && crow < 6) { pV[6 * r] = pc; pA[6 * r] = pac; }
       if (r == 4) __syncthreads();   // the torso (depth 4) is in LDS before the right arm starts
     }
   }
