@@ -94,6 +94,13 @@ __device__ __forceinline__ double gshfld(double v, int src) { return __shfl(v, s
 // shallow penetrations; correct rounding makes every transcendental reproducible bit-for-bit.
 __device__ __forceinline__ float sin_rn(float x) { return (float)sin((double)x); }
 __device__ __forceinline__ float cos_rn(float x) { return (float)cos((double)x); }
+// both from one fp64 argument reduction
+__device__ __forceinline__ void sincos_rn(float x, float& sn, float& cs) {
+  double sd, cd;
+  sincos((double)x, &sd, &cd);
+  sn = (float)sd;
+  cs = (float)cd;
+}
 
 // sin_rn and cos_rn of one argument on a short path for |x| <= 1/8 (the free joint's half rotation
 // per substep): the fp64 Taylor series by Horner, sin to x^11 and cos to x^12 (truncation below
@@ -118,8 +125,7 @@ __device__ __forceinline__ void sincos_small_rn(float x, float& sn, float& cs) {
     sn = (x == 0.f) ? x : s_;   // sin(-0) = -0
     cs = (float)__builtin_fma(z, pc, 1.0);
   } else {
-    sn = sin_rn(x);
-    cs = cos_rn(x);
+    sincos_rn(x, sn, cs);
   }
 }
 
@@ -357,8 +363,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   Q4 xq{1.f, 0.f, 0.f, 0.f};
   V3 xip{0.f, 0.f, 0.f};
   {
-    const float h = 0.5f * st.jq, sn = sin_rn(h);
-    const Q4 aa{cos_rn(h), L.axis.x * sn, L.axis.y * sn, L.axis.z * sn};
+    const float h = 0.5f * st.jq;
+    float sn, cs;
+    sincos_rn(h, sn, cs);
+    const Q4 aa{cs, L.axis.x * sn, L.axis.y * sn, L.axis.z * sn};
     if (L.hinge) {
       xp = L.bpos;
       xq = qmul(L.bquat, aa);

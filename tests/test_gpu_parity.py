@@ -298,6 +298,33 @@ def test_small_angle_sincos_exhaustive(g1, orc):
     assert np.array_equal(ds.cpu().numpy(), want_s) and np.array_equal(dc.cpu().numpy(), want_c)
 
 
+def test_hinge_sincos_exhaustive(g1, orc):
+    """Above 1/8 the probe takes the FK's hinge path (one fp64 sincos, each result rounded once):
+    bit-identical to the oracle's fp64 libm sin and cos rounded once for EVERY float with
+    1/8 < |x| <= 4 (hinge half-angles, joint ranges included), plus a sample of larger ones."""
+    import torch
+    lo = int(np.float32(0.125).view(np.uint32)) + 1
+    hi = int(np.float32(4.0).view(np.uint32))
+    chunk = 1 << 25
+    for start in range(lo, hi + 1, chunk):
+        bits = np.arange(start, min(start + chunk, hi + 1), dtype=np.uint32)
+        for sign in (np.uint32(0), np.uint32(0x80000000)):
+            x = (bits | sign).view(np.float32)
+            dx = torch.from_numpy(x).cuda()
+            ds, dc = torch.zeros_like(dx), torch.zeros_like(dx)
+            g1.lib.g1_probe_sincos(x.size, g1.dev_ptr(dx), g1.dev_ptr(ds), g1.dev_ptr(dc))
+            want_s, want_c = orc.sincos(x)
+            assert np.array_equal(ds.cpu().numpy().view(np.uint32), want_s.view(np.uint32)), start
+            assert np.array_equal(dc.cpu().numpy().view(np.uint32), want_c.view(np.uint32)), start
+    rng = np.random.default_rng(7)
+    x = (rng.uniform(4, 1e4, 1 << 22) * rng.choice([-1, 1], 1 << 22)).astype(np.float32)
+    dx = torch.from_numpy(x).cuda()
+    ds, dc = torch.zeros_like(dx), torch.zeros_like(dx)
+    g1.lib.g1_probe_sincos(x.size, g1.dev_ptr(dx), g1.dev_ptr(ds), g1.dev_ptr(dc))
+    want_s, want_c = orc.sincos(x)
+    assert np.array_equal(ds.cpu().numpy(), want_s) and np.array_equal(dc.cpu().numpy(), want_c)
+
+
 def test_policy_mlp_trained_checkpoint(g1, orc):
     """The reference's trained policy (converted checkpoint) through the MFMA policy kernel vs the
     oracle's fp32 MLP on normalised observations of perturbed stand states."""
