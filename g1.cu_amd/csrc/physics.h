@@ -653,11 +653,20 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // tau - S.F (the bias in the lane-per-body form's order).
   float Fc = 0.f;                                  // component rowc of the last body's subtree force
   float Sn[6], In[6], Fn, tn, an, kn;
+  // per-lane base pointers: depth cd's operands and results sit at constant offsets from them
+  const float* const pSc = &s.u.fac.S[c_off + 4][0];
+  const float* const pFc = Fo + 6 * c_off + rowc;
+  const float* pIc[6];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) pIc[j] = I6 + 21 * c_off + symidx(rowc, j);
+  float* const pUc = &s.u.fac.U[c_off][crow];
+  float* const pDc = &s.u.fac.invD[c_off];
+  float* const pUs = &s.u.fac.us[c_off];
   auto prefetch = [&](int cd) {
     const int b = chain_body(cd);
 #pragma unroll
-    for (int j = 0; j < 6; ++j) { Sn[j] = s.u.fac.S[b + 4][j]; In[j] = I6[b * 21 + symidx(rowc, j)]; }
-    Fn = Fo[6 * b + rowc];
+    for (int j = 0; j < 6; ++j) { Sn[j] = pSc[6 * cd + j]; In[j] = pIc[j][21 * cd]; }
+    Fn = pFc[6 * cd];
     tn = gshfl(jtau, b);
     an = gshfl(L.arm, b);
     kn = gshfl(L.bdt, b);
@@ -711,8 +720,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       cs[j] = c;
     }
     Fc = F;
-    if (act && crow < 6) s.u.fac.U[b][crow] = ur;
-    if (act && crow == 0) { s.u.fac.invD[b] = invD; s.u.fac.us[b] = u; }
+    if (act && crow < 6) pUc[6 * cd] = ur;
+    if (act && crow == 0) { pDc[cd] = invD; pUs[cd] = u; }
   };
   // Issue priority (s_setprio): two waves share a SIMD, and the phases that are dependency chains
   // over the tree or the PGS rows (this factor: 1; the contact pipeline from PASS 1 through PGS: 3)
