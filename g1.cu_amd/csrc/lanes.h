@@ -50,6 +50,17 @@ __device__ __forceinline__ float gsum16(float v) {
   return v;
 }
 
+// gsum when only lanes 0..3 of the group can be nonzero (the others hold +-0): for lanes 0..3 the
+// butterfly's stages over 8 and 4 lanes add only zeros, and its last two stages are the quad's xor-2
+// and xor-1 exchanges, done here by quad_perm; the same operands in every addition (IEEE addition is
+// commutative), so lanes 0..3 get gsum16's result except for the sign of an exactly-zero sum. Lanes
+// 4..31 get their own quads' sums.
+__device__ __forceinline__ float gsum4(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 2 | (3 << 2) | (0 << 4) | (1 << 6), 0xF, 0xF, true));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 1 | (0 << 2) | (3 << 4) | (2 << 6), 0xF, 0xF, true));
+  return v;
+}
+
 // maximum of an int over the whole wave (both groups): uniform trip counts for loops whose
 // length depends on per-world data
 __device__ __forceinline__ int wave_max(int v) {

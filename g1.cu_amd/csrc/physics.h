@@ -311,22 +311,26 @@ struct SolveParams {
 // sum. The quotient x / A_ii uses the correctly rounded reciprocal y = RN(1/A_ii) and one
 // exact-residual correction: q0 = RN(x y), r = x - A_ii q0 (exact with fma), q = RN(q0 + r y) equals
 // RN(x / A_ii) (Markstein's theorem), the IEEE quotient, on a 3-op dependency chain.
-// Half: the wave has at most 16 rows per world (nefc_max <= 16), so lanes 16..31 hold zero columns and
-// zero f and the row sums skip their stage (gsum16; only the sign of an exactly-zero sum can differ).
-template <int II, bool Half>
+// W: the rows a world can hold in this wave (nefc_max <= W). W = 16: lanes 16..31 hold zero columns
+// and zero f and the row sums skip their stage (gsum16); W = 4 (at most one contact per world):
+// only lanes 0..3 hold nonzero products and the sums take the butterfly's last two stages (gsum4).
+// Either way only the sign of an exactly-zero sum can differ from the full sum's, and only the
+// row's own lane keeps its update.
+template <int II, int W>
 __device__ __forceinline__ void pgs_sweep(const float (&Acol)[kMaxEfc], float Aii, float yi, float bi, int l,
                                           int nefc_max, float& fi) {
-  if constexpr (II < (Half ? kGroup / 2 : kMaxEfc)) {
+  if constexpr (II < W) {
     if (II < nefc_max) {
       // sum_j A[II][j] f_j (lane j holds column j)
-      const float sum = Half ? gsum16(Acol[II] * fi) : gsum(Acol[II] * fi);
+      const float pr = Acol[II] * fi;
+      const float sum = W == 4 ? gsum4(pr) : (W == 16 ? gsum16(pr) : gsum(pr));
       const float ri = fmaf_(-Aii, fi, bi + sum);
       const float x = -ri;
       const float q0 = x * yi;
       const float fn = __builtin_fmaf(__builtin_fmaf(-q0, Aii, x), yi, q0);
       const float fnew = fn > 0.f ? fn : 0.f;
       fi = (l == II) ? fnew : fi;
-      pgs_sweep<II + 1, Half>(Acol, Aii, yi, bi, l, nefc_max, fi);
+      pgs_sweep<II + 1, W>(Acol, Aii, yi, bi, l, nefc_max, fi);
     }
   }
 }
@@ -1211,12 +1215,15 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // ---------------- projected Gauss-Seidel (reference: src/contact.cuh:159-171), P.pgs sweeps
   float fi = 0.f;
   const float yi = rcp_rn(Aii);
-  if (nefc_max <= kGroup / 2) {
+  if (nefc_max <= 4) {
 #pragma unroll 1
-    for (int it = 0; it < P.pgs; ++it) pgs_sweep<0, true>(Acol, Aii, yi, bi, l, nefc_max, fi);
+    for (int it = 0; it < P.pgs; ++it) pgs_sweep<0, 4>(Acol, Aii, yi, bi, l, nefc_max, fi);
+  } else if (nefc_max <= kGroup / 2) {
+#pragma unroll 1
+    for (int it = 0; it < P.pgs; ++it) pgs_sweep<0, kGroup / 2>(Acol, Aii, yi, bi, l, nefc_max, fi);
   } else {
 #pragma unroll 1
-    for (int it = 0; it < P.pgs; ++it) pgs_sweep<0, false>(Acol, Aii, yi, bi, l, nefc_max, fi);
+    for (int it = 0; it < P.pgs; ++it) pgs_sweep<0, kMaxEfc>(Acol, Aii, yi, bi, l, nefc_max, fi);
   }
   __builtin_amdgcn_s_setprio(0);
   if (row) s.f[l] = fi;
