@@ -911,39 +911,42 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   __builtin_amdgcn_s_setprio(3);   // the contact pipeline (see the factor above)
   // ---------------- PASS 1: basis rows, R, aref (reference: src/env_qacc.cuh:67-136)
   const float mu = P.mu;
+  static_assert(kContactDofs == 12 && 2 * kContactDofs <= kGroup, "two contacts' rows per pass");
+  if (ncon_max > 0) {
+    // the basis rows, lane-parallel: in pass ps lane l < 24 forms the three entries of contact
+    // 2 ps + l / 12 on its ancestor dof k = l mod 12, walked foot -> root: leg hinges (foot first),
+    // then the free base 0..5. Point Jacobian column w x r + lv; on the free base the structural
+    // zeros of S_base are skipped (see sbase_dot): translation a gives e_a, rotation a gives w x r.
+    const int k = l % kContactDofs;
+#pragma unroll
+    for (int ps = 0; ps < (kNFoot + 1) / 2; ++ps) {
+      if (2 * ps >= ncon_max) break;
+      const int ci = 2 * ps + l / kContactDofs;
+      const bool on = l < 2 * kContactDofs && ci < ncon;
+      const int c = on ? ci : 0;
+      const int a = (k < 6) ? (s.con_leg[c] ? 12 : 6) + 5 - k : k - 6;
+      const V3 r = vsub(V3{s.con[c][0], s.con[c][1], s.con[c][2]}, p);
+      const float* Sa = s.u.fac.S[a];   // (base translation rows: never stored, unused)
+      const V3 cr = cross(V3{Sa[0], Sa[1], Sa[2]}, r);
+      const V3 leg = vadd(cr, V3{Sa[3], Sa[4], Sa[5]});
+      const bool trans = k >= 6 && a < 3;
+      const V3 jc{k < 6 ? leg.x : (trans ? (a == 0 ? 1.f : 0.f) : cr.x),
+                  k < 6 ? leg.y : (trans ? (a == 1 ? 1.f : 0.f) : cr.y),
+                  k < 6 ? leg.z : (trans ? (a == 2 ? 1.f : 0.f) : cr.z)};
+      if (on) { s.Eb[c][0][k] = jc.z; s.Eb[c][1][k] = mu * jc.y; s.Eb[c][2][k] = -mu * jc.x; }
+    }
+  }
+  __syncthreads();   // the basis rows in LDS
   if (ncon_max > 0 && l < ncon) {
     const int c = l;
     const int legbase = s.con_leg[c] ? 12 : 6;
-    const V3 r = vsub(V3{s.con[c][0], s.con[c][1], s.con[c][2]}, p);
+    // the reference velocities of the four pyramid rows: sum_k e_a[k] qd[k] in dof order
     float v0 = 0.f, v1 = 0.f, v2 = 0.f;
-    // the rows are stored after the loop: stores between the reads would keep each dof's reads
-    // from issuing before the previous dof's stores
-    float E[3][kContactDofs];
 #pragma unroll
     for (int k = 0; k < kContactDofs; ++k) {
-      // ancestor dofs walked foot -> root: leg hinges (foot first), then the free base 0..5
-      const int a = (k < 6) ? legbase + 5 - k : k - 6;
-      // point Jacobian column w x r + lv; on the free base (k >= 6) the structural zeros of
-      // S_base are skipped (see sbase_dot): translation a gives e_a, rotation a gives w x r
-      V3 jc;
-      if (k < 6) {
-        const V3 w{s.u.fac.S[a][0], s.u.fac.S[a][1], s.u.fac.S[a][2]};
-        const V3 lv{s.u.fac.S[a][3], s.u.fac.S[a][4], s.u.fac.S[a][5]};
-        jc = vadd(cross(w, r), lv);
-      } else if (a < 3) {
-        jc = {a == 0 ? 1.f : 0.f, a == 1 ? 1.f : 0.f, a == 2 ? 1.f : 0.f};
-      } else {
-        jc = cross(V3{s.u.fac.S[a][0], s.u.fac.S[a][1], s.u.fac.S[a][2]}, r);
-      }
-      const float e0 = jc.z, e1 = mu * jc.y, e2 = -mu * jc.x;
-      E[0][k] = e0; E[1][k] = e1; E[2][k] = e2;
-      const float qd = s.qvel[a];
-      v0 = fmaf_(e0, qd, v0); v1 = fmaf_(e1, qd, v1); v2 = fmaf_(e2, qd, v2);
+      const float qd = s.qvel[(k < 6) ? legbase + 5 - k : k - 6];
+      v0 = fmaf_(s.Eb[c][0][k], qd, v0); v1 = fmaf_(s.Eb[c][1][k], qd, v1); v2 = fmaf_(s.Eb[c][2][k], qd, v2);
     }
-#pragma unroll
-    for (int a = 0; a < 3; ++a)
-#pragma unroll
-      for (int k = 0; k < kContactDofs; ++k) s.Eb[c][a][k] = E[a][k];
     const float dmax = MF::foot_solimp[1], tc = MF::foot_solref[0], dr = MF::foot_solref[1];
     const float bcoef = 2.f / (dmax * tc);
     const float kcoef = 1.f / (dmax * dmax * tc * tc * dr * dr);
