@@ -100,6 +100,20 @@ __device__ __forceinline__ float shr3_upper_quads(float x) {   // lanes 4..7 of 
   return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x113, 0xF, 0xA, false));
 }
 
+// Chain-to-chain moves at the factor's junctions (chains g on lanes 8g..8g+7 of the group): lane i
+// of a 16-lane row takes lane i + 8 (row_shl:8; the upper half of the row reads 0) or lane i - 8
+// (row_shr:8; the lower half reads 0), i.e. chain 1 -> 0 and 3 -> 2, or 0 -> 1 and 2 -> 3.
+__device__ __forceinline__ float from_next_chain(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x108, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float from_prev_chain(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x118, 0xF, 0xF, true));
+}
+// lanes 0..15 of each group take lanes 16..31 (chains 2, 3 -> 0, 1) by v_permlane16_swap
+__device__ __forceinline__ float from_upper_row(float v) {
+  return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
+}
+
 // A chain holds a spatial vector as (w0 w1 w2 v0 v1 v2) in lanes 0..5 of its aligned 8 lanes;
 // lane r < 6, k = r mod 3, gets w[(k+1) mod 3], w[(k+2) mod 3], v[(k+1) mod 3], v[(k+2) mod 3],
 // the operands of component k of a cross product (lanes 6, 7: unspecified). Lanes 0..3 permute

@@ -742,10 +742,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     // the right arm (chain 3, lanes 24..) ends at depth 5; its downdate and bias force join the
     // torso (chain 2) at depth 4
     static_assert(body_parent[24] == 16 && body_parent[17] == 16 && body_depth[24] == kTorsoDepth + 1, "torso");
-    float gD[6], gc[6];
+    float gD[6], gc[6];   // chain 3's rows on chain 2's lanes (row_shl:8)
 #pragma unroll
-    for (int j = 0; j < 6; ++j) { gD[j] = gshfl(Dlr[j], 24 + rowc); gc[j] = gshfl(cs[j], 24 + rowc); }
-    level(kTorsoDepth, grp == 2, gD, gc, gshfl(Fc, 24 + rowc));
+    for (int j = 0; j < 6; ++j) { gD[j] = from_next_chain(Dlr[j]); gc[j] = from_next_chain(cs[j]); }
+    level(kTorsoDepth, grp == 2, gD, gc, from_next_chain(Fc));
   }
 #pragma unroll
   for (int cd = kTorsoDepth - 1; cd >= 2; --cd) level(cd, false, none, none, 0.f);
@@ -756,8 +756,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   {
     // pelvis subtree force F_1 = F_own_1 + F_14 + F_8 + F_2 (descending children), component r
     // on lane r of chain 0, then the free joint's right-hand side -S_base.F_1 on lane 1
-    const float F1 = ((Fo[6 + rowc] + gshfl(Fc, 16 + rowc)) + gshfl(Fc, 8 + rowc)) + Fc;
-    const V3 Fw{gshfl(F1, 0), gshfl(F1, 1), gshfl(F1, 2)}, Fv{gshfl(F1, 3), gshfl(F1, 4), gshfl(F1, 5)};
+    // (chain 2's and chain 1's lanes reach chain 0's by v_permlane16_swap and row_shl:8)
+    const float F1 = ((Fo[6 + rowc] + from_upper_row(Fc)) + from_next_chain(Fc)) + Fc;
+    const V3 Fw{chain_bcast<0>(F1), chain_bcast<1>(F1), chain_bcast<2>(F1)};
+    const V3 Fv{chain_bcast<3>(F1), chain_bcast<4>(F1), chain_bcast<5>(F1)};
     if (base) {
       // x_base = 0 - S_base.F_1 (see sbase_dot): translation k takes Fv_k, rotation k R1 col k . Fw
       xb[0] = -Fv.x; xb[1] = -Fv.y; xb[2] = -Fv.z;
@@ -767,8 +769,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     float I1[6];
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
-      const float d14 = gshfl(Dlr[j], 16 + rowc), d8 = gshfl(Dlr[j], 8 + rowc);
-      const float c14 = gshfl(cs[j], 16 + rowc), c8 = gshfl(cs[j], 8 + rowc);
+      const float d14 = from_upper_row(Dlr[j]), d8 = from_next_chain(Dlr[j]);
+      const float c14 = from_upper_row(cs[j]), c8 = from_next_chain(cs[j]);
       I1[j] = ((I6[1 * 21 + symidx(rowc, j)] + d14) + d8) + Dlr[j];
       pAs[j] = (c14 + c8) + cs[j];
     }
@@ -891,7 +893,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       if (r == kTorsoDepth + 1) {
         float at[6];
 #pragma unroll
-        for (int k = 0; k < 6; ++k) at[k] = gshfl(a[k], 16 + crow);
+        for (int k = 0; k < 6; ++k) at[k] = from_prev_chain(a[k]);   // chain 2's lanes (row_shr:8)
         if (grp == 3) {
 #pragma unroll
           for (int k = 0; k < 6; ++k) a[k] = at[k];
