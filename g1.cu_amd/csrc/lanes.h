@@ -109,9 +109,13 @@ __device__ __forceinline__ float from_next_chain(float v) {
 __device__ __forceinline__ float from_prev_chain(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x118, 0xF, 0xF, true));
 }
-// lanes 0..15 of each group take lanes 16..31 (chains 2, 3 -> 0, 1) by v_permlane16_swap
+// lanes 0..15 of each group take lanes 16..31 (chains 2, 3 -> 0, 1), or lanes 16..31 take lanes
+// 0..15 (chains 0, 1 -> 2, 3), by v_permlane16_swap
 __device__ __forceinline__ float from_upper_row(float v) {
   return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
+}
+__device__ __forceinline__ float from_lower_row(float v) {
+  return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[0]);
 }
 
 // A chain holds a spatial vector as (w0 w1 w2 v0 v1 v2) in lanes 0..5 of its aligned 8 lanes;

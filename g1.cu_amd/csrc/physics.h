@@ -33,6 +33,7 @@ using namespace g1;
 using MF = ModelT<float>;
 
 constexpr int kCols = 1 + 3 * kNFoot;  // smooth column + 3 basis columns per contact
+constexpr int kChainSolveCon = 2;      // contacts per world up to which the M^-1 solves use the chain layout
 constexpr int kMmStride = 37;          // odd stride: column-parallel LDS reads are conflict-free
 constexpr int kPairs = kNFoot * (kNFoot + 1) / 2;
 
@@ -333,6 +334,38 @@ __device__ __forceinline__ void pgs_sweep(const float (&Acol)[kMaxEfc], float Ai
       pgs_sweep<II + 1, W>(Acol, Aii, yi, bi, l, nefc_max, fi);
     }
   }
+}
+
+// Free joint of one M^-1 solve column (reference: src/aba_factor.cuh:139-155): D qdd = x_b -
+// S_base.pA_1 with the factored D = L L' in LDS (forward, then backward substitution, each quotient
+// by div_rn), then the pelvis acceleration a1 = S_base qdd (see sbase_dot / sbase_col).
+__device__ __forceinline__ void base_solve(const WorldLds& s, const float (&xb)[6], const float (&p1)[6],
+                                           float (&qdd)[6], float (&a1)[6]) {
+  float rhs6[6];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) rhs6[k] = xb[k] - sbase_dot(k, s.u.fac.S[k], p1);
+  const float* Lf = s.u.fac.Dfac;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    float a = rhs6[i];
+#pragma unroll
+    for (int k = 0; k < i; ++k) a = fmaf_(-Lf[i * 6 + k], qdd[k], a);
+    qdd[i] = div_rn(a, Lf[i * 6 + i], s.u.fac.Dinv[i]);
+  }
+#pragma unroll
+  for (int i = 5; i >= 0; --i) {
+    float a = qdd[i];
+#pragma unroll
+    for (int k = i + 1; k < 6; ++k) a = fmaf_(-Lf[k * 6 + i], qdd[k], a);
+    qdd[i] = div_rn(a, Lf[i * 6 + i], s.u.fac.Dinv[i]);
+  }
+  float S3[3][3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+#pragma unroll
+    for (int i = 0; i < 3; ++i) S3[k][i] = s.u.fac.S[3 + k][i];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) a1[i] = sbase_col(i, S3, qdd);
 }
 
 // ================================================================ substep: qacc of one world
@@ -970,7 +1003,120 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // The traversal is unrolled over the static tree. Articulated bias forces travel as explicit
   // carries along each chain (arm chains end in the torso 16, leg and waist chains in the pelvis 1);
   // parents with several children accumulate them in the reference's descending-child order.
+  float xb0[6];   // the smooth right-hand side on the base dofs (lane 1 holds it)
   if (ncon_max > 0) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) xb0[k] = gshfl(xb[k], 1);
+  }
+  if (ncon_max > 0 && ncon_max <= kChainSolveCon) {
+    // Chain layout (waves with at most two contacts per world, at most seven columns): lane
+    // (g, c) = (l / 8, l mod 8) takes column c (0: smooth, 1 + 3 c' + a: basis row a of contact
+    // c'; c = 7 idle) on chain g of the factor's layout. The same operations per column and body
+    // as the lane-per-column form below, but the four chains walk in lock-step over depth: 6 + 10
+    // levels instead of 12 + 29 bodies in sequence.
+    const int col = l & 7;
+    const int cj = col >= 1 ? (col - 1) / 3 : 0, aj = col >= 1 ? (col - 1) % 3 : 0;
+    const bool basis = col >= 1 && col < 7 && cj < ncon;
+    const bool right = s.con_leg[cj] != 0;
+    const float* eb = s.Eb[cj][aj];
+    const bool smooth = col == 0;
+    const bool wr = col < 7;
+    // leaf -> root over the legs (the waist/arm subtree carries zero bias for the basis rows, as
+    // below): the lanes of chains 0 and 2 walk the left leg 7..2, those of 1 and 3 the right leg
+    // 13..8 (chains 2 and 3 repeat 0 and 1), body = depth + loff; operands read a level ahead
+    const int lc = grp & 1, loff = lc ? 6 : 0;
+    const bool own = basis && (lc ? right : !right);
+    float ul[6];                 // u of the lane's leg bodies at depth 2..7
+    float car[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    {
+      const float* const pS = &s.u.fac.S[loff + 4][0];
+      const float* const pU = &s.u.fac.U[loff][0];
+      const float* const pD = &s.u.fac.invD[loff];
+      float nS[6], nU[6], nD, nE;
+      auto ld = [&](int d) {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) { nS[k] = pS[6 * d + k]; nU[k] = pU[6 * d + k]; }
+        nD = pD[d];
+        nE = eb[7 - d];   // xrhs(d + loff + 4) before its select (both legs: entry 7 - d)
+      };
+      ld(7);
+#pragma unroll
+      for (int d = 7; d >= 2; --d) {
+        float Sd[6], Ud[6];
+#pragma unroll
+        for (int k = 0; k < 6; ++k) { Sd[k] = nS[k]; Ud[k] = nU[k]; }
+        const float iD = nD, e = nE;
+        if (d > 2) ld(d - 1);
+        float pb[6];   // the leaf (7, 13) has no child
+#pragma unroll
+        for (int k = 0; k < 6; ++k) pb[k] = d == 7 ? 0.f : car[k];
+        const float ub = (own ? e : 0.f) - dot6(Sd, pb);
+        ul[d - 2] = ub;
+        const float ud = ub * iD;
+#pragma unroll
+        for (int k = 0; k < 6; ++k) car[k] = fmaf_(Ud[k], ud, pb[k]);
+      }
+    }
+    // pelvis: p1 = c8 + c2 (the right leg's root first) on chain 0's lanes, then to every chain
+    float p1[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const float c8 = from_next_chain(car[k]);
+      float v = smooth ? pAs[k] : c8 + car[k];
+      const float v1 = from_prev_chain(v);           // chain 0 -> 1
+      v = grp == 1 ? v1 : v;
+      const float v2 = from_lower_row(v);            // chains 0, 1 -> 2, 3
+      p1[k] = grp >= 2 ? v2 : v;
+    }
+    float qdd[6], a1[6], xbj[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) xbj[k] = smooth ? xb0[k] : (basis ? eb[6 + k] : 0.f);
+    base_solve(s, xbj, p1, qdd, a1);
+    float* const ycol = s.Mm[wr ? col : 0];
+    if (grp == 0 && wr) {
+#pragma unroll
+      for (int k = 0; k < 6; ++k) ycol[k] = qdd[k];
+    }
+    // root -> leaf, the chains in lock-step: legs and waist from the pelvis at depth 2, the right
+    // arm from the torso (chain 2's depth-4 result) at depth 5
+    {
+      const float* const pS = &s.u.fac.S[c_off + 4][0];
+      const float* const pU = &s.u.fac.U[c_off][0];
+      const float* const pD = &s.u.fac.invD[c_off];
+      const float* const pUs = &s.u.fac.us[c_off];
+      float nS[6], nU[6], nD, nUs;
+      auto ld = [&](int d) {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) { nS[k] = pS[6 * d + k]; nU[k] = pU[6 * d + k]; }
+        nD = pD[d];
+        nUs = pUs[d];
+      };
+      ld(2);
+      float ac[6];
+#pragma unroll
+      for (int k = 0; k < 6; ++k) ac[k] = a1[k];
+#pragma unroll
+      for (int d = 2; d <= kMaxDepth; ++d) {
+        if (d == kTorsoDepth + 1) {
+#pragma unroll
+          for (int k = 0; k < 6; ++k) {
+            const float at = from_prev_chain(ac[k]);   // chain 2 -> 3
+            ac[k] = grp == 3 ? at : ac[k];
+          }
+        }
+        float Sd[6], Ud[6];
+#pragma unroll
+        for (int k = 0; k < 6; ++k) { Sd[k] = nS[k]; Ud[k] = nU[k]; }
+        const float iD = nD, us = nUs;
+        if (d < kMaxDepth) ld(d + 1);
+        const float ub = smooth ? us : ((grp <= 1 && d <= 7) ? ul[d <= 7 ? d - 2 : 0] : 0.f);
+        const float q = (ub - dot6(Ud, ac)) * iD;
+        if (wr && d >= c_lo && d <= c_hi) ycol[chain_body(d) + 4] = q;
+#pragma unroll
+        for (int k = 0; k < 6; ++k) ac[k] = fmaf_(Sd[k], q, ac[k]);
+      }
+    }
+  } else if (ncon_max > 0) {
     const int j = l;
     const int cj = (j >= 1 && j < kCols) ? (j - 1) / 3 : 0, aj = (j >= 1) ? (j - 1) % 3 : 0;
     const bool basis = (j >= 1) && (j < kCols) && (cj < ncon);
@@ -1036,43 +1182,13 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const bool smooth = j == 0;
 #pragma unroll
     for (int k = 0; k < 6; ++k) p1[k] = smooth ? pAs[k] : c8[k] + c2[k];
-    float xb0[6];   // the smooth right-hand side on the base dofs (lane 1 holds it)
-#pragma unroll
-    for (int k = 0; k < 6; ++k) xb0[k] = gshfl(xb[k], 1);
     // free joint: D qdd = x_base - S_base.pA_1 with D = L L'
-    float qdd[6];
-    {
-      float rhs6[6];
+    float qdd[6], a1[6], xbj[6];
 #pragma unroll
-      for (int k = 0; k < 6; ++k) rhs6[k] = (smooth ? xb0[k] : xrhs(k)) - sbase_dot(k, s.u.fac.S[k], p1);
-      const float* Lf = s.u.fac.Dfac;
-#pragma unroll
-      for (int i = 0; i < 6; ++i) {
-        float a = rhs6[i];
-#pragma unroll
-        for (int k = 0; k < i; ++k) a = fmaf_(-Lf[i * 6 + k], qdd[k], a);
-        qdd[i] = div_rn(a, Lf[i * 6 + i], s.u.fac.Dinv[i]);
-      }
-#pragma unroll
-      for (int i = 5; i >= 0; --i) {
-        float a = qdd[i];
-#pragma unroll
-        for (int k = i + 1; k < 6; ++k) a = fmaf_(-Lf[k * 6 + i], qdd[k], a);
-        qdd[i] = div_rn(a, Lf[i * 6 + i], s.u.fac.Dinv[i]);
-      }
-    }
+    for (int k = 0; k < 6; ++k) xbj[k] = smooth ? xb0[k] : xrhs(k);
+    base_solve(s, xbj, p1, qdd, a1);
     float* ycol = s.Mm[j < kCols ? j : kCols - 1];
     const bool wr = j < kCols;
-    float a1[6];
-    {
-      float S3[3][3];
-#pragma unroll
-      for (int k = 0; k < 3; ++k)
-#pragma unroll
-        for (int i = 0; i < 3; ++i) S3[k][i] = s.u.fac.S[3 + k][i];
-#pragma unroll
-      for (int i = 0; i < 6; ++i) a1[i] = sbase_col(i, S3, qdd);
-    }
     if (wr) {
 #pragma unroll
       for (int k = 0; k < 6; ++k) ycol[k] = qdd[k];
