@@ -534,6 +534,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // the index linear in cd lets every per-level LDS address be a loop-invariant register plus an
   // immediate offset.
   auto chain_body = [&](int cd) { return cd + c_off; };
+  constexpr int kTorsoDepth = body_depth[16];   // the arms' parent, the waist chain's last body
   static_assert(kMaxDepth + 19 < kNBody, "chain bodies in range");
   static_assert(body_parent[2] == 1 && body_parent[8] == 1 && body_parent[14] == 1 && body_parent[24] == 16 &&
                 body_depth[24] == 5 && body_depth[2] == 2, "chain roots");
@@ -572,18 +573,20 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const bool act = r >= c_lo && r <= c_hi;
       const float Sr = nS[0], Sw1 = nS[1], Sw2 = nS[2], Sv1 = nS[3], Sv2 = nS[4], qd = nq;
       if (r < kMaxDepth) ld(r + 1);
-      // parent's components: the chain's previous level, or from LDS at a chain's first body
+      // parent's components: the chain's previous level; the right arm's first body takes the
+      // torso from chain 2's lanes (row_shr:8), the other chains' first bodies the pelvis from LDS
+      if (r == kTorsoDepth + 1) {
+        const float tp = from_prev_chain(pc), ta = from_prev_chain(pac);
+        pc = grp == 3 ? tp : pc;
+        pac = grp == 3 ? ta : pac;
+      }
       float X1, X2, Y1, Y2;   // w_p[k+1], w_p[k+2], v_p[k+1], v_p[k+2]
       chain_rot3(pc, X1, X2, Y1, Y2);
       float P = pc, PA = pac;
-      if (r == 2 || r == 5) {
-        const bool start = (r == c_lo);
-        const int pb = grp == 3 ? 16 : 1;
-        const float* pv6 = V6 + 6 * pb;
-        if (start) {
-          X1 = pv6[k1]; X2 = pv6[k2]; Y1 = pv6[3 + k1]; Y2 = pv6[3 + k2];
-          P = pv6[rowc]; PA = A6[6 * pb + rowc];
-        }
+      if (r == 2 && r == c_lo) {
+        const float* pv6 = V6 + 6;
+        X1 = pv6[k1]; X2 = pv6[k2]; Y1 = pv6[3 + k1]; Y2 = pv6[3 + k2];
+        P = pv6[rowc]; PA = A6[6 + rowc];
       }
       const float vn = fmaf_(Sr, qd, P);
       const float t1 = fmaf_(-X2, Sw1, X1 * Sw2);   // (w_p x s_w)_k, or (w_p x s_v)_k
@@ -595,7 +598,6 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       pc = vn;
       pac = an;
       if (act && crow < 6) { pV[6 * r] = pc; pA[6 * r] = pac; }
-      if (r == 4) __syncthreads();   // the torso (depth 4) is in LDS before the right arm starts
     }
   }
   __syncthreads();
@@ -768,7 +770,6 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   __builtin_amdgcn_s_setprio(1);
   prefetch(kMaxDepth);
   const float none[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  constexpr int kTorsoDepth = body_depth[16];
 #pragma unroll
   for (int cd = kMaxDepth; cd > kTorsoDepth; --cd) level(cd, false, none, none, 0.f);
   {
