@@ -1241,50 +1241,82 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   }
 
   // ---------------- Gram blocks + b (reference: src/env_qacc.cuh:154-192); G aliases the factor
-  float bb0 = 0.f, bb1 = 0.f, bb2 = 0.f;
-  if (l < ncon) {
-    const int legbase = s.con_leg[l] ? 12 : 6;
+  // Block row c of column j: g_a = e_{c,a} . m_j over contact c's 12 ancestor dofs (dof
+  // legbase + 5 - k on the leg, legbase 6 left, 12 right; k - 6 on the base), and b_c from the same
+  // products with the smooth column (j = 0).
+  if (ncon_max <= kChainSolveCon) {
+    // lane (c, j) = (l / 8, l mod 8): one block row per lane (contact c <= 1, column j <= 6); the
+    // lanes of column 0 form b of their contact
+    const int c = l >> 3, j = l & 7;
+    const int cp = j >= 1 ? (j - 1) / 3 : 0, bcol = j >= 1 ? (j - 1) % 3 : 0;
+    const bool blk = j >= 1 && j < 7 && cp < ncon && c <= cp;
+    const bool bvc = j == 0 && c < ncon;
+    const int cc = c < kChainSolveCon ? c : 0;
+    const float* mcol = s.Mm[j < 7 ? j : 0];
+    const bool rightleg = s.con_leg[cc] != 0;
+    float g0 = 0.f, g1 = 0.f, g2 = 0.f;
 #pragma unroll
     for (int k = 0; k < kContactDofs; ++k) {
-      const int a = (k < 6) ? legbase + 5 - k : k - 6;
-      const float qa = s.Mm[0][a];
-      bb0 = fmaf_(s.Eb[l][0][k], qa, bb0); bb1 = fmaf_(s.Eb[l][1][k], qa, bb1); bb2 = fmaf_(s.Eb[l][2][k], qa, bb2);
+      const float mv = (k < 6) ? (rightleg ? mcol[17 - k] : mcol[11 - k]) : mcol[k - 6];
+      g0 = fmaf_(s.Eb[cc][0][k], mv, g0); g1 = fmaf_(s.Eb[cc][1][k], mv, g1); g2 = fmaf_(s.Eb[cc][2][k], mv, g2);
     }
-  }
-  __syncthreads();   // factor region is dead from here on: the Gram blocks overwrite it
-  {
-    const int j = l;
-    const int cp = (j >= 1) ? (j - 1) / 3 : 0, bcol = (j >= 1) ? (j - 1) % 3 : 0;
-    const bool active = (j >= 1) && (cp < ncon);
-    // the lane's solve column on the base and both legs' dofs (0..17), read once for all c
-    float mj[18];
-    const float* mcol = s.Mm[active ? j : 0];
+    if (blk) {
+      const int pr = cp * (cp + 1) / 2 + c;
+      s.u.G[pr][0 * 3 + bcol] = g0; s.u.G[pr][1 * 3 + bcol] = g1; s.u.G[pr][2 * 3 + bcol] = g2;
+    }
+    if (bvc) {
+      s.bvec[4 * c + 0] = fmaf_(0.f, g2, fmaf_(1.f, g1, 1.f * g0)) - s.aref[4 * c + 0];
+      s.bvec[4 * c + 1] = fmaf_(0.f, g2, fmaf_(-1.f, g1, 1.f * g0)) - s.aref[4 * c + 1];
+      s.bvec[4 * c + 2] = fmaf_(1.f, g2, fmaf_(0.f, g1, 1.f * g0)) - s.aref[4 * c + 2];
+      s.bvec[4 * c + 3] = fmaf_(-1.f, g2, fmaf_(0.f, g1, 1.f * g0)) - s.aref[4 * c + 3];
+    }
+    __syncthreads();
+  } else {
+    float bb0 = 0.f, bb1 = 0.f, bb2 = 0.f;
+    if (l < ncon) {
+      const int legbase = s.con_leg[l] ? 12 : 6;
 #pragma unroll
-    for (int a = 0; a < 18; ++a) mj[a] = mcol[a];
-#pragma unroll
-    for (int c = 0; c < kNFoot; ++c) {
-      if (c >= ncon_max) break;
-      if (active && c <= cp) {
-        const bool rightleg = s.con_leg[c] != 0;
-        float g0 = 0.f, g1 = 0.f, g2 = 0.f;
-#pragma unroll
-        for (int k = 0; k < kContactDofs; ++k) {
-          // dof a = legbase + 5 - k on the leg (legbase 6 left, 12 right), k - 6 on the base
-          const float mv = (k < 6) ? (rightleg ? mj[17 - k] : mj[11 - k]) : mj[k - 6];
-          g0 = fmaf_(s.Eb[c][0][k], mv, g0); g1 = fmaf_(s.Eb[c][1][k], mv, g1); g2 = fmaf_(s.Eb[c][2][k], mv, g2);
-        }
-        const int pr = cp * (cp + 1) / 2 + c;
-        s.u.G[pr][0 * 3 + bcol] = g0; s.u.G[pr][1 * 3 + bcol] = g1; s.u.G[pr][2 * 3 + bcol] = g2;
+      for (int k = 0; k < kContactDofs; ++k) {
+        const int a = (k < 6) ? legbase + 5 - k : k - 6;
+        const float qa = s.Mm[0][a];
+        bb0 = fmaf_(s.Eb[l][0][k], qa, bb0); bb1 = fmaf_(s.Eb[l][1][k], qa, bb1); bb2 = fmaf_(s.Eb[l][2][k], qa, bb2);
       }
     }
+    __syncthreads();   // factor region is dead from here on: the Gram blocks overwrite it
+    {
+      const int j = l;
+      const int cp = (j >= 1) ? (j - 1) / 3 : 0, bcol = (j >= 1) ? (j - 1) % 3 : 0;
+      const bool active = (j >= 1) && (cp < ncon);
+      // the lane's solve column on the base and both legs' dofs (0..17), read once for all c
+      float mj[18];
+      const float* mcol = s.Mm[active ? j : 0];
+#pragma unroll
+      for (int a = 0; a < 18; ++a) mj[a] = mcol[a];
+#pragma unroll
+      for (int c = 0; c < kNFoot; ++c) {
+        if (c >= ncon_max) break;
+        if (active && c <= cp) {
+          const bool rightleg = s.con_leg[c] != 0;
+          float g0 = 0.f, g1 = 0.f, g2 = 0.f;
+#pragma unroll
+          for (int k = 0; k < kContactDofs; ++k) {
+            // dof a = legbase + 5 - k on the leg (legbase 6 left, 12 right), k - 6 on the base
+            const float mv = (k < 6) ? (rightleg ? mj[17 - k] : mj[11 - k]) : mj[k - 6];
+            g0 = fmaf_(s.Eb[c][0][k], mv, g0); g1 = fmaf_(s.Eb[c][1][k], mv, g1); g2 = fmaf_(s.Eb[c][2][k], mv, g2);
+          }
+          const int pr = cp * (cp + 1) / 2 + c;
+          s.u.G[pr][0 * 3 + bcol] = g0; s.u.G[pr][1 * 3 + bcol] = g1; s.u.G[pr][2 * 3 + bcol] = g2;
+        }
+      }
+    }
+    if (l < ncon) {
+      s.bvec[4 * l + 0] = fmaf_(0.f, bb2, fmaf_(1.f, bb1, 1.f * bb0)) - s.aref[4 * l + 0];
+      s.bvec[4 * l + 1] = fmaf_(0.f, bb2, fmaf_(-1.f, bb1, 1.f * bb0)) - s.aref[4 * l + 1];
+      s.bvec[4 * l + 2] = fmaf_(1.f, bb2, fmaf_(0.f, bb1, 1.f * bb0)) - s.aref[4 * l + 2];
+      s.bvec[4 * l + 3] = fmaf_(-1.f, bb2, fmaf_(0.f, bb1, 1.f * bb0)) - s.aref[4 * l + 3];
+    }
+    __syncthreads();
   }
-  if (l < ncon) {
-    s.bvec[4 * l + 0] = fmaf_(0.f, bb2, fmaf_(1.f, bb1, 1.f * bb0)) - s.aref[4 * l + 0];
-    s.bvec[4 * l + 1] = fmaf_(0.f, bb2, fmaf_(-1.f, bb1, 1.f * bb0)) - s.aref[4 * l + 1];
-    s.bvec[4 * l + 2] = fmaf_(1.f, bb2, fmaf_(0.f, bb1, 1.f * bb0)) - s.aref[4 * l + 2];
-    s.bvec[4 * l + 3] = fmaf_(-1.f, bb2, fmaf_(0.f, bb1, 1.f * bb0)) - s.aref[4 * l + 3];
-  }
-  __syncthreads();
 
   // ---------------- A column of row-lane i (reference: src/env_qacc.cuh:154-190); pyramid
   // directions d0=(1,1,0) d1=(1,-1,0) d2=(1,0,1) d3=(1,0,-1). For a pair c < c' the reference
