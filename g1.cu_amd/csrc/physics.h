@@ -368,6 +368,20 @@ __device__ __forceinline__ void base_solve(const WorldLds& s, const float (&xb)[
   for (int i = 0; i < 6; ++i) a1[i] = sbase_col(i, S3, qdd);
 }
 
+// Ordering point between the phases of world_qacc, whose callers run it in workgroups of one wave
+// (k_physics, k_rollout, k_probe: 64 threads). A wave's LDS accesses are performed in program
+// order, so a wavefront-scope fence (the compiler keeps the accesses in order; no instruction) is
+// all a hand-over through LDS between its lanes needs; __syncthreads() adds an lgkmcnt(0) drain of
+// every outstanding LDS access at each phase boundary. The translation unit of k_rollout
+// (compiled with the ILP-first scheduler) defines G1_PHASE_FENCE and takes the fence: config 3
+// 10.50 -> 10.43 ms; k_physics keeps the barrier, with which its schedule is faster (config 4
+// 194.4 -> 193.3 ms).
+#ifdef G1_PHASE_FENCE
+__device__ __forceinline__ void wave_sync() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
+#else
+__device__ __forceinline__ void wave_sync() { __syncthreads(); }
+#endif
+
 // ================================================================ substep: qacc of one world
 // Inputs: lane state, PD torque of the lane's hinge dof (jtau). Output: qacc of the lane's dofs
 // (lane 1: 6 base dofs into bqacc[], hinge lanes: jqacc). Returns this world's contact count.
@@ -545,7 +559,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     V6[6 + 0] = vw.x; V6[6 + 1] = vw.y; V6[6 + 2] = vw.z; V6[6 + 3] = vv.x; V6[6 + 4] = vv.y; V6[6 + 5] = vv.z;
     A6[6 + 0] = aw.x; A6[6 + 1] = aw.y; A6[6 + 2] = aw.z; A6[6 + 3] = av.x; A6[6 + 4] = av.y; A6[6 + 5] = av.z;
   }
-  __syncthreads();   // pelvis velocity / acceleration and every motion axis and hinge qvel in LDS
+  wave_sync();   // pelvis velocity / acceleration and every motion axis and hinge qvel in LDS
   {
     const int k = rowc < 3 ? rowc : rowc - 3, k1 = k == 2 ? 0 : k + 1, k2 = k == 0 ? 2 : k - 1;
     const bool isv = rowc >= 3;
@@ -600,7 +614,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       if (act && crow < 6) { pV[6 * r] = pc; pA[6 * r] = pac; }
     }
   }
-  __syncthreads();
+  wave_sync();
   if (L.hinge) {
     const float* v6 = V6 + 6 * L.b;
     const float* a6 = A6 + 6 * L.b;
@@ -668,7 +682,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       for (int j = i; j < 6; ++j) I6[L.b * 21 + symidx(i, j)] = M6[i * 6 + j];
   }
   const float S6[6] = {sw.x, sw.y, sw.z, sv.x, sv.y, sv.z};
-  __syncthreads();   // S, I6 and the own forces of every body in LDS
+  wave_sync();   // S, I6 and the own forces of every body in LDS
 
   // ---------------- damped articulated-inertia factor, chain-parallel (reference:
   // src/aba_factor.cuh:77-88), fused with the leaf -> root sweep of the smooth solve
@@ -818,7 +832,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // ---------------- free-joint 6x6 block (reference: src/aba_factor.cuh:90-108): lane c < 6
   // builds column c of U6 = I^A S_base and of D = S_base' U6; lane 1 factors D and solves the
   // base of the smooth system.
-  __syncthreads();   // I^A of the pelvis and the hinge factor complete in LDS
+  wave_sync();   // I^A of the pelvis and the hinge factor complete in LDS
   if (l < 6) {
     // column l of U6 = I^A S_base: translation l < 3 picks column 3 + l of I^A, rotation l >= 3
     // is I^A's angular columns times R1 col (l - 3) (structural zeros skipped, see sbase_dot).
@@ -845,7 +859,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
     for (int k = 0; k < 6; ++k) s.u.fac.Dm[k * 6 + l] = sbase_dot(k, S3[k < 3 ? 0 : k - 3], U6c);
   }
-  __syncthreads();
+  wave_sync();
   float a6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (base) {
     float Dm[36], Dinv[6];
@@ -972,7 +986,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       if (on) { s.Eb[c][0][k] = jc.z; s.Eb[c][1][k] = mu * jc.y; s.Eb[c][2][k] = -mu * jc.x; }
     }
   }
-  __syncthreads();   // the basis rows in LDS
+  wave_sync();   // the basis rows in LDS
   if (ncon_max > 0 && l < ncon) {
     const int c = l;
     const int legbase = s.con_leg[c] ? 12 : 6;
@@ -995,7 +1009,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     s.aref[4 * c + 2] = -bcoef * (v0 + v2) - kip;
     s.aref[4 * c + 3] = -bcoef * (v0 - v2) - kip;
   }
-  __syncthreads();
+  wave_sync();
 
   // ---------------- PASS 2: M^-1 solves, lane j = basis column j (reference: src/aba_factor.cuh:121-165,
   // src/env_qacc.cuh:137-152). Lane 0 finishes column 0, the smooth solve: its leaf -> root part
@@ -1227,7 +1241,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       if (i + 1 < 29) dc = dn;
     }
   }
-  __syncthreads();
+  wave_sync();
 
   if (ncon_max == 0) {
     if (base) {
@@ -1236,7 +1250,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     }
     jqacc = L.hinge ? s.Mm[0][L.b + 4] : 0.f;
     __builtin_amdgcn_s_setprio(0);
-    __syncthreads();
+    wave_sync();
     return ncon;
   }
 
@@ -1270,7 +1284,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       s.bvec[4 * c + 2] = fmaf_(1.f, g2, fmaf_(0.f, g1, 1.f * g0)) - s.aref[4 * c + 2];
       s.bvec[4 * c + 3] = fmaf_(-1.f, g2, fmaf_(0.f, g1, 1.f * g0)) - s.aref[4 * c + 3];
     }
-    __syncthreads();
+    wave_sync();
   } else {
     float bb0 = 0.f, bb1 = 0.f, bb2 = 0.f;
     if (l < ncon) {
@@ -1282,7 +1296,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         bb0 = fmaf_(s.Eb[l][0][k], qa, bb0); bb1 = fmaf_(s.Eb[l][1][k], qa, bb1); bb2 = fmaf_(s.Eb[l][2][k], qa, bb2);
       }
     }
-    __syncthreads();   // factor region is dead from here on: the Gram blocks overwrite it
+    wave_sync();   // factor region is dead from here on: the Gram blocks overwrite it
     {
       const int j = l;
       const int cp = (j >= 1) ? (j - 1) / 3 : 0, bcol = (j >= 1) ? (j - 1) % 3 : 0;
@@ -1315,7 +1329,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       s.bvec[4 * l + 2] = fmaf_(1.f, bb2, fmaf_(0.f, bb1, 1.f * bb0)) - s.aref[4 * l + 2];
       s.bvec[4 * l + 3] = fmaf_(-1.f, bb2, fmaf_(0.f, bb1, 1.f * bb0)) - s.aref[4 * l + 3];
     }
-    __syncthreads();
+    wave_sync();
   }
 
   // ---------------- A column of row-lane i (reference: src/env_qacc.cuh:154-190); pyramid
@@ -1381,7 +1395,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   }
   __builtin_amdgcn_s_setprio(0);
   if (row) s.f[l] = fi;
-  __syncthreads();
+  wave_sync();
 
   // ---------------- qacc = qacc_smooth + sum_c sum_a fb_c[a] m_{c,a} (reference: src/env_qacc.cuh:196-211)
   // lane l: dof l and (lanes 0..2) dof 32 + l, both accumulated in one pass over the contacts
@@ -1402,13 +1416,13 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     s.qacc[d1] = s.Mm[0][d1] + dq1;
     if (kGroup + l < kNV) s.qacc[d2] = s.Mm[0][d2] + dq2;
   }
-  __syncthreads();
+  wave_sync();
   if (base) {
 #pragma unroll
     for (int k = 0; k < 6; ++k) bqacc[k] = s.qacc[k];
   }
   jqacc = L.hinge ? s.qacc[L.b + 4] : 0.f;
-  __syncthreads();
+  wave_sync();
   return ncon;
 }
 

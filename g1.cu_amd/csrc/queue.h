@@ -40,6 +40,7 @@ struct PhysArgs {
 };
 
 constexpr int kPhysThreads = 64;   // one wave64 = two 32-lane world groups
+static_assert(kPhysThreads == 64, "world_qacc orders its LDS hand-overs with wave_sync(): one wave per block");
 constexpr int kXcds = 8;           // XCDs of the MI355X
 constexpr int kQueues = 32;        // work queues, kQueues / kXcds per XCD (spreads the claim atomics)
 constexpr unsigned kSpinLimit = 1u << 22;

@@ -3,6 +3,7 @@
 // scheduler: measured faster for this kernel, slower for k_physics and k_policy.
 #include <hip/hip_runtime.h>
 
+#define G1_PHASE_FENCE   // world_qacc's phase boundaries as wavefront fences (see wave_sync)
 #include "queue.h"
 
 namespace g1k {
