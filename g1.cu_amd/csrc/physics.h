@@ -1383,15 +1383,30 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // ---------------- projected Gauss-Seidel (reference: src/contact.cuh:159-171), P.pgs sweeps
   float fi = 0.f;
   const float yi = rcp_rn(Aii);
+  // A sweep that leaves every f of the wave bit-for-bit unchanged is a fixed point: every later
+  // sweep would repeat it exactly, so the sweeps stop there with the same result.
+  auto moved = [&](float f0) { return __ballot(__float_as_uint(fi) != __float_as_uint(f0)) != 0ull; };
   if (nefc_max <= 4) {
 #pragma unroll 1
-    for (int it = 0; it < P.pgs; ++it) pgs_sweep<0, 4>(Acol, Aii, yi, bi, l, nefc_max, fi);
+    for (int it = 0; it < P.pgs; ++it) {
+      const float f0 = fi;
+      pgs_sweep<0, 4>(Acol, Aii, yi, bi, l, nefc_max, fi);
+      if (!moved(f0)) break;
+    }
   } else if (nefc_max <= kGroup / 2) {
 #pragma unroll 1
-    for (int it = 0; it < P.pgs; ++it) pgs_sweep<0, kGroup / 2>(Acol, Aii, yi, bi, l, nefc_max, fi);
+    for (int it = 0; it < P.pgs; ++it) {
+      const float f0 = fi;
+      pgs_sweep<0, kGroup / 2>(Acol, Aii, yi, bi, l, nefc_max, fi);
+      if (!moved(f0)) break;
+    }
   } else {
 #pragma unroll 1
-    for (int it = 0; it < P.pgs; ++it) pgs_sweep<0, kMaxEfc>(Acol, Aii, yi, bi, l, nefc_max, fi);
+    for (int it = 0; it < P.pgs; ++it) {
+      const float f0 = fi;
+      pgs_sweep<0, kMaxEfc>(Acol, Aii, yi, bi, l, nefc_max, fi);
+      if (!moved(f0)) break;
+    }
   }
   __builtin_amdgcn_s_setprio(0);
   if (row) s.f[l] = fi;
