@@ -464,6 +464,13 @@ __global__ void k_divide(const float* a, const float* b, float* rcp, float* quot
   quot[i] = div_rn(a[i], b[i], y);
 }
 
+// sqrt_rn_pos of the physics kernel (the Cholesky pivots) on caller-given arguments (parity probe)
+__global__ void k_sqrt(const float* x, float* out, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = sqrt_rn_pos(x[i]);
+}
+
 // sincos_small_rn of the physics kernel on caller-given arguments (parity probe)
 __global__ void k_sincos(const float* x, float* sn, float* cs, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1188,6 +1195,12 @@ int g1_probe_policy(int n, int nlayers, const int* hidden, int activation, const
 void g1_probe_divide(int n, const float* a, const float* b, float* rcp, float* quot) {
   if (n <= 0) return;
   hipLaunchKernelGGL(k_divide, dim3((n + 255) / 256), dim3(256), 0, 0, a, b, rcp, quot, n);
+  HIPCHECK(hipGetLastError());
+}
+
+void g1_probe_sqrt(int n, const float* x, float* out) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_sqrt, dim3((n + 255) / 256), dim3(256), 0, 0, x, out, n);
   HIPCHECK(hipGetLastError());
 }
 

@@ -146,6 +146,18 @@ __device__ __forceinline__ float div_rn(float a, float b, float yb) {
   return __builtin_fmaf(__builtin_fmaf(-q0, b, a), yb, q0);
 }
 __device__ __forceinline__ float rsqrt_rn(float x) { return rcp_rn(sqrtf(x)); }
+// Correctly rounded square root of x >= 2^-96 (and of +0, +inf): the hardware root s is within
+// one ulp, and the residuals x - s_dn s and x - s_up s of its neighbours select RN(sqrt x). The
+// compiler's sqrtf makes the same selection after scaling arguments below 2^-96 and routing 0,
+// inf and NaN around it; the Cholesky pivots (Schur complements of the free joint's articulated
+// inertia, of the order of the robot's mass and inertia) need neither. Checked bit-exact against
+// the IEEE square root for every float from 2^-96 up, +0 and +inf.
+__device__ __forceinline__ float sqrt_rn_pos(float x) {
+  const float s = __builtin_amdgcn_sqrtf(x);
+  const float sd = __int_as_float(__float_as_int(s) - 1), su = __int_as_float(__float_as_int(s) + 1);
+  const float r = __builtin_fmaf(-sd, s, x) <= 0.f ? sd : s;
+  return __builtin_fmaf(-su, s, x) > 0.f ? su : r;
+}
 
 __device__ __forceinline__ Q4 qnorm(Q4 q) {
   float n = rsqrt_rn(fmaf_(q.z, q.z, fmaf_(q.y, q.y, fmaf_(q.x, q.x, q.w * q.w))));
@@ -873,7 +885,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
         for (int k = 0; k < j; ++k) a = fmaf_(-Dm[i * 6 + k], Dm[j * 6 + k], a);
         if (i == j) {
-          Dm[i * 6 + i] = sqrtf(a);
+          Dm[i * 6 + i] = sqrt_rn_pos(a);
           Dinv[i] = rcp_rn(Dm[i * 6 + i]);
         } else {
           Dm[i * 6 + j] = div_rn(a, Dm[j * 6 + j], Dinv[j]);

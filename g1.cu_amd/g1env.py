@@ -60,6 +60,7 @@ SIGNATURES = {
     "g1_probe_policy": (_c.c_int, [_c.c_int, _c.c_int, _ip, _c.c_int, _vp, _vp, _vp, _vp]),
     "g1_dynamics_bench": (None, [_c.c_int, _vp, _vp, _vp] + [_c.c_int] * 5 + [_c.c_float, _vp, _vp]),
     "g1_probe_divide": (None, [_c.c_int, _vp, _vp, _vp, _vp]),
+    "g1_probe_sqrt": (None, [_c.c_int, _vp, _vp]),
     "g1_probe_sincos": (None, [_c.c_int, _vp, _vp, _vp]),
     "g1_probe_philox": (None, [_c.c_int, _vp, _vp, _c.c_uint, _c.c_uint]),
 }

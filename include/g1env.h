@@ -151,6 +151,10 @@ void g1_dynamics_bench(int n, float* qpos, float* qvel, const float* tau, int ns
  * quot[i] = a[i]/b[i] (both correctly rounded for positive normal b). */
 void g1_probe_divide(int n, const float* a, const float* b, float* rcp, float* quot);
 
+/* The physics kernel's square root of the Cholesky pivots on n DEVICE arguments: out[i] =
+ * sqrt(x[i]) correctly rounded for x[i] >= 2^-96, +0 and +inf. */
+void g1_probe_sqrt(int n, const float* x, float* out);
+
 /* The physics kernel's sine/cosine of the free joint's half rotation angle on n DEVICE arguments:
  * sn[i] = sin(x[i]), cs[i] = cos(x[i]) rounded to float. */
 void g1_probe_sincos(int n, const float* x, float* sn, float* cs);

@@ -273,6 +273,27 @@ def test_reciprocal_and_quotient_are_ieee(g1):
         assert np.array_equal(q.view(np.uint32), (a / bs).view(np.uint32))
 
 
+def test_pivot_sqrt_exhaustive(g1):
+    """The Cholesky pivots' short square root against the IEEE one (numpy rounds float32 sqrt
+    correctly) for EVERY float from 2^-96 up to the largest finite, plus +0 and +inf; inputs are
+    generated on the device, 2^25 bit patterns per launch."""
+    import torch
+    lo = int(np.float32(2.0 ** -96).view(np.uint32))
+    hi = int(np.float32(np.inf).view(np.uint32))
+    chunk = 1 << 25
+    for start in range(lo, hi + 1, chunk):
+        stop = min(start + chunk, hi + 1)
+        dx = torch.arange(start, stop, dtype=torch.int32, device="cuda").view(torch.float32)
+        out = torch.empty_like(dx)
+        g1.lib.g1_probe_sqrt(dx.numel(), g1.dev_ptr(dx), g1.dev_ptr(out))
+        want = np.sqrt(np.arange(start, stop, dtype=np.uint32).view(np.float32))
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32)), hex(start)
+    z = torch.zeros(64, device="cuda")
+    out = torch.full_like(z, 1.0)
+    g1.lib.g1_probe_sqrt(z.numel(), g1.dev_ptr(z), g1.dev_ptr(out))
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), np.zeros(64, np.uint32))
+
+
 def test_small_angle_sincos_exhaustive(g1, orc):
     """The free joint's quaternion update takes sin/cos of the half rotation per substep on a short
     fp64 path for |x| <= 1/8: bit-identical to the oracle's fp64 libm rounded once for EVERY float
