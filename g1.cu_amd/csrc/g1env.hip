@@ -481,6 +481,16 @@ __global__ void k_sincos(const float* x, float* sn, float* cs, int n) {
   cs[i] = c;
 }
 
+// sincos_hinge_rn of the physics kernel (the FK's hinge half-angles) on caller-given arguments
+__global__ void k_sincos_hinge(const float* x, float* sn, float* cs, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s, c;
+  sincos_hinge_rn(x[i], s, c);
+  sn[i] = s;
+  cs[i] = c;
+}
+
 // ====================================================================== host side
 struct EnvState {
   int N, S, pgs;
@@ -1207,6 +1217,12 @@ void g1_probe_sqrt(int n, const float* x, float* out) {
 void g1_probe_sincos(int n, const float* x, float* sn, float* cs) {
   if (n <= 0) return;
   hipLaunchKernelGGL(k_sincos, dim3((n + 255) / 256), dim3(256), 0, 0, x, sn, cs, n);
+  HIPCHECK(hipGetLastError());
+}
+
+void g1_probe_sincos_hinge(int n, const float* x, float* sn, float* cs) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_sincos_hinge, dim3((n + 255) / 256), dim3(256), 0, 0, x, sn, cs, n);
   HIPCHECK(hipGetLastError());
 }
 

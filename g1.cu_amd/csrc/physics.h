@@ -103,6 +103,54 @@ __device__ __forceinline__ void sincos_rn(float x, float& sn, float& cs) {
   cs = (float)cd;
 }
 
+// A double constant materialised in scalar registers where it is used: the polynomial
+// coefficients below would otherwise be hoisted out of the substep loop into ~20 vector registers.
+__device__ __forceinline__ double kc(double c) {
+  __asm__ volatile("" : "+s"(c));
+  return c;
+}
+// sin_rn and cos_rn of one argument for the hinge half-angles on a short fp64 path for |x| <= 4:
+// k = rint(x 2/pi), r = (x - k P1) - k P2 with P1 + P2 = pi/2 (P1 = RN(pi/2), so x - k P1 is exact
+// in the fma: both are multiples of 2^-52 and the difference is below 1), the Taylor series of
+// sin to r^15 and cos to r^14 by Horner (truncation at |r| = pi/4: 5e-17 and 1e-15 absolute), the
+// quadrant k mod 4 by selects and one rounding to float. For every float with |x| <= 4 this
+// equals the fp64-libm value rounded to float (tests: the probe g1_probe_sincos_hinge against the
+// oracle over all of them; one term fewer in either series breaks it for a few dozen), so the
+// 24-bit rounding absorbs the truncation; larger or non-finite x take the library. The two terms
+// that a series with margin would add cost the kernel its second wave per SIMD (their constants
+// are held in vector registers across the substep loop).
+__device__ __forceinline__ void sincos_hinge_rn(float x, float& sn, float& cs) {
+  if (fabsf(x) <= 4.f) {
+    const double xd = x;
+    const double kd = __builtin_rint(xd * 0.63661977236758134308);
+    const double r = __builtin_fma(-kd, 6.123233995736766e-17, __builtin_fma(-kd, 1.5707963267948966, xd));
+    const double z = r * r;
+    double ps = -1.0 / 1307674368000.0;
+    ps = __builtin_fma(z, ps, 1.0 / 6227020800.0);
+    ps = __builtin_fma(z, ps, -1.0 / 39916800.0);
+    ps = __builtin_fma(z, ps, 1.0 / 362880.0);
+    ps = __builtin_fma(z, ps, -1.0 / 5040.0);
+    ps = __builtin_fma(z, ps, 1.0 / 120.0);
+    ps = __builtin_fma(z, ps, -1.0 / 6.0);
+    double pc = -1.0 / 87178291200.0;
+    pc = __builtin_fma(z, pc, 1.0 / 479001600.0);
+    pc = __builtin_fma(z, pc, -1.0 / 3628800.0);
+    pc = __builtin_fma(z, pc, 1.0 / 40320.0);
+    pc = __builtin_fma(z, pc, -1.0 / 720.0);
+    pc = __builtin_fma(z, pc, 1.0 / 24.0);
+    pc = __builtin_fma(z, pc, -0.5);
+    const double sr = __builtin_fma(r * z, ps, r), cr = __builtin_fma(z, pc, 1.0);
+    // (sin x, cos x) = (sin r, cos r), (cos r, -sin r), (-sin r, -cos r), (-cos r, sin r) for k mod 4
+    const int k = (int)kd;
+    const float so = (float)((k & 1) ? cr : sr), co = (float)((k & 1) ? sr : cr);
+    sn = (k & 2) ? -so : so;
+    cs = ((k + 1) & 2) ? -co : co;
+    if (x == 0.f) sn = x;   // sin(-0) = -0 (r = +0 there)
+  } else {
+    sincos_rn(x, sn, cs);
+  }
+}
+
 // sin_rn and cos_rn of one argument on a short path for |x| <= 1/8 (the free joint's half rotation
 // per substep): the fp64 Taylor series by Horner, sin to x^11 and cos to x^12 (truncation below
 // 2^-68 relative), coefficients (-1)^k / n! rounded once, then one rounding to float. For every
@@ -126,7 +174,7 @@ __device__ __forceinline__ void sincos_small_rn(float x, float& sn, float& cs) {
     sn = (x == 0.f) ? x : s_;   // sin(-0) = -0
     cs = (float)__builtin_fma(z, pc, 1.0);
   } else {
-    sincos_rn(x, sn, cs);
+    sincos_hinge_rn(x, sn, cs);
   }
 }
 
@@ -428,7 +476,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   {
     const float h = 0.5f * st.jq;
     float sn, cs;
-    sincos_rn(h, sn, cs);
+    sincos_hinge_rn(h, sn, cs);
     const Q4 aa{cs, L.axis.x * sn, L.axis.y * sn, L.axis.z * sn};
     if (L.hinge) {
       xp = L.bpos;

@@ -62,6 +62,7 @@ SIGNATURES = {
     "g1_probe_divide": (None, [_c.c_int, _vp, _vp, _vp, _vp]),
     "g1_probe_sqrt": (None, [_c.c_int, _vp, _vp]),
     "g1_probe_sincos": (None, [_c.c_int, _vp, _vp, _vp]),
+    "g1_probe_sincos_hinge": (None, [_c.c_int, _vp, _vp, _vp]),
     "g1_probe_philox": (None, [_c.c_int, _vp, _vp, _c.c_uint, _c.c_uint]),
 }
 

@@ -159,6 +159,10 @@ void g1_probe_sqrt(int n, const float* x, float* out);
  * sn[i] = sin(x[i]), cs[i] = cos(x[i]) rounded to float. */
 void g1_probe_sincos(int n, const float* x, float* sn, float* cs);
 
+/* The physics kernel's sine/cosine of the hinge half-angles (forward kinematics) on n DEVICE
+ * arguments: sn[i] = sin(x[i]), cs[i] = cos(x[i]) rounded to float. */
+void g1_probe_sincos_hinge(int n, const float* x, float* sn, float* cs);
+
 /* Philox4x32-10 of n DEVICE counters ctr [n*4] with key (k0, k1) into out [n*4]. */
 void g1_probe_philox(int n, const unsigned* ctr, unsigned* out, unsigned k0, unsigned k1);
 

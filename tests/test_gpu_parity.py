@@ -320,30 +320,34 @@ def test_small_angle_sincos_exhaustive(g1, orc):
 
 
 def test_hinge_sincos_exhaustive(g1, orc):
-    """Above 1/8 the probe takes the FK's hinge path (one fp64 sincos, each result rounded once):
-    bit-identical to the oracle's fp64 libm sin and cos rounded once for EVERY float with
-    1/8 < |x| <= 4 (hinge half-angles, joint ranges included), plus a sample of larger ones."""
+    """The FK's hinge half-angle path (fp64 reduction by pi/2 and Taylor series, each result
+    rounded once; the library above |x| = 4): bit-identical to the oracle's fp64 libm sin and cos
+    rounded once for EVERY float with |x| <= 4 (both signs, zeros and denormals; hinge half-angles,
+    joint ranges included), plus a sample of larger ones. The free joint's path takes the same
+    function above 1/8, checked over 1/8 < |x| <= 4 through its own probe."""
     import torch
-    lo = int(np.float32(0.125).view(np.uint32)) + 1
     hi = int(np.float32(4.0).view(np.uint32))
+    lo8 = int(np.float32(0.125).view(np.uint32)) + 1
     chunk = 1 << 25
-    for start in range(lo, hi + 1, chunk):
-        bits = np.arange(start, min(start + chunk, hi + 1), dtype=np.uint32)
-        for sign in (np.uint32(0), np.uint32(0x80000000)):
-            x = (bits | sign).view(np.float32)
-            dx = torch.from_numpy(x).cuda()
-            ds, dc = torch.zeros_like(dx), torch.zeros_like(dx)
-            g1.lib.g1_probe_sincos(x.size, g1.dev_ptr(dx), g1.dev_ptr(ds), g1.dev_ptr(dc))
-            want_s, want_c = orc.sincos(x)
-            assert np.array_equal(ds.cpu().numpy().view(np.uint32), want_s.view(np.uint32)), start
-            assert np.array_equal(dc.cpu().numpy().view(np.uint32), want_c.view(np.uint32)), start
+    for probe, lo in ((g1.lib.g1_probe_sincos_hinge, 0), (g1.lib.g1_probe_sincos, lo8)):
+        for start in range(lo, hi + 1, chunk):
+            bits = np.arange(start, min(start + chunk, hi + 1), dtype=np.uint32)
+            for sign in (np.uint32(0), np.uint32(0x80000000)):
+                x = (bits | sign).view(np.float32)
+                dx = torch.from_numpy(x).cuda()
+                ds, dc = torch.zeros_like(dx), torch.zeros_like(dx)
+                probe(x.size, g1.dev_ptr(dx), g1.dev_ptr(ds), g1.dev_ptr(dc))
+                want_s, want_c = orc.sincos(x)
+                assert np.array_equal(ds.cpu().numpy().view(np.uint32), want_s.view(np.uint32)), start
+                assert np.array_equal(dc.cpu().numpy().view(np.uint32), want_c.view(np.uint32)), start
     rng = np.random.default_rng(7)
     x = (rng.uniform(4, 1e4, 1 << 22) * rng.choice([-1, 1], 1 << 22)).astype(np.float32)
     dx = torch.from_numpy(x).cuda()
-    ds, dc = torch.zeros_like(dx), torch.zeros_like(dx)
-    g1.lib.g1_probe_sincos(x.size, g1.dev_ptr(dx), g1.dev_ptr(ds), g1.dev_ptr(dc))
-    want_s, want_c = orc.sincos(x)
-    assert np.array_equal(ds.cpu().numpy(), want_s) and np.array_equal(dc.cpu().numpy(), want_c)
+    for probe in (g1.lib.g1_probe_sincos_hinge, g1.lib.g1_probe_sincos):
+        ds, dc = torch.zeros_like(dx), torch.zeros_like(dx)
+        probe(x.size, g1.dev_ptr(dx), g1.dev_ptr(ds), g1.dev_ptr(dc))
+        want_s, want_c = orc.sincos(x)
+        assert np.array_equal(ds.cpu().numpy(), want_s) and np.array_equal(dc.cpu().numpy(), want_c)
 
 
 def test_policy_mlp_trained_checkpoint(g1, orc):
