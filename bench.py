@@ -18,7 +18,7 @@ HIP events on the kernel's stream; `peak` is the MI355X fp32 figure. Hardware
 counters come from rocprofv3 passes over a one-rollout run of this script, started as child
 processes before this process touches the GPU: HBM traffic per dispatch (FETCH_SIZE and
 WRITE_SIZE, each scaled by what the counter reads for a copy of known size in the same run),
-VALU busy and lane utilisation, LDS utilisation and bank-conflict share. The working-set unit of
+VALU busy and lane utilisation, LDS utilisation, bank-conflict share and LDS bytes moved. The working-set unit of
 the reference algorithm (bytes of every per-world intermediate written and read once) is reported
 beside it as `hbm_proxy`: a workload measure, not an HBM ceiling.
 """
@@ -48,6 +48,8 @@ COUNTER_PASSES = (
     ("write", ["WRITE_SIZE"]),
     ("sq", ["VALUBusy", "VALUUtilization", "LdsUtil", "LDSBankConflict", "SQ_INSTS_VALU", "SQ_INSTS_LDS",
             "SQ_WAVES"]),
+    # LDS bytes moved: instruction size x active lanes, in 64-byte units
+    ("lds", ["SQ_INSTS_LDS_LOAD_BANDWIDTH", "SQ_INSTS_LDS_STORE_BANDWIDTH"]),
 )
 
 
@@ -259,6 +261,13 @@ def main():
             "lds_util_frac": counters.get("LdsUtil", float("nan")) / 100.0,
             "lds_bank_conflict_frac": counters.get("LDSBankConflict", float("nan")) / 100.0,
             "lds_insts_per_dispatch": counters.get("SQ_INSTS_LDS")}
+        lds_ld, lds_st = counters.get("SQ_INSTS_LDS_LOAD_BANDWIDTH"), counters.get("SQ_INSTS_LDS_STORE_BANDWIDTH")
+        if lds_ld is not None and lds_st is not None:
+            lds_bytes = (lds_ld + lds_st) * 64.0
+            roof["counters"].update({
+                "lds_bytes_per_dispatch": lds_bytes, "lds_load_bytes_per_dispatch": lds_ld * 64.0,
+                "lds_gbs": lds_bytes / avg_launch_s / 1e9, "lds_peak_gbs": rf.LDS_PEAK_GBS,
+                "lds_frac": lds_bytes / avg_launch_s / 1e9 / rf.LDS_PEAK_GBS})
     else:
         roof["counters"] = {"note": counter_note}
 

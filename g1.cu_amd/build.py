@@ -5,7 +5,9 @@
 The library lands where the reference's Python looks for it relative to its scripts folder
 (<root>/build/libg1env.so, reference scripts/ppo.py:20-24), with <root> = g1.cu_amd.
 """
+import json
 import os
+import re
 import subprocess
 import sys
 
@@ -38,22 +40,51 @@ SOURCES = (
 )
 
 
+# the compiler's per-kernel resource report (-Rpass-analysis=kernel-resource-usage), kept beside the
+# library: the persistent kernels are sized for two waves per SIMD (k_rollout sits at the 256-VGPR
+# edge of that occupancy, and one wave per SIMD runs it ~70% slower), which tests/test_abi_exports.py
+# checks from this file
+RESOURCES = os.path.join(OUT_DIR, "resource_usage.json")
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|Occupancy \[waves/SIMD\]|"
+                     r"VGPRs Spill|LDS Size \[bytes/block\]):\s+(\S+)")
+
+
+def _parse_resources(text, table):
+    fn = None
+    for m in _REMARK.finditer(text):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            fn = val
+            table[fn] = {}
+        elif fn is not None:
+            table[fn][key.split(" [")[0]] = int(val)
+
+
 def build(verbose=False):
     os.makedirs(OUT_DIR, exist_ok=True)
     objs = []
+    resources = {}
     for name, extra in SOURCES:
         obj = os.path.join(OUT_DIR, os.path.splitext(name)[0] + ".o")
-        cmd = ["hipcc", *FLAGS, *extra, "-c", os.path.join(HERE, "csrc", name), "-o", obj]
+        cmd = ["hipcc", *FLAGS, *extra, "-Rpass-analysis=kernel-resource-usage", "-c",
+               os.path.join(HERE, "csrc", name), "-o", obj]
         if verbose:
-            cmd.append("-Rpass-analysis=kernel-resource-usage")
             print(" ".join(cmd), flush=True)
-        subprocess.run(cmd, check=True)
+        p = subprocess.run(cmd, check=True, capture_output=True, text=True)
+        _parse_resources(p.stderr, resources)
+        if verbose:
+            sys.stderr.write(p.stderr)
         objs.append(obj)
     cmd = ["hipcc", f"--offload-arch={ARCH}", "-fPIC", "-shared", *objs, "-o", OUT + ".tmp"]
     subprocess.run(cmd, check=True)
     for obj in objs:
         os.remove(obj)
     os.replace(OUT + ".tmp", OUT)
+    with open(RESOURCES, "w") as f:
+        json.dump(resources, f, indent=1, sort_keys=True)
+    for fn, r in resources.items():
+        if ("k_rollout" in fn or "k_physics" in fn) and (r.get("Occupancy", 0) < 2 or r.get("ScratchSize", 0)):
+            sys.stderr.write(f"WARNING: {fn}: {r} (the persistent kernels are sized for 2 waves/SIMD, no scratch)\n")
     return OUT
 
 

@@ -25,6 +25,8 @@ FP32_PEAK_TFLOPS = 157.3       # dense fp32, vector and matrix (the vector figur
 FP32_UNPACKED_TFLOPS = 78.65   # 256 CUs x 128 fp32 FMA-flops/clock x 2.4 GHz (no packed-FP32 ops)
 CUS, PEAK_CLOCK_GHZ = 256, 2.4
 VALU_ISSUE_PEAK = CUS * PEAK_CLOCK_GHZ * 1e9   # wave64 VALU instructions per second (1 per CU per clock)
+LDS_BYTES_PER_CLK_CU = 128     # LDS data path per CU per clock (CDNA3/CDNA4 ISA figure)
+LDS_PEAK_GBS = CUS * LDS_BYTES_PER_CLK_CU * PEAK_CLOCK_GHZ   # 78,643 GB/s
 
 PGS_TABLE = 8
 FLOPS_P8 = (35939, 43859, 52598, 62205, 72680, 84023, 96234, 109313, 123260)   # c = 0..8 at p = 8
