@@ -237,97 +237,82 @@ struct PolicyArgs {
   float* mu_out;                    // probe mode: [N][29] mean action
 };
 
-__global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
+__global__ void __launch_bounds__(kPolicyThreads) __attribute__((amdgpu_waves_per_eu(4))) k_policy(PolicyArgs a) {
+  // One activation buffer per tile, X[32][ld] (k-octet interleaved columns): the hidden layers
+  // replace their input in place (mfma_layer_inplace), so two tiles fit in a CU's LDS at config 4's
+  // widths and one tile's observation, barriers and sampling overlap the other's MFMAs. Columns
+  // past a phase's live data hold its staging: the tile's state at kPolicyStage.. during the
+  // observation, the head's split-K partial tiles at ld - 256.. (policy_ldx sizes ld for both).
   extern __shared__ float smem[];
-  const int kLdx = a.ldx;
-  float* X = smem;                          // [32][ldx]
-  float* Y = smem + kTileWorlds * kLdx;     // [32][ldx]
+  const int ld = a.ldx;
+  float* X = smem;
   const int tid = threadIdx.x;
   const int w0 = blockIdx.x * kTileWorlds;
   // ---- observation + frozen normalisation (reference: src/g1_env.cu:297-304)
   if (!a.obs_in) {
-    // the tile's state first, with coalesced loads all in flight together (qp, qv, pa of worlds
-    // w0.. are contiguous blocks), into the second activation buffer (free until layer 1)
-    // (with the frozen statistics: mean and the divisor sqrt(var + 1e-8) per observation index)
-    float* Sq = Y;
-    float* Sv = Sq + kTileWorlds * kNQ;
-    float* Sp = Sv + kTileWorlds * kNV;
-    float* Smean = Sp + kTileWorlds * kAct;
-    float* Sdiv = Smean + kObs;
-    float* Srcp = Sdiv + kObs;   // RN(1 / divisor): the quotient below is div_rn, the IEEE quotient
-    static_assert(kTileWorlds * (kNQ + kNV + kAct) + 3 * kObs <= kTileWorlds * ((kObs + 31) / 32 * 32 + 4),
-                  "staging fits the smallest activation tile (pitch of policy_ldx)");
+    // the tile's state first, with coalesced loads (qp, qv, pa of worlds w0.. are contiguous
+    // blocks): world m's qpos, qvel and previous action at X[m][kPolicyStage + 0 | kNQ | kNQ + kNV]
     const int nw = a.N - w0 < kTileWorlds ? a.N - w0 : kTileWorlds;
-    for (int idx = tid; idx < kTileWorlds * (kNQ + kNV + kAct) + kObs; idx += kPolicyThreads) {
+    for (int idx = tid; idx < kTileWorlds * (kNQ + kNV + kAct); idx += kPolicyThreads) {
       float v = 0.f;
+      int m, c;
       if (idx < kTileWorlds * kNQ) {
-        if (idx < nw * kNQ) v = a.qp[(long)w0 * kNQ + idx];
+        m = idx / kNQ; c = idx - m * kNQ;
+        if (m < nw) v = a.qp[(long)w0 * kNQ + idx];
       } else if (idx < kTileWorlds * (kNQ + kNV)) {
         const int r = idx - kTileWorlds * kNQ;
-        if (r < nw * kNV) v = a.qv[(long)w0 * kNV + r];
-      } else if (idx < kTileWorlds * (kNQ + kNV + kAct)) {
-        const int r = idx - kTileWorlds * (kNQ + kNV);
-        if (r < nw * kAct) v = a.pa[(long)w0 * kAct + r];
+        m = r / kNV; c = kNQ + r - m * kNV;
+        if (m < nw) v = a.qv[(long)w0 * kNV + r];
       } else {
-        const int i = idx - kTileWorlds * (kNQ + kNV + kAct);
-        v = a.mean[i];
-        const float dv = sqrtf(a.var[i] + 1e-8f);
-        Sdiv[i] = dv;
-        Srcp[i] = rcp_rn(dv);
+        const int r = idx - kTileWorlds * (kNQ + kNV);
+        m = r / kAct; c = kNQ + kNV + r - m * kAct;
+        if (m < nw) v = a.pa[(long)w0 * kAct + r];
       }
-      Sq[idx] = v;
+      X[m * ld + kPolicyStage + c] = v;
     }
     __syncthreads();
+    // features go to columns kperm(i) < kPolicyStage: the staging is read, never overwritten
     for (int idx = tid; idx < kTileWorlds * kObs; idx += kPolicyThreads) {
       const int m = idx / kObs, i = idx - m * kObs;
       const int w = w0 + m;
       float z = 0.f;
       if (w < a.N) {
-        const float o = obs_value(Sq + m * kNQ, Sv + m * kNV, Sp + m * kAct, i);
+        const float* st = X + m * ld + kPolicyStage;
+        const float o = obs_value(st, st + kNQ, st + kNQ + kNV, i);
         if (a.t < a.H) a.O[((long)a.t * a.N + w) * kObs + i] = o;
-        z = div_rn(o - Smean[i], Sdiv[i], Srcp[i]);
+        // the divisor sqrt(var + 1e-8) and its RN reciprocal: z is div_rn, the IEEE quotient
+        const float dv = sqrtf(a.var[i] + 1e-8f);
+        z = div_rn(o - a.mean[i], dv, rcp_rn(dv));
         if (z < -10.f) z = -10.f; else if (z > 10.f) z = 10.f;
       }
-      X[m * kLdx + kperm(i)] = z;
+      X[m * ld + kperm(i)] = z;
     }
   } else {
     for (int idx = tid; idx < kTileWorlds * kObs; idx += kPolicyThreads) {
       const int m = idx / kObs, i = idx - m * kObs;
       const int w = w0 + m;
-      X[m * kLdx + kperm(i)] = w < a.N ? a.obs_in[(long)w * kObs + i] : 0.f;
+      X[m * ld + kperm(i)] = w < a.N ? a.obs_in[(long)w * kObs + i] : 0.f;
     }
   }
   // zero the first layer's K padding (observation index kObs .. K0 - 1; its weight rows are zero)
   for (int idx = tid; idx < kTileWorlds * (a.pp.K[0] - kObs); idx += kPolicyThreads) {
     const int m = idx / (a.pp.K[0] - kObs), i = kObs + idx % (a.pp.K[0] - kObs);
-    X[m * kLdx + kperm(i)] = 0.f;
+    X[m * ld + kperm(i)] = 0.f;
   }
   __syncthreads();
-  // ---- hidden layers
-  float* in = X;
-  float* out = Y;
-  for (int ly = 0; ly < a.shape.nl; ++ly) {
-    mfma_layer(in, kLdx, out, kLdx, a.pp.Wp + a.pp.woff[ly], a.pp.Wp + a.pp.boff[ly], a.pp.K[ly], a.pp.Np[ly],
-               a.shape.act, true, true);
-    __syncthreads();
-    float* t = in; in = out; out = t;
-  }
-  // ---- fused head [mu(29) | v | pad]: its K range is split over the waves when the free buffer
-  // holds their partial tiles; the summed head then overwrites the (consumed) input tile
-  float* head = out;
-  if (kTileWorlds * kLdx >= kPolicyWaves * 32 * 32) {
-    mfma_head_splitk(in, kLdx, in, kLdx, out, a.pp.Wp + a.pp.woff[a.shape.nl], a.pp.Wp + a.pp.boff[a.shape.nl],
-                     a.pp.K[a.shape.nl]);
-    head = in;
-  } else {
-    mfma_layer(in, kLdx, out, kLdx, a.pp.Wp + a.pp.woff[a.shape.nl], a.pp.Wp + a.pp.boff[a.shape.nl],
-               a.pp.K[a.shape.nl], 32, 0, false, false);
-  }
+  // ---- hidden layers, each over its own input
+  for (int ly = 0; ly < a.shape.nl; ++ly)
+    mfma_layer_inplace(X, ld, a.pp.Wp + a.pp.woff[ly], a.pp.Wp + a.pp.boff[ly], a.pp.K[ly], a.pp.Np[ly],
+                       a.shape.act);
+  // ---- fused head [mu(29) | v | pad] into columns 0..31 (natural order)
+  mfma_head_splitk(X, ld, ld - kPolicyWaves * 32, a.pp.Wp + a.pp.woff[a.shape.nl], a.pp.Wp + a.pp.boff[a.shape.nl],
+                   a.pp.K[a.shape.nl]);
   __syncthreads();
   // ---- sampling + log-prob (reference: src/g1_env.cu:308-318): one thread per (world, action)
   // draws the noise and writes the action; each world's log-prob terms are then summed by one
-  // thread in action order (the terms go through the free activation buffer)
-  float* lpt = (head == in) ? out : in;   // [32][kAct] log-prob terms
+  // thread in action order (the terms go to columns 32.. of the world's row)
+  const float* head = X;
+  float* lpt = X + 32;   // [32][ld]: log-prob terms
   const bool sample = !a.mu_out && a.t < a.H;
   if (sample) {
     // one thread per (world, action pair 2p, 2p + 1): both Box-Muller normals of one draw
@@ -337,7 +322,7 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
     const int m = tid / kPairs, pi = tid - m * kPairs;
     const int w = w0 + m;
     if (m < kTileWorlds && w < a.N) {
-      const float* h = head + m * kLdx;
+      const float* h = head + m * ld;
       const long ab = ((long)a.t * a.N + w) * kAct;
       float nz[2];
       if (a.act_noise) {
@@ -352,7 +337,7 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
         if (i < kAct) {
           const float ls = a.pp.log_std[i];
           a.A[ab + i] = h[i] + expf(ls) * nz[e];
-          lpt[m * kAct + i] = -0.5f * nz[e] * nz[e] - ls - 0.5f * LOG2PI;
+          lpt[m * ld + i] = -0.5f * nz[e] * nz[e] - ls - 0.5f * LOG2PI;
         }
       }
     }
@@ -361,7 +346,7 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
   if (tid < kTileWorlds) {
     const int w = w0 + tid;
     if (w < a.N) {
-      const float* h = head + tid * kLdx;
+      const float* h = head + tid * ld;
       const float val = h[kAct];
       if (a.mu_out) {
         for (int i = 0; i < kAct; ++i) a.mu_out[(long)w * kAct + i] = h[i];
@@ -370,7 +355,7 @@ __global__ void __launch_bounds__(kPolicyThreads) k_policy(PolicyArgs a) {
         a.Vlast[w] = val;
       } else {
         float lpsum = 0.f;
-        for (int i = 0; i < kAct; ++i) lpsum += lpt[tid * kAct + i];
+        for (int i = 0; i < kAct; ++i) lpsum += lpt[tid * ld + i];
         a.LP[(long)a.t * a.N + w] = lpsum;
         a.V[(long)a.t * a.N + w] = val;
       }
@@ -603,10 +588,17 @@ static void pack_policy(EnvState* E, const float* W, PackedPolicy* out, float* d
   *out = pp;
 }
 
-// activation tile pitch: widest layer rounded up to the 32-column tiles, + 4 floats (keeps rows off
-// the same LDS banks; a multiple of 4 for the 16-byte operand reads)
-static int policy_ldx(const PolicyShape& sh) { return (max_width(sh) + 31) / 32 * 32 + 4; }
-static size_t policy_smem(const PolicyShape& sh) { return 2 * (size_t)kTileWorlds * policy_ldx(sh) * sizeof(float); }
+// activation tile pitch: the widest of (every layer's width, the head's input plus its split-K
+// partial tiles, the observation staging) rounded up to the 32-column tiles, + 4 floats (keeps rows
+// off the same LDS banks; a multiple of 4 for the 16-byte operand reads)
+static int policy_ldx(const PolicyShape& sh) {
+  int m = max_width(sh);
+  const int khead = (sh.hid[sh.nl - 1] + 7) / 8 * 8;   // the head's K (make_packed pads to 8)
+  m = khead + kPolicyWaves * 32 > m ? khead + kPolicyWaves * 32 : m;
+  m = kPolicyStage + kNQ + kNV + kAct > m ? kPolicyStage + kNQ + kNV + kAct : m;
+  return (m + 31) / 32 * 32 + 4;
+}
+static size_t policy_smem(const PolicyShape& sh) { return (size_t)kTileWorlds * policy_ldx(sh) * sizeof(float); }
 
 static void launch_policy_kernel(const PolicyArgs& a, int N, const PolicyShape& sh) {
   const size_t smem = policy_smem(sh);

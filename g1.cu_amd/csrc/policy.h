@@ -1,10 +1,11 @@
 // policy.h -- observation, frozen normalisation, policy MLP on fp32 MFMA, Gaussian sampling.
 //
-// One workgroup (8 waves) owns a tile of 32 worlds. Activations live in LDS ([32][K], k-octet
-// interleaved, padded rows); each dense layer is a [32 x K] . [K x N] contraction on
-// v_mfma_f32_32x32x2f32 with the weights pre-packed k-octet-major, so the operands of four MFMA
-// steps are one float4 global load (B) and one 16-byte LDS read (A) per lane. Waves take 32-column
-// output tiles round-robin. The mu (29) and value (1) heads are fused into one 32-wide tile.
+// One workgroup (8 waves) owns a tile of 32 worlds. Activations live in one LDS buffer per tile
+// ([32][ld], k-octet interleaved, padded rows; each layer replaces its input); each dense layer is
+// a [32 x K] . [K x N] contraction on v_mfma_f32_32x32x2f32 with the weights pre-packed
+// k-octet-major, so the operands of four MFMA steps are one float4 global load (B) and one 16-byte
+// LDS read (A) per lane. Waves take 32-column output tiles round-robin. The mu (29) and value (1)
+// heads are fused into one 32-wide tile.
 //
 // Reference: obs src/g1_env.cu:46-81; normalise/clamp :298-302; MLP :219-239 (AC of
 // scripts/ppo.py:85-99, packing scripts/ppo_fused.py:35-44); sampling + log-prob :308-318.
@@ -44,9 +45,31 @@ struct PackedPolicy {
   const float* log_std;    // 29 values (torch order, unpacked tail of W)
 };
 
-__device__ __forceinline__ float act_fn(float x, int act) {
-  return act == 0 ? tanhf(x) : (x > 0.f ? x : expm1f(x));
+// Hidden-layer activations of the policy MLP (k_policy and the one-launch tile), branch-free so
+// that they issue between MFMAs. tanh: below |x| = 1/8 the odd series to x^7 (truncation < 2e-10),
+// above it 1 - 2 / (e^{2|x|} + 1) with the hardware exp2 (absolute error ~1e-7, no cancellation);
+// the sign restored. ELU: x for x > 0, else e^x - 1, below |x| = 1/8 by the series to x^5
+// (truncation < 6e-9). A layer's K sums over at most 512 such values, so the outputs stay far
+// inside the policy outputs' 1e-5 bound. ACT: 0 tanh, 1 ELU.
+template <int ACT>
+__device__ __forceinline__ float act_tile(float x) {
+  const float a = __builtin_fabsf(x);
+  if (ACT == 0) {
+    const float a2 = a * a;
+    const float ser = __builtin_fmaf(a * a2, __builtin_fmaf(a2, __builtin_fmaf(a2, -17.f / 315.f, 2.f / 15.f), -1.f / 3.f), a);
+    const float e = __builtin_amdgcn_exp2f(a * 2.8853900817779268f);   // e^{2a}
+    const float big = 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
+    const float r = a < 0.125f ? ser : big;
+    return __builtin_copysignf(r, x);
+  } else {
+    const float ser = x * __builtin_fmaf(x, __builtin_fmaf(x, __builtin_fmaf(x, __builtin_fmaf(x, 1.f / 120.f, 1.f / 24.f), 1.f / 6.f), 0.5f), 1.f);
+    const float em1 = __builtin_amdgcn_exp2f(x * 1.4426950408889634f) - 1.f;
+    const float neg = a < 0.125f ? ser : em1;
+    return x > 0.f ? x : neg;
+  }
 }
+
+__device__ __forceinline__ float act_fn(float x, int act) { return act == 0 ? act_tile<0>(x) : act_tile<1>(x); }
 
 // obs i of one world (reference: src/g1_env.cu:69-81)
 __device__ __forceinline__ float obs_value(const float* qp, const float* qv, const float* pa, int i) {
@@ -115,9 +138,9 @@ __host__ __device__ __forceinline__ int kperm(int k) { return (k & ~7) | ((k & 1
 
 // acc += A . B over k-octets [o0, o1) of one 32-column tile (B base at the tile's column), in
 // batches of kO octets whose loads are all in flight before the batch's MFMAs
+template <int kO>
 __device__ __forceinline__ void mfma_octets(f32x16& acc, const float* __restrict__ arow,
                                             const float4* __restrict__ wq, long wstride, int o0, int o1) {
-  constexpr int kO = 8;
   int o = o0;
   for (; o + kO <= o1; o += kO) {
     float4 b[kO], av[kO];
@@ -155,38 +178,58 @@ __device__ __forceinline__ void mfma_octets(f32x16& acc, const float* __restrict
   }
 }
 
-// out[m][n] = act(sum_k in[m][k] W[n][k] + b[n]) for the 32 worlds of the tile.
-// in: LDS [32][ldi] k-octet interleaved; out: LDS [32][ldo], interleaved when it feeds another
-// layer (permute_out), natural otherwise; wave wv takes n-tiles wv, wv + kPolicyWaves, ...
-__device__ __forceinline__ void mfma_layer(const float* __restrict__ in, int ldi, float* __restrict__ out, int ldo,
-                                           const float* __restrict__ Wp, const float* __restrict__ bias, int K,
-                                           int Np, int act, bool apply_act, bool permute_out) {
+// Columns of a tile row that hold the tile's state during the observation (past the first layer's
+// K = 104 interleaved input columns).
+constexpr int kPolicyStage = 128;
+// output tiles of one wave in a hidden layer (32 columns each, dealt round-robin over the waves)
+constexpr int kLayerTiles = (kMaxHidden / 32 + kPolicyWaves - 1) / kPolicyWaves;
+// k-octets whose operands one wave holds in flight (two tiles per CU at 4 waves per SIMD: <= 128
+// VGPRs per wave)
+constexpr int kLayerBatch = 4;
+
+// out[m][n] = act(sum_k in[m][k] W[n][k] + b[n]) for the 32 worlds of the tile, written over its
+// input: buf [32][ld] holds the input k-octet interleaved. Wave wv computes the output tiles wv,
+// wv + kPolicyWaves, .. into registers, the block barrier ends every read of the input, then the
+// activated outputs replace it (columns interleaved for the next layer) and a second barrier
+// publishes them.
+__device__ __forceinline__ void mfma_layer_inplace(float* buf, int ld, const float* __restrict__ Wp,
+                                                   const float* __restrict__ bias, int K, int Np, int act) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int mrow = lane & 31, khalf = lane >> 5;
-  for (int nt = wv; nt < Np / 32; nt += kPolicyWaves) {
-    const int n0 = nt * 32;
-    const float bv = bias[n0 + mrow];
-    f32x16 acc;
+  f32x16 acc[kLayerTiles];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = bv;
-    const float4* wq = reinterpret_cast<const float4*>(Wp) + (long)(n0 + mrow) * 2 + khalf;
-    mfma_octets(acc, in + mrow * ldi + 4 * khalf, wq, (long)Np * 2, 0, K / 8);
-    const int nc = permute_out ? kperm(n0 + mrow) : n0 + mrow;
+  for (int j = 0; j < kLayerTiles; ++j) {
+    const int nt = wv + j * kPolicyWaves;
+    if (nt < Np / 32) {
+      const int n0 = nt * 32;
+      const float bv = bias[n0 + mrow];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int m = (i & 3) + 4 * khalf + 8 * (i >> 2);
-      const float v = acc[i];
-      out[m * ldo + nc] = apply_act ? act_fn(v, act) : v;
+      for (int i = 0; i < 16; ++i) acc[j][i] = bv;
+      const float4* wq = reinterpret_cast<const float4*>(Wp) + (long)(n0 + mrow) * 2 + khalf;
+      mfma_octets<kLayerBatch>(acc[j], buf + mrow * ld + 4 * khalf, wq, (long)Np * 2, 0, K / 8);
     }
   }
+  __syncthreads();   // every wave has read the layer's input
+#pragma unroll
+  for (int j = 0; j < kLayerTiles; ++j) {
+    const int nt = wv + j * kPolicyWaves;
+    if (nt < Np / 32) {
+      const int nc = kperm(nt * 32 + mrow);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = (i & 3) + 4 * khalf + 8 * (i >> 2);
+        buf[m * ld + nc] = act_fn(acc[j][i], act);
+      }
+    }
+  }
+  __syncthreads();
 }
 
-// The fused 32-wide head has a single output tile: its k-octets are split over the waves and the
-// partial tiles are summed through LDS in wave order (scratch: kPolicyWaves x 32 x 32 floats, not
-// aliasing `in`; `out` may alias `in`: every wave has finished reading `in` at the barrier before
-// the sum is written). Output in natural column order.
-__device__ __forceinline__ void mfma_head_splitk(const float* in, int ldi, float* out, int ldo,
-                                                 float* __restrict__ scratch, const float* __restrict__ Wp,
+// The fused 32-wide head has a single output tile: its k-octets are split over the waves, wave wv's
+// partial tile goes to columns scr + 32 wv .. of the tile's rows (scr >= K: past the head's input),
+// and after a barrier the partial tiles are summed in wave order into columns 0..31 (natural
+// order; the input is dead by then).
+__device__ __forceinline__ void mfma_head_splitk(float* buf, int ld, int scr, const float* __restrict__ Wp,
                                                  const float* __restrict__ bias, int K) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int mrow = lane & 31, khalf = lane >> 5;
@@ -199,19 +242,20 @@ __device__ __forceinline__ void mfma_head_splitk(const float* in, int ldi, float
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = bv;
   const float4* wq = reinterpret_cast<const float4*>(Wp) + (long)mrow * 2 + khalf;
-  if (o0 < o1) mfma_octets(acc, in + mrow * ldi + 4 * khalf, wq, (long)Np * 2, o0, o1);
+  if (o0 < o1) mfma_octets<kLayerBatch>(acc, buf + mrow * ld + 4 * khalf, wq, (long)Np * 2, o0, o1);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int m = (i & 3) + 4 * khalf + 8 * (i >> 2);
-    scratch[(wv * 32 + m) * 32 + mrow] = acc[i];
+    buf[m * ld + scr + 32 * wv + mrow] = acc[i];
   }
   __syncthreads();
   for (int idx = threadIdx.x; idx < 32 * 32; idx += kPolicyThreads) {
     const int m = idx >> 5, n = idx & 31;
-    float v = scratch[m * 32 + n];
+    const float* row = buf + m * ld + scr;
+    float v = row[n];
 #pragma unroll
-    for (int w = 1; w < kPolicyWaves; ++w) v = v + scratch[(32 * w + m) * 32 + n];
-    out[m * ldo + n] = v;
+    for (int w = 1; w < kPolicyWaves; ++w) v = v + row[32 * w + n];
+    buf[m * ld + n] = v;
   }
 }
 

@@ -94,30 +94,6 @@ __device__ __forceinline__ f32x4 mfma4(f32x4 w, const float* x, f32x4 acc) {
   return acc;
 }
 
-// Hidden-layer activations of the tile MLP, branch-free so that they issue between the MFMAs of
-// the next output tile. tanh: below |x| = 1/8 the odd series to x^7 (truncation < 2e-10), above it
-// 1 - 2 / (e^{2|x|} + 1) with the hardware exp2 (absolute error ~1e-7, no cancellation); the sign
-// restored. ELU: x for x > 0, else e^x - 1, below |x| = 1/8 by the series to x^5 (truncation
-// < 6e-9). The first layer's K sums over 256 such values, so the outputs stay far inside the policy
-// outputs' 1e-5 bound. ACT: 0 tanh, 1 ELU.
-template <int ACT>
-__device__ __forceinline__ float act_tile(float x) {
-  const float a = __builtin_fabsf(x);
-  if (ACT == 0) {
-    const float a2 = a * a;
-    const float ser = __builtin_fmaf(a * a2, __builtin_fmaf(a2, __builtin_fmaf(a2, -17.f / 315.f, 2.f / 15.f), -1.f / 3.f), a);
-    const float e = __builtin_amdgcn_exp2f(a * 2.8853900817779268f);   // e^{2a}
-    const float big = 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
-    const float r = a < 0.125f ? ser : big;
-    return __builtin_copysignf(r, x);
-  } else {
-    const float ser = x * __builtin_fmaf(x, __builtin_fmaf(x, __builtin_fmaf(x, __builtin_fmaf(x, 1.f / 120.f, 1.f / 24.f), 1.f / 6.f), 0.5f), 1.f);
-    const float em1 = __builtin_amdgcn_exp2f(x * 1.4426950408889634f) - 1.f;
-    const float neg = a < 0.125f ? ser : em1;
-    return x > 0.f ? x : neg;
-  }
-}
-
 constexpr int kObsLoads = 25;   // k-steps of the first layer that read a state value (4 s + g < 100)
 
 // Observation feature i (reference: src/g1_env.cu:69-81): base angular and linear velocity (qvel
