@@ -240,9 +240,9 @@ struct PolicyArgs {
 __global__ void __launch_bounds__(kPolicyThreads) __attribute__((amdgpu_waves_per_eu(4))) k_policy(PolicyArgs a) {
   // One activation buffer per tile, X[32][ld] (k-octet interleaved columns): the hidden layers
   // replace their input in place (mfma_layer_inplace), so two tiles fit in a CU's LDS at config 4's
-  // widths and one tile's observation, barriers and sampling overlap the other's MFMAs. Columns
-  // past a phase's live data hold its staging: the tile's state at kPolicyStage.. during the
-  // observation, the head's split-K partial tiles at ld - 256.. (policy_ldx sizes ld for both).
+  // widths. Columns past a phase's live data hold its staging: the tile's state at kPolicyStage..
+  // and the normalisation constants at kPolicyConst.. (rows 0..9) during the observation, the
+  // head's split-K partial tiles at ld - 256.. (policy_ldx sizes ld for all of them).
   extern __shared__ float smem[];
   const int ld = a.ldx;
   float* X = smem;
@@ -253,6 +253,16 @@ __global__ void __launch_bounds__(kPolicyThreads) __attribute__((amdgpu_waves_pe
     // the tile's state first, with coalesced loads (qp, qv, pa of worlds w0.. are contiguous
     // blocks): world m's qpos, qvel and previous action at X[m][kPolicyStage + 0 | kNQ | kNQ + kNV]
     const int nw = a.N - w0 < kTileWorlds ? a.N - w0 : kTileWorlds;
+    // the frozen statistics per feature i: mean, the divisor sqrt(var + 1e-8) and its RN
+    // reciprocal (the quotient below is div_rn, the IEEE quotient), entry j of the 3 x kObs at
+    // X[j / 32][kPolicyConst + j mod 32]
+    auto cst = [&](int j) -> float& { return X[(j >> 5) * ld + kPolicyConst + (j & 31)]; };
+    for (int i = tid; i < kObs; i += kPolicyThreads) {
+      const float dv = sqrtf(a.var[i] + 1e-8f);
+      cst(i) = a.mean[i];
+      cst(kObs + i) = dv;
+      cst(2 * kObs + i) = rcp_rn(dv);
+    }
     for (int idx = tid; idx < kTileWorlds * (kNQ + kNV + kAct); idx += kPolicyThreads) {
       float v = 0.f;
       int m, c;
@@ -280,9 +290,7 @@ __global__ void __launch_bounds__(kPolicyThreads) __attribute__((amdgpu_waves_pe
         const float* st = X + m * ld + kPolicyStage;
         const float o = obs_value(st, st + kNQ, st + kNQ + kNV, i);
         if (a.t < a.H) a.O[((long)a.t * a.N + w) * kObs + i] = o;
-        // the divisor sqrt(var + 1e-8) and its RN reciprocal: z is div_rn, the IEEE quotient
-        const float dv = sqrtf(a.var[i] + 1e-8f);
-        z = div_rn(o - a.mean[i], dv, rcp_rn(dv));
+        z = div_rn(o - cst(i), cst(kObs + i), cst(2 * kObs + i));
         if (z < -10.f) z = -10.f; else if (z > 10.f) z = 10.f;
       }
       X[m * ld + kperm(i)] = z;
@@ -595,7 +603,7 @@ static int policy_ldx(const PolicyShape& sh) {
   int m = max_width(sh);
   const int khead = (sh.hid[sh.nl - 1] + 7) / 8 * 8;   // the head's K (make_packed pads to 8)
   m = khead + kPolicyWaves * 32 > m ? khead + kPolicyWaves * 32 : m;
-  m = kPolicyStage + kNQ + kNV + kAct > m ? kPolicyStage + kNQ + kNV + kAct : m;
+  m = kPolicyConst + 32 > m ? kPolicyConst + 32 : m;
   return (m + 31) / 32 * 32 + 4;
 }
 static size_t policy_smem(const PolicyShape& sh) { return (size_t)kTileWorlds * policy_ldx(sh) * sizeof(float); }

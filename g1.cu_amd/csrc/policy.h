@@ -181,6 +181,8 @@ __device__ __forceinline__ void mfma_octets(f32x16& acc, const float* __restrict
 // Columns of a tile row that hold the tile's state during the observation (past the first layer's
 // K = 104 interleaved input columns).
 constexpr int kPolicyStage = 128;
+// and, in rows 0..9, the 3 x 100 normalisation constants (32 per row)
+constexpr int kPolicyConst = kPolicyStage + 100;
 // output tiles of one wave in a hidden layer (32 columns each, dealt round-robin over the waves)
 constexpr int kLayerTiles = (kMaxHidden / 32 + kPolicyWaves - 1) / kPolicyWaves;
 // k-octets whose operands one wave holds in flight (two tiles per CU at 4 waves per SIMD: <= 128
