@@ -178,6 +178,49 @@ __device__ __forceinline__ void mfma_octets(f32x16& acc, const float* __restrict
   }
 }
 
+// mfma_octets for two output tiles of the same input rows (acc0: weights wq0, acc1: wq1): the A
+// operands are read once for both, and the two tiles' MFMAs alternate, so consecutive MFMAs do not
+// depend on each other. Each tile accumulates its octets in the same order as mfma_octets.
+template <int kO>
+__device__ __forceinline__ void mfma_octets2(f32x16& acc0, f32x16& acc1, const float* __restrict__ arow,
+                                             const float4* __restrict__ wq0, const float4* __restrict__ wq1,
+                                             long wstride, int o0, int o1) {
+  int o = o0;
+  for (; o + kO <= o1; o += kO) {
+    float4 b0[kO], b1[kO], av[kO];
+#pragma unroll
+    for (int u = 0; u < kO; ++u) {
+      b0[u] = wq0[(long)(o + u) * wstride];
+      b1[u] = wq1[(long)(o + u) * wstride];
+      av[u] = *reinterpret_cast<const float4*>(arow + 8 * (o + u));
+    }
+#pragma unroll
+    for (int u = 0; u < kO; ++u) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].x, b0[u].x, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].x, b1[u].x, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].y, b0[u].y, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].y, b1[u].y, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].z, b0[u].z, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].z, b1[u].z, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].w, b0[u].w, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].w, b1[u].w, acc1, 0, 0, 0);
+    }
+  }
+  // the last partial batch (o1 - o is wave-uniform)
+  for (; o < o1; ++o) {
+    const float4 b0 = wq0[(long)o * wstride], b1 = wq1[(long)o * wstride];
+    const float4 av = *reinterpret_cast<const float4*>(arow + 8 * o);
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, b0.x, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, b1.x, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, b0.y, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, b1.y, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, b0.z, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, b1.z, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, b0.w, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, b1.w, acc1, 0, 0, 0);
+  }
+}
+
 // Columns of a tile row that hold the tile's state during the observation (past the first layer's
 // K = 104 interleaved input columns).
 constexpr int kPolicyStage = 128;
@@ -198,17 +241,22 @@ __device__ __forceinline__ void mfma_layer_inplace(float* buf, int ld, const flo
                                                    const float* __restrict__ bias, int K, int Np, int act) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int mrow = lane & 31, khalf = lane >> 5;
+  static_assert(kLayerTiles == 2, "a wave takes at most two output tiles of a layer");
   f32x16 acc[kLayerTiles];
+  const int nt0 = wv, nt1 = wv + kPolicyWaves;
+  const float4* wq0 = reinterpret_cast<const float4*>(Wp) + (long)(nt0 * 32 + mrow) * 2 + khalf;
+  const float4* wq1 = reinterpret_cast<const float4*>(Wp) + (long)(nt1 * 32 + mrow) * 2 + khalf;
+  if (nt0 < Np / 32) {
+    const float bv0 = bias[nt0 * 32 + mrow];
 #pragma unroll
-  for (int j = 0; j < kLayerTiles; ++j) {
-    const int nt = wv + j * kPolicyWaves;
-    if (nt < Np / 32) {
-      const int n0 = nt * 32;
-      const float bv = bias[n0 + mrow];
+    for (int i = 0; i < 16; ++i) acc[0][i] = bv0;
+    if (nt1 < Np / 32) {
+      const float bv1 = bias[nt1 * 32 + mrow];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[j][i] = bv;
-      const float4* wq = reinterpret_cast<const float4*>(Wp) + (long)(n0 + mrow) * 2 + khalf;
-      mfma_octets<kLayerBatch>(acc[j], buf + mrow * ld + 4 * khalf, wq, (long)Np * 2, 0, K / 8);
+      for (int i = 0; i < 16; ++i) acc[1][i] = bv1;
+      mfma_octets2<kLayerBatch>(acc[0], acc[1], buf + mrow * ld + 4 * khalf, wq0, wq1, (long)Np * 2, 0, K / 8);
+    } else {
+      mfma_octets<kLayerBatch>(acc[0], buf + mrow * ld + 4 * khalf, wq0, (long)Np * 2, 0, K / 8);
     }
   }
   __syncthreads();   // every wave has read the layer's input
