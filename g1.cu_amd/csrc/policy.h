@@ -180,44 +180,46 @@ __device__ __forceinline__ void mfma_octets(f32x16& acc, const float* __restrict
 
 // mfma_octets for two output tiles of the same input rows (acc0: weights wq0, acc1: wq1): the A
 // operands are read once for both, and the two tiles' MFMAs alternate, so consecutive MFMAs do not
-// depend on each other. Each tile accumulates its octets in the same order as mfma_octets.
+// depend on each other. Each tile accumulates its octets in the same order as mfma_octets. The
+// weights are double-buffered: the next batch's global loads are issued before the current batch's
+// MFMAs (indices clamped to the last octet so every load is issued on every path; the surplus is
+// unused).
 template <int kO>
 __device__ __forceinline__ void mfma_octets2(f32x16& acc0, f32x16& acc1, const float* __restrict__ arow,
                                              const float4* __restrict__ wq0, const float4* __restrict__ wq1,
                                              long wstride, int o0, int o1) {
-  int o = o0;
-  for (; o + kO <= o1; o += kO) {
-    float4 b0[kO], b1[kO], av[kO];
+  if (o0 >= o1) return;
+  const int last = o1 - 1;
+  float4 b0[kO], b1[kO];
 #pragma unroll
-    for (int u = 0; u < kO; ++u) {
-      b0[u] = wq0[(long)(o + u) * wstride];
-      b1[u] = wq1[(long)(o + u) * wstride];
-      av[u] = *reinterpret_cast<const float4*>(arow + 8 * (o + u));
-    }
-#pragma unroll
-    for (int u = 0; u < kO; ++u) {
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].x, b0[u].x, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].x, b1[u].x, acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].y, b0[u].y, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].y, b1[u].y, acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].z, b0[u].z, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].z, b1[u].z, acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].w, b0[u].w, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].w, b1[u].w, acc1, 0, 0, 0);
-    }
+  for (int u = 0; u < kO; ++u) {
+    b0[u] = wq0[(long)min(o0 + u, last) * wstride];
+    b1[u] = wq1[(long)min(o0 + u, last) * wstride];
   }
-  // the last partial batch (o1 - o is wave-uniform)
-  for (; o < o1; ++o) {
-    const float4 b0 = wq0[(long)o * wstride], b1 = wq1[(long)o * wstride];
-    const float4 av = *reinterpret_cast<const float4*>(arow + 8 * o);
-    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, b0.x, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, b1.x, acc1, 0, 0, 0);
-    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, b0.y, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, b1.y, acc1, 0, 0, 0);
-    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, b0.z, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, b1.z, acc1, 0, 0, 0);
-    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, b0.w, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, b1.w, acc1, 0, 0, 0);
+  for (int o = o0; o < o1; o += kO) {
+    float4 n0[kO], n1[kO], av[kO];
+#pragma unroll
+    for (int u = 0; u < kO; ++u) {
+      n0[u] = wq0[(long)min(o + kO + u, last) * wstride];
+      n1[u] = wq1[(long)min(o + kO + u, last) * wstride];
+    }
+#pragma unroll
+    for (int u = 0; u < kO; ++u) av[u] = *reinterpret_cast<const float4*>(arow + 8 * min(o + u, last));
+#pragma unroll
+    for (int u = 0; u < kO; ++u) {
+      if (o + u < o1) {
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].x, b0[u].x, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].x, b1[u].x, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].y, b0[u].y, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].y, b1[u].y, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].z, b0[u].z, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].z, b1[u].z, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].w, b0[u].w, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u].w, b1[u].w, acc1, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kO; ++u) { b0[u] = n0[u]; b1[u] = n1[u]; }
   }
 }
 
@@ -231,6 +233,8 @@ constexpr int kLayerTiles = (kMaxHidden / 32 + kPolicyWaves - 1) / kPolicyWaves;
 // k-octets whose operands one wave holds in flight (two tiles per CU at 4 waves per SIMD: <= 128
 // VGPRs per wave)
 constexpr int kLayerBatch = 4;
+// the same for the two-tile loop, per buffer of its double-buffered weights
+constexpr int kPairBatch = 2;
 
 // out[m][n] = act(sum_k in[m][k] W[n][k] + b[n]) for the 32 worlds of the tile, written over its
 // input: buf [32][ld] holds the input k-octet interleaved. Wave wv computes the output tiles wv,
@@ -254,7 +258,7 @@ __device__ __forceinline__ void mfma_layer_inplace(float* buf, int ld, const flo
       const float bv1 = bias[nt1 * 32 + mrow];
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[1][i] = bv1;
-      mfma_octets2<kLayerBatch>(acc[0], acc[1], buf + mrow * ld + 4 * khalf, wq0, wq1, (long)Np * 2, 0, K / 8);
+      mfma_octets2<kPairBatch>(acc[0], acc[1], buf + mrow * ld + 4 * khalf, wq0, wq1, (long)Np * 2, 0, K / 8);
     } else {
       mfma_octets<kLayerBatch>(acc[0], buf + mrow * ld + 4 * khalf, wq0, (long)Np * 2, 0, K / 8);
     }
