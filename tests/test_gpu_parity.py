@@ -214,9 +214,12 @@ def test_substep_teacher_forced(g1, orc):
     assert np.array_equal(q.cpu().numpy(), q1) and np.array_equal(v.cpu().numpy(), v1)
 
 
-@pytest.mark.parametrize("hidden,act", [((256, 256), 0), ((512, 512, 256), 1)])
+@pytest.mark.parametrize("hidden,act", [((256, 256), 0), ((512, 512, 256), 1), ((48, 32), 1), ((80, 144), 0),
+                                        ((512,), 0), ((512, 512, 512), 1)])
 def test_policy_mlp(g1, orc, hidden, act):
-    """Policy MLP on fp32 MFMA vs the oracle's serial MLP and torch (config 3 and config 4 shapes)."""
+    """Policy MLP on fp32 MFMA (k_policy) vs the oracle's serial MLP: config 3 and config 4 shapes,
+    and narrow, single-layer and widest shapes, whose LDS tile pitch is set by the observation
+    staging, the head's split-K partial tiles or the widest layer respectively."""
     import torch
     import configs
     rng = np.random.default_rng(3)
