@@ -70,10 +70,12 @@ def build(verbose=False):
                os.path.join(HERE, "csrc", name), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
-        p = subprocess.run(cmd, check=True, capture_output=True, text=True)
+        p = subprocess.run(cmd, capture_output=True, text=True)
+        if p.returncode != 0 or verbose:
+            sys.stderr.write(p.stdout + p.stderr)
+        if p.returncode != 0:
+            raise subprocess.CalledProcessError(p.returncode, cmd)
         _parse_resources(p.stderr, resources)
-        if verbose:
-            sys.stderr.write(p.stderr)
         objs.append(obj)
     cmd = ["hipcc", f"--offload-arch={ARCH}", "-fPIC", "-shared", *objs, "-o", OUT + ".tmp"]
     subprocess.run(cmd, check=True)
