@@ -145,9 +145,32 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
   // Every state value is loaded first (one load per feature, all in flight together), then the
   // normalisation constants.
   const float qw = ld(qp + 3), qx = ld(qp + 4), qy = ld(qp + 5), qz = ld(qp + 6);
+  // Feature k = 4 s + g comes from one array for every lane of a quad s except at the array
+  // boundaries (s = 1, 2, 9, 16): one lane-dependent base per array (qv[k], qp[k - 2], qv[k - 32],
+  // pa[k - 67]) with the quad's offset as an immediate keeps the addresses at one register per
+  // array; the boundary quads load both candidates at in-range indices and select per lane.
+  // (Lanes whose feature is computed, not loaded, take an unused in-range value.)
   float raw[kObsLoads];
+  const float* const fv = qv + g;
+  const float* const fq = qp + g - 2;
+  const float* const fw = qv + g - 32;
+  const float* const fa = pa + g - 67;
 #pragma unroll
-  for (int s = 0; s < kObsLoads; ++s) raw[s] = ld(obs_src(qp, qv, pa, 4 * s + g));
+  for (int s = 0; s < kObsLoads; ++s) {
+    const int k0 = 4 * s;
+    if (k0 + 3 < 6) raw[s] = ld(fv + k0);                                  // qvel 0..5
+    else if (k0 < 9) raw[s] = k0 + g < 9 ? ld(qv + (g < 2 ? 4 + g : 0)) : ld(fq + k0);   // qvel 4, 5 | gravity | qpos
+    else if (k0 + 3 < 38) raw[s] = ld(fq + k0);                            // qpos 7..35
+    else if (k0 < 38) {                                                    // qpos 34, 35 | qvel 6, 7
+      const float a = ld(qp + (g < 2 ? k0 + g - 2 : 0)), b = ld(qv + (g < 2 ? 0 : k0 + g - 32));
+      raw[s] = g < 2 ? a : b;
+    } else if (k0 + 3 < 67) raw[s] = ld(fw + k0);                          // qvel 6..34
+    else if (k0 < 67) {                                                    // qvel 32..34 | prev action 0
+      const float a = ld(qv + (k0 + g < 67 ? k0 + g - 32 : 0)), b = ld(pa + (k0 + g < 67 ? 0 : k0 + g - 67));
+      raw[s] = k0 + g < 67 ? a : b;
+    } else if (k0 + 3 < 96) raw[s] = ld(fa + k0);                          // prev action 1..28
+    else raw[s] = ld(fv);                                                  // command and padding (unused)
+  }
   const float4* NC = reinterpret_cast<const float4*>(a.Wt + T.nrm_off + kObsSteps * g);
   float4 nmean[kObsSteps / 4], ndiv[kObsSteps / 4], nrcp[kObsSteps / 4];
 #pragma unroll
