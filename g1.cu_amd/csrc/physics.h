@@ -741,8 +741,47 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
       for (int j = i; j < 6; ++j) I6[L.b * 21 + symidx(i, j)] = M6[i * 6 + j];
   }
-  const float S6[6] = {sw.x, sw.y, sw.z, sv.x, sv.y, sv.z};
   wave_sync();   // S, I6 and the own forces of every body in LDS
+
+  // ---------------- RNE force gather (reference: src/aba_bias.cuh:112-120), chain-parallel, and
+  // the hinge right-hand sides x_b = tau_b - S_b.F_b of the smooth solve. Lane (chain g, row r)
+  // carries component r of the subtree force F_b = F_own_b + the children's F in descending child
+  // order (torso: + F_24 then + F_17), walked leaf -> root in lock-step over depth in the factor's
+  // layout below, and overwrites F_own_b in place; the pelvis' F_1 = F_own_1 + F_14 + F_8 + F_2
+  // closes the sweep. The chain is one addition per level with no exchange inside the chain, and
+  // each hinge lane then takes its own body's F from LDS for S_b.F_b (the lane-per-body form's
+  // order), so the factor's sweep only reads x_b.
+  {
+    float* const pF = Fo + 6 * c_off + rowc;
+    float Fc = 0.f;   // component rowc of the last body's subtree force
+#pragma unroll
+    for (int cd = kMaxDepth; cd >= 2; --cd) {
+      const bool act = cd >= c_lo && cd <= c_hi;
+      float F = pF[6 * cd];
+      if (cd == kTorsoDepth) {
+        // the right arm (chain 3) ends at depth 5; its force joins the torso (chain 2) first
+        const float g24 = from_next_chain(Fc);
+        F = grp == 2 ? F + g24 : F;
+      }
+      F = cd == c_hi ? F : F + Fc;
+      if (act && crow < 6) pF[6 * cd] = F;
+      Fc = F;
+    }
+    // pelvis, component r on lane r of chain 0 (chain 2's and chain 1's roots reach chain 0's
+    // lanes by v_permlane16_swap and row_shl:8)
+    const float F1 = ((Fo[6 + rowc] + from_upper_row(Fc)) + from_next_chain(Fc)) + Fc;
+    if (l < 6) Fo[6 + l] = F1;
+  }
+  wave_sync();   // every subtree force in LDS
+  if (L.hinge) {
+    const float* const Fb = Fo + 6 * L.b;
+    const float* const Sb = s.u.fac.S[L.b + 4];   // (w, v) of the hinge axis, as stored above
+    float bias = Sb[0] * Fb[0];
+#pragma unroll
+    for (int j = 1; j < 6; ++j) bias = fmaf_(Sb[j], Fb[j], bias);
+    s.u.fac.us[L.b] = -bias + jtau;   // x_b; the factor replaces it by u_b = x_b - S_b.pA_b
+  }
+  wave_sync();
 
   // ---------------- damped articulated-inertia factor, chain-parallel (reference:
   // src/aba_factor.cuh:77-88), fused with the leaf -> root sweep of the smooth solve
@@ -758,17 +797,11 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // symmetric downdate equals the packed entries bit for bit.
   float Dlr[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // row `crow` of the last body's downdate
   float cs[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};    // last body's pA + U u / D (all six components)
-  // the next level's body inputs (motion axis, I6 row, right-hand side, armature, dt kd; the
-  // last three live on lane b and come by shuffle), loaded while the current level computes
-  // The RNE force gather rides on the same sweep (reference: src/aba_bias.cuh:112-120): lane r
-  // carries component r of the body's subtree force F_b = F_own_b + the children's F in
-  // descending child order (torso: + F_24 then + F_17), and the body's right-hand side is
-  // tau - S.F (the bias in the lane-per-body form's order).
-  float Fc = 0.f;                                  // component rowc of the last body's subtree force
-  float Sn[6], In[6], Fn, tn, an, kn;
+  // the next level's body inputs (motion axis, I6 row, right-hand side x_b, armature, dt kd; the
+  // last two live on lane b and come by shuffle), loaded while the current level computes
+  float Sn[6], In[6], xn, an, kn;
   // per-lane base pointers: depth cd's operands and results sit at constant offsets from them
   const float* const pSc = &s.u.fac.S[c_off + 4][0];
-  const float* const pFc = Fo + 6 * c_off + rowc;
   const float* pIc[6];
 #pragma unroll
   for (int j = 0; j < 6; ++j) pIc[j] = I6 + 21 * c_off + symidx(rowc, j);
@@ -779,22 +812,17 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const int b = chain_body(cd);
 #pragma unroll
     for (int j = 0; j < 6; ++j) { Sn[j] = pSc[6 * cd + j]; In[j] = pIc[j][21 * cd]; }
-    Fn = pFc[6 * cd];
-    tn = gshfl(jtau, b);
+    xn = pUs[cd];
     an = gshfl(L.arm, b);
     kn = gshfl(L.bdt, b);
   };
   // one level of the chains; `junction` adds the right arm's downdate and bias force (gD, gc)
   // to the torso before its own child's
-  auto level = [&](int cd, bool junction, const float* gD, const float* gc, float gF) {
+  auto level = [&](int cd, bool junction, const float* gD, const float* gc) {
     const bool act = cd >= c_lo && cd <= c_hi;
     const bool leaf = cd == c_hi;
-    const int b = chain_body(cd);
     float Sd[6], IAr[6], pA[6];
-    const float tb = tn, arm = an, bdt = kn;
-    float F = Fn;
-    if (junction) F = F + gF;
-    F = leaf ? F : F + Fc;
+    const float xb_ = xn, arm = an, bdt = kn;
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
       Sd[j] = Sn[j];
@@ -805,12 +833,6 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       IAr[j] = leaf ? v : v + Dlr[j];
       pA[j] = leaf ? 0.f : (junction ? gc[j] + cs[j] : cs[j]);
     }
-    const float Fb[6] = {chain_bcast<0>(F), chain_bcast<1>(F), chain_bcast<2>(F),
-                         chain_bcast<3>(F), chain_bcast<4>(F), chain_bcast<5>(F)};
-    float bias = Sd[0] * Fb[0];
-#pragma unroll
-    for (int j = 1; j < 6; ++j) bias = fmaf_(Sd[j], Fb[j], bias);
-    const float xb_ = -bias + tb;
     float ur = 0.f;
 #pragma unroll
     for (int j = 0; j < 6; ++j) ur = fmaf_(IAr[j], Sd[j], ur);
@@ -832,7 +854,6 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       Dlr[j] = dl;
       cs[j] = c;
     }
-    Fc = F;
     if (act && crow < 6) pUc[6 * cd] = ur;
     if (act && crow == 0) { pDc[cd] = invD; pUs[cd] = u; }
   };
@@ -845,7 +866,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   prefetch(kMaxDepth);
   const float none[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int cd = kMaxDepth; cd > kTorsoDepth; --cd) level(cd, false, none, none, 0.f);
+  for (int cd = kMaxDepth; cd > kTorsoDepth; --cd) level(cd, false, none, none);
   {
     // the right arm (chain 3, lanes 24..) ends at depth 5; its downdate and bias force join the
     // torso (chain 2) at depth 4
@@ -853,22 +874,18 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     float gD[6], gc[6];   // chain 3's rows on chain 2's lanes (row_shl:8)
 #pragma unroll
     for (int j = 0; j < 6; ++j) { gD[j] = from_next_chain(Dlr[j]); gc[j] = from_next_chain(cs[j]); }
-    level(kTorsoDepth, grp == 2, gD, gc, from_next_chain(Fc));
+    level(kTorsoDepth, grp == 2, gD, gc);
   }
 #pragma unroll
-  for (int cd = kTorsoDepth - 1; cd >= 2; --cd) level(cd, false, none, none, 0.f);
+  for (int cd = kTorsoDepth - 1; cd >= 2; --cd) level(cd, false, none, none);
   // pelvis: I^A_1 = I6_1 + D_14 + D_8 + D_2 and pA_1 = cs_14 + cs_8 + cs_2 (descending children),
   // row r on lane r of chain 0; lane 1 keeps pA_1 for the base solve
   float pAs[6];
   float xb[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   {
-    // pelvis subtree force F_1 = F_own_1 + F_14 + F_8 + F_2 (descending children), component r
-    // on lane r of chain 0, then the free joint's right-hand side -S_base.F_1 on lane 1
-    // (chain 2's and chain 1's lanes reach chain 0's by v_permlane16_swap and row_shl:8)
-    const float F1 = ((Fo[6 + rowc] + from_upper_row(Fc)) + from_next_chain(Fc)) + Fc;
-    const V3 Fw{chain_bcast<0>(F1), chain_bcast<1>(F1), chain_bcast<2>(F1)};
-    const V3 Fv{chain_bcast<3>(F1), chain_bcast<4>(F1), chain_bcast<5>(F1)};
+    // the free joint's right-hand side -S_base.F_1 on lane 1 (F_1 from the force gather)
     if (base) {
+      const V3 Fw{Fo[6], Fo[7], Fo[8]}, Fv{Fo[9], Fo[10], Fo[11]};
       // x_base = 0 - S_base.F_1 (see sbase_dot): translation k takes Fv_k, rotation k R1 col k . Fw
       xb[0] = -Fv.x; xb[1] = -Fv.y; xb[2] = -Fv.z;
 #pragma unroll
