@@ -1425,12 +1425,13 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   float Acol[kMaxEfc];
 #pragma unroll
   for (int ii = 0; ii < kMaxEfc; ++ii) Acol[ii] = 0.f;
+  float Aii = 1.f;   // the lane's diagonal entry, taken as it is formed (1 on lanes without a row)
   const float Rci = s.Rc[ci];
   // pyramid coefficients of the lane's own row (d0 = 1 for every direction)
   const float dki1 = dcoef(ki, 1), dki2 = dcoef(ki, 2);
 #pragma unroll
   for (int c2 = 0; c2 < kNFoot; ++c2) {
-    if (c2 >= ncon_max) break;
+    if (c2 >= ncon_max) continue;
     const int lo = c2 < ci ? c2 : ci, hi = c2 < ci ? ci : c2;
     const float* Gp = s.u.G[hi * (hi + 1) / 2 + lo];
     float G[9];
@@ -1448,14 +1449,13 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const float t1 = fmaf_(dl2, G[7], fmaf_(dl1, G[4], 1.f * G[1]));
       const float t2 = fmaf_(dl2, G[8], fmaf_(dl1, G[5], 1.f * G[2]));
       float val = fmaf_(t2, dh2, fmaf_(t1, dh1, t0 * 1.f));
-      val = (eq && k2 == ki) ? val + Rci : val;
+      const bool diag = eq && k2 == ki;
+      val = diag ? val + Rci : val;
       Acol[4 * c2 + k2] = keep ? val : 0.f;
+      Aii = (diag && row) ? val : Aii;
     }
   }
   const float bi = row ? s.bvec[l] : 0.f;
-  float Aii = 1.f;
-#pragma unroll
-  for (int ii = 0; ii < kMaxEfc; ++ii) Aii = (ii == l && row) ? Acol[ii] : Aii;
 
   // ---------------- projected Gauss-Seidel (reference: src/contact.cuh:159-171), P.pgs sweeps
   float fi = 0.f;
