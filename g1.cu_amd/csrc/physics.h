@@ -442,6 +442,12 @@ __device__ __forceinline__ void wave_sync() { __builtin_amdgcn_fence(__ATOMIC_AC
 __device__ __forceinline__ void wave_sync() { __syncthreads(); }
 #endif
 
+constexpr bool hinge_armature_uniform() {
+  for (int d = 7; d < kNV; ++d)
+    if (MF::dof_armature[d] != MF::dof_armature[6]) return false;
+  return true;
+}
+
 // ================================================================ substep: qacc of one world
 // Inputs: lane state, PD torque of the lane's hinge dof (jtau). Output: qacc of the lane's dofs
 // (lane 1: 6 base dofs into bqacc[], hinge lanes: jqacc). Returns this world's contact count.
@@ -799,7 +805,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   float cs[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};    // last body's pA + U u / D (all six components)
   // the next level's body inputs (motion axis, I6 row, right-hand side x_b, armature, dt kd; the
   // last two live on lane b and come by shuffle), loaded while the current level computes
-  float Sn[6], In[6], xn, an, kn;
+  float Sn[6], In[6], xn, kn;
+  // every hinge has the same armature (the model's 0.01): a constant, not a per-body gather
+  constexpr float kArm = MF::dof_armature[6];
+  static_assert(hinge_armature_uniform(), "one armature for every hinge dof");
   // per-lane base pointers: depth cd's operands and results sit at constant offsets from them
   const float* const pSc = &s.u.fac.S[c_off + 4][0];
   const float* pIc[6];
@@ -813,7 +822,6 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
     for (int j = 0; j < 6; ++j) { Sn[j] = pSc[6 * cd + j]; In[j] = pIc[j][21 * cd]; }
     xn = pUs[cd];
-    an = gshfl(L.arm, b);
     kn = gshfl(L.bdt, b);
   };
   // one level of the chains; `junction` adds the right arm's downdate and bias force (gD, gc)
@@ -822,7 +830,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const bool act = cd >= c_lo && cd <= c_hi;
     const bool leaf = cd == c_hi;
     float Sd[6], IAr[6], pA[6];
-    const float xb_ = xn, arm = an, bdt = kn;
+    const float xb_ = xn, arm = kArm, bdt = kn;
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
       Sd[j] = Sn[j];
