@@ -31,12 +31,14 @@ FLAGS = [
 ]
 
 
-# translation units and their own flags: the one-launch rollout kernel is scheduled ILP-first
-# (config 3 rollout 12.83 -> 12.77 ms); the same scheduler makes k_physics and k_policy slower
-# (config 4 rollout 233.5 -> 240.8 ms), so they keep the default one
+# translation units and their own flags: both are scheduled ILP-first (LLVM's max-ilp machine
+# scheduler). The one-launch rollout kernel since its first version (config 3 rollout 12.83 -> 12.77
+# ms); k_physics and k_policy since the physics lost its force broadcast and select cascades
+# (config 4 rollout 185.4 -> 183.5 ms; with the older physics the same flag had made it 3% slower)
+ILP_FIRST = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
 SOURCES = (
-    ("g1env.hip", []),
-    ("rollout_kernel.hip", ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]),
+    ("g1env.hip", ILP_FIRST),
+    ("rollout_kernel.hip", ILP_FIRST),
 )
 
 

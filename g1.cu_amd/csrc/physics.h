@@ -432,10 +432,10 @@ __device__ __forceinline__ void base_solve(const WorldLds& s, const float (&xb)[
 // (k_physics, k_rollout, k_probe: 64 threads). A wave's LDS accesses are performed in program
 // order, so a wavefront-scope fence (the compiler keeps the accesses in order; no instruction) is
 // all a hand-over through LDS between its lanes needs; __syncthreads() adds an lgkmcnt(0) drain of
-// every outstanding LDS access at each phase boundary. The translation unit of k_rollout
-// (compiled with the ILP-first scheduler) defines G1_PHASE_FENCE and takes the fence: config 3
-// 10.50 -> 10.43 ms; k_physics keeps the barrier, with which its schedule is faster (config 4
-// 194.4 -> 193.3 ms).
+// every outstanding LDS access at each phase boundary. The translation unit of k_rollout defines
+// G1_PHASE_FENCE and takes the fence: config 3 10.50 -> 10.43 ms; k_physics keeps the barrier
+// (with the default scheduler it was faster, 194.4 against 193.3 ms at config 4; with the ILP-first
+// one both measure the same).
 #ifdef G1_PHASE_FENCE
 __device__ __forceinline__ void wave_sync() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
 #else

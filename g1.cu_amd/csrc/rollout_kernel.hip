@@ -1,6 +1,6 @@
 // rollout_kernel.hip -- k_rollout, the whole g1_rollout in one persistent launch (the scheme and
-// its argument block are described in queue.h). Compiled on its own with the ILP-first machine
-// scheduler: measured faster for this kernel, slower for k_physics and k_policy.
+// its argument block are described in queue.h). Its own translation unit, so that it alone takes
+// the wavefront-fence phase boundaries (G1_PHASE_FENCE below).
 #include <hip/hip_runtime.h>
 
 #define G1_PHASE_FENCE   // world_qacc's phase boundaries as wavefront fences (see wave_sync)
