@@ -94,7 +94,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
     const int p = qc + kQueues * (int)(it - (unsigned)j * nq);
     const int k = j / nch, c = j - k * nch;
     if (j > 0) wait_flag(a.flags + p, a.fbase + (unsigned)j, a.qerr, a.xlocal);
-    physics_item(a, s, L, g, l, p, k, c, hcnt);
+    physics_item(kernarg_reread<PhysArgs>(), s, L, g, l, p, k, c, hcnt);
     release_flag(a.flags + p, a.fbase + (unsigned)j + 1u, a.xlocal);
   }
   if (a.ncon_hist && l < 9 && hcnt) atomicAdd(&a.ncon_hist[l], (unsigned long long)hcnt);

@@ -254,6 +254,18 @@ struct RolloutArgs {
                             // (zero between launches)
 };
 
+// A kernel's by-value argument block (its only argument, at offset 0 of the kernarg segment),
+// re-read where it is used: the opaque copy of the segment address keeps the compiler from
+// loading every field once at the top and holding them across the work loop, in scalar
+// registers spilled to vector lanes and in copies in vector registers the physics needs.
+template <class T>
+__device__ __forceinline__ const T& kernarg_reread() {
+  typedef const __attribute__((address_space(4))) T* KargPtr;
+  KargPtr p = (KargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  __asm__ volatile("" : "+s"(p));
+  return *(const T*)p;
+}
+
 // Enqueue the one-launch rollout kernel on the null stream (rollout_kernel.hip).
 void launch_rollout_kernel(const RolloutArgs& ra, int grid);
 

@@ -42,8 +42,10 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
     const int w = tile_world(qq, u, jw, kQueues);
     const bool valid = (jw >> 1) < np && w < a.N;
     const auto ld = [](const auto* ptr) { return ld_l2(ptr); };
-    if (ra.po.tl.act == 0) policy_tile<0>(ra.po, a.qp, a.qv, a.pa, a.rng, a.seed, a.N, t, w, valid, scratch_lds, ld);
-    else policy_tile<1>(ra.po, a.qp, a.qv, a.pa, a.rng, a.seed, a.N, t, w, valid, scratch_lds, ld);
+    const RolloutArgs& rb = kernarg_reread<RolloutArgs>();
+    const PhysArgs& b = rb.ph;
+    if (rb.po.tl.act == 0) policy_tile<0>(rb.po, b.qp, b.qv, b.pa, b.rng, b.seed, b.N, t, w, valid, scratch_lds, ld);
+    else policy_tile<1>(rb.po, b.qp, b.qv, b.pa, b.rng, b.seed, b.N, t, w, valid, scratch_lds, ld);
     release_flag(ra.tflags + qq + kQueues * u, ra.tbase + (unsigned)t + 1u, a.xlocal);
   };
 
@@ -85,7 +87,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
       int lo = l;
       __asm__ volatile("" : "+v"(lo));
       const LaneModel L = lane_model(lo);
-      physics_item(a, s, L, g, l, p, t, c, hcnt);
+      physics_item(kernarg_reread<RolloutArgs>().ph, s, L, g, l, p, t, c, hcnt);
     }
     release_flag(a.flags + p, a.fbase + (unsigned)jj + 1u, a.xlocal);
     if (c == nck - 1) {
