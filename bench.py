@@ -53,27 +53,72 @@ COUNTER_PASSES = (
 )
 
 
+def cpu_model():
+    """The host CPU's model name (lscpu's "Model name"), from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, threads, seed=0):
-    """The CPU oracle's rollout (fp32, OpenMP over worlds) on a bounded sample of the workload."""
+    """The CPU oracle's rollout (fp32) on a bounded sample of the workload, on `threads` host
+    threads (OpenMP over worlds) and on one thread (a sixteenth of the sample)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     import configs
     oracle.build()
-    rng = np.random.default_rng(seed)
-    n = min(8192, cfg["N"])   # config 3 whole (~25 core-seconds); config 4 as its first 8192 worlds
     H, S = cfg["H"], cfg["S"]
-    qp, qv, pa, st = configs.reset_states(rng, n)
-    W = configs.policy_init(rng, hidden=cfg["hidden"])
-    an, rn = configs.rollout_noise(rng, H, n)
-    mean = np.zeros(100, np.float32)
-    var = np.ones(100, np.float32)
-    t0 = time.perf_counter()
-    oracle.rollout(qp, qv, pa, st, W, mean, var, an, rn, H, S=S, pgs=cfg["pgs"], hidden=cfg["hidden"],
-                   act=cfg["act"], threads=threads)
-    dt = time.perf_counter() - t0
+
+    def run(n, nthreads):
+        rng = np.random.default_rng(seed)
+        qp, qv, pa, st = configs.reset_states(rng, n)
+        W = configs.policy_init(rng, hidden=cfg["hidden"])
+        an, rn = configs.rollout_noise(rng, H, n)
+        mean = np.zeros(100, np.float32)
+        var = np.ones(100, np.float32)
+        t0 = time.perf_counter()
+        oracle.rollout(qp, qv, pa, st, W, mean, var, an, rn, H, S=S, pgs=cfg["pgs"], hidden=cfg["hidden"],
+                       act=cfg["act"], threads=nthreads)
+        return time.perf_counter() - t0
+
+    n = min(8192, cfg["N"])   # config 3 whole (~25 core-seconds); config 4 as its first 8192 worlds
+    dt = run(n, threads)
+    n1 = n // 16
+    dt1 = run(n1, 1)
     return dict(value=n * H * S / dt, unit="substeps/s", cores=threads, kind="port",
+                cpu_model=cpu_model(), nproc=os.cpu_count(),
                 sample=f"oracle rollout of {n} worlds x {H} control steps x {S} substeps "
-                       f"({n * H * S} world-substeps, {dt:.1f} s wall on {threads} threads)")
+                       f"({n * H * S} world-substeps, {dt:.1f} s wall on {threads} threads)",
+                single_thread={"value": n1 * H * S / dt1, "unit": "substeps/s", "cores": 1,
+                               "sample": f"the first {n1} worlds of the same rollout ({n1 * H * S} "
+                                         f"world-substeps, {dt1:.1f} s on one thread)"})
+
+
+def measure_copy_bandwidth(mib=COPY_MIB, reps=10):
+    """BW_meas: device-to-device copy of `mib` MiB timed with HIP events (read + write bytes per
+    second), the box's measured HBM stream bandwidth."""
+    import torch
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del a, b
+    torch.cuda.empty_cache()
+    return 2.0 * mib * (1 << 20) / (ms * 1e-3) / 1e9
 
 
 # ---------------------------------------------------------------- hardware counters (rocprofv3)
@@ -129,6 +174,7 @@ def measure_counters(config, kernel, timeout_s=150):
             return None, f"counter pass {name} timed out"
         rows = _read_counters(outdir)
         shutil.rmtree(outdir, ignore_errors=True)
+        print(f"bench: counter pass {name} done (exit {p.returncode}, {len(rows)} rows)", file=sys.stderr, flush=True)
         if not rows:
             return None, f"counter pass {name}: no output (exit {p.returncode}): {p.stderr[-300:]}"
         for r in rows:
@@ -222,6 +268,7 @@ def main():
     ms_rollout = wall * 1e3 / args.steps
     substeps_per_s = N * H * S / (wall / args.steps)
 
+    bw_meas = measure_copy_bandwidth()
     launches = max(pr["physics_launches"], 1)
     avg_launch_s = pr["physics_ms"] / launches * 1e-3
     bytes_total, flops_total = rf.physics_work(hist, pgs, control_steps_worlds=N * H * args.steps)
@@ -241,8 +288,10 @@ def main():
             "kernel": kernel, "avg_launch_ms": avg_launch_s * 1e3, "algorithmic_flops_per_launch": flops_launch,
             "physics_flops_per_launch": phys_flops_launch, "mlp_flops_per_launch": mlp_flops_launch,
             "mean_ncon": cbar, "frac_of_unpacked_fp32": achieved_tf / rf.FP32_UNPACKED_TFLOPS,
+            "bw_meas_gbs": bw_meas,
             "hbm_proxy": {"unit": "GB/s", "achieved": bytes_launch / avg_launch_s / 1e9, "peak": rf.HBM_PEAK_GBS,
                           "frac": bytes_launch / avg_launch_s / 1e9 / rf.HBM_PEAK_GBS,
+                          "frac_of_bw_meas": bytes_launch / avg_launch_s / 1e9 / bw_meas,
                           "algorithmic_bytes_per_launch": bytes_launch,
                           "note": "reference-algorithm working set per world-substep, written and read once; "
                                   "held in registers and LDS, not HBM"}}
@@ -252,6 +301,7 @@ def main():
             "source": f"rocprofv3 --pmc, one-rollout run of this script ({counters['dispatches']} {kernel} dispatches)",
             "hbm_bytes_per_dispatch": counters["traffic_bytes"],
             "hbm_gbs": counters["traffic_bytes"] / avg_launch_s / 1e9,
+            "hbm_frac_of_bw_meas": counters["traffic_bytes"] / avg_launch_s / 1e9 / bw_meas,
             "fetch_write_scale": [counters["fetch_scale"], counters["write_scale"]],
             "valu_busy_frac": counters.get("VALUBusy", float("nan")) / 100.0,
             "valu_lane_utilization": counters.get("VALUUtilization", float("nan")) / 100.0,
@@ -299,6 +349,7 @@ def main():
                     "policy_mfma_frac": pol_tf / rf.FP32_PEAK_TFLOPS if pol_tf else None}),
         "ncon_hist": hist.tolist(),
     }
+    print(f"bench: {args.steps} rollouts timed, {ms_rollout:.3f} ms each", file=sys.stderr, flush=True)
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(cfg, threads)

@@ -64,6 +64,8 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
   if (blockIdx.x == 0 && threadIdx.x < kQueues) a.qctr[(a.qpar ^ 1) * kQueues + threadIdx.x] = 0u;
   const int npairs = (a.N + 1) >> 1;
   const int nch = a.nch;
+  // items of a pair: nch per control step, nchl in the launch's last one (its own chunk table)
+  const unsigned per_pair = (unsigned)((a.K - 1) * nch + a.nchl), nreg = (unsigned)((a.K - 1) * nch);
   // queue qc being drained: the block's own, then the other queues of its XCD (same L2, so the
   // hand-over holds; every item waited for was claimed earlier by a running wave)
   int qc = q;
@@ -71,7 +73,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
   unsigned* ctr;
   auto set_queue = [&](int qq) {
     nq = npairs > qq ? (unsigned)((npairs - qq + kQueues - 1) / kQueues) : 0u;
-    nitems = nq * (unsigned)(a.K * nch);
+    nitems = nq * per_pair;
     ctr = a.qctr + a.qpar * kQueues + qq;
   };
   set_queue(q);
@@ -92,7 +94,8 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
     }
     const int j = (int)(it / nq);
     const int p = qc + kQueues * (int)(it - (unsigned)j * nq);
-    const int k = j / nch, c = j - k * nch;
+    const int k = (unsigned)j < nreg ? j / nch : a.K - 1;
+    const int c = j - k * nch;
     if (j > 0) wait_flag(a.flags + p, a.fbase + (unsigned)j, a.qerr, a.xlocal);
     physics_item(kernarg_reread<PhysArgs>(), s, L, g, l, p, k, c, hcnt);
     release_flag(a.flags + p, a.fbase + (unsigned)j + 1u, a.xlocal);
@@ -290,7 +293,7 @@ __global__ void __launch_bounds__(kPolicyThreads) __attribute__((amdgpu_waves_pe
         const float* st = X + m * ld + kPolicyStage;
         const float o = obs_value(st, st + kNQ, st + kNQ + kNV, i);
         if (a.t < a.H) a.O[((long)a.t * a.N + w) * kObs + i] = o;
-        z = div_rn(o - cst(i), cst(kObs + i), cst(2 * kObs + i));
+        z = div_rn_inf(o - cst(i), cst(kObs + i), cst(2 * kObs + i));
         if (z < -10.f) z = -10.f; else if (z > 10.f) z = 10.f;
       }
       X[m * ld + kperm(i)] = z;
@@ -523,7 +526,19 @@ struct EnvState {
   int prof_on;
   std::vector<hipEvent_t> ev_phys, ev_pol;
   size_t n_phys, n_pol;
+  long dev_bytes;   // device memory held (g1_env_device_bytes)
 };
+
+// Device allocations of an env, counted in dev_bytes.
+template <class T>
+static void dev_alloc(EnvState* E, T** p, size_t bytes) {
+  HIPCHECK(hipMalloc((void**)p, bytes));
+  E->dev_bytes += (long)bytes;
+}
+static void dev_free(EnvState* E, void* p, size_t bytes) {
+  HIPCHECK(hipFree(p));
+  E->dev_bytes -= (long)bytes;
+}
 
 static void prof_mark(std::vector<hipEvent_t>& v, size_t& n) {
   if (n == v.size()) {
@@ -581,8 +596,8 @@ static void pack_policy(EnvState* E, const float* W, PackedPolicy* out, float* d
   float* Wp = dst;
   if (!Wp) {
     if (total > E->Wp_cap) {
-      if (E->Wp) HIPCHECK(hipFree(E->Wp));
-      HIPCHECK(hipMalloc(&E->Wp, total * sizeof(float)));
+      if (E->Wp) dev_free(E, E->Wp, E->Wp_cap * sizeof(float));
+      dev_alloc(E, &E->Wp, total * sizeof(float));
       E->Wp_cap = total;
     }
     Wp = E->Wp;
@@ -687,7 +702,7 @@ static void chunk_schedule(PhysArgs& a, int pgrid, bool one_launch = false) {
 static void launch_physics(EnvState* E, PhysArgs& a) {
   if (a.K <= 0) fail("physics launch: K must be positive");
   chunk_schedule(a, E->pgrid);
-  const long per_pair = (long)a.K * a.nch;
+  const long per_pair = (long)(a.K - 1) * a.nch + a.nchl;
   if (per_pair > (1L << 30)) fail("physics launch: too many work items per pair");
   a.fbase = E->qdone;
   a.qpar = E->qpar;
@@ -741,8 +756,8 @@ static void rollout_fused(EnvState* E, int H, const float* W, const float* mean,
   float* Wt = wp;
   if (!Wt) {
     if (tl.total > E->Wt_cap) {
-      if (E->Wt) HIPCHECK(hipFree(E->Wt));
-      HIPCHECK(hipMalloc(&E->Wt, tl.total * sizeof(float)));
+      if (E->Wt) dev_free(E, E->Wt, E->Wt_cap * sizeof(float));
+      dev_alloc(E, &E->Wt, tl.total * sizeof(float));
       E->Wt_cap = tl.total;
     }
     Wt = E->Wt;
@@ -834,29 +849,29 @@ void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
   EnvState* E = new EnvState();
   E->N = N; E->S = substeps; E->pgs = pgs_iters; E->seed = seed; E->mu = MF::foot_mu;
   E->shape = PolicyShape{2, {256, 256, 0, 0}, 0};
-  HIPCHECK(hipMalloc(&E->qp, (size_t)N * kNQ * 4));
-  HIPCHECK(hipMalloc(&E->qv, (size_t)N * kNV * 4));
-  HIPCHECK(hipMalloc(&E->pa, (size_t)N * kAct * 4));
-  HIPCHECK(hipMalloc(&E->steps, (size_t)N * 4));
-  HIPCHECK(hipMalloc(&E->rng, (size_t)N * 4));
-  HIPCHECK(hipMalloc(&E->dact, (size_t)N * kAct * 4));
-  HIPCHECK(hipMalloc(&E->zero_act, (size_t)N * kAct * 4));
-  HIPCHECK(hipMalloc(&E->bench_r, (size_t)N * 4));
-  HIPCHECK(hipMalloc(&E->bench_d, (size_t)N * 4));
-  HIPCHECK(hipMalloc(&E->ncon_hist, 9 * sizeof(unsigned long long)));
+  dev_alloc(E, &E->qp, (size_t)N * kNQ * 4);
+  dev_alloc(E, &E->qv, (size_t)N * kNV * 4);
+  dev_alloc(E, &E->pa, (size_t)N * kAct * 4);
+  dev_alloc(E, &E->steps, (size_t)N * 4);
+  dev_alloc(E, &E->rng, (size_t)N * 4);
+  dev_alloc(E, &E->dact, (size_t)N * kAct * 4);
+  dev_alloc(E, &E->zero_act, (size_t)N * kAct * 4);
+  dev_alloc(E, &E->bench_r, (size_t)N * 4);
+  dev_alloc(E, &E->bench_d, (size_t)N * 4);
+  dev_alloc(E, &E->ncon_hist, 9 * sizeof(unsigned long long));
   const int npairs = (N + 1) / 2;
-  HIPCHECK(hipMalloc(&E->qflags, (size_t)npairs * sizeof(unsigned)));
-  HIPCHECK(hipMalloc(&E->qctr, 2 * kQueues * sizeof(unsigned)));
-  HIPCHECK(hipMalloc(&E->qerr, sizeof(int)));
-  HIPCHECK(hipMalloc(&E->qacc_e, (size_t)N * kGroup * 4));
-  HIPCHECK(hipMalloc(&E->qacc_vx, (size_t)N * 4));
+  dev_alloc(E, &E->qflags, (size_t)npairs * sizeof(unsigned));
+  dev_alloc(E, &E->qctr, 2 * kQueues * sizeof(unsigned));
+  dev_alloc(E, &E->qerr, sizeof(int));
+  dev_alloc(E, &E->qacc_e, (size_t)N * kGroup * 4);
+  dev_alloc(E, &E->qacc_vx, (size_t)N * 4);
   HIPCHECK(hipMemset(E->qflags, 0, (size_t)npairs * sizeof(unsigned)));
   HIPCHECK(hipMemset(E->qctr, 0, 2 * kQueues * sizeof(unsigned)));
   HIPCHECK(hipMemset(E->qerr, 0, sizeof(int)));
   E->qdone = 0; E->qpar = 0;
-  HIPCHECK(hipMalloc(&E->tflags, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
+  dev_alloc(E, &E->tflags, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned));
   HIPCHECK(hipMemset(E->tflags, 0, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
-  HIPCHECK(hipMalloc(&E->tcount, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
+  dev_alloc(E, &E->tcount, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned));
   HIPCHECK(hipMemset(E->tcount, 0, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
   E->tdone = 0;
   E->fused = 1;
@@ -883,7 +898,7 @@ void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
     for (int b = 0; b < E->pgrid; ++b)
       if (hx[b] != b % kXcds) E->xlocal = 0;
   }
-  HIPCHECK(hipMalloc(&E->dout, (size_t)N * (kObs + 2) * 4));
+  dev_alloc(E, &E->dout, (size_t)N * (kObs + 2) * 4);
   HIPCHECK(hipHostMalloc((void**)&E->h_act, (size_t)N * kAct * 4, hipHostMallocDefault));
   HIPCHECK(hipHostMalloc((void**)&E->h_out, ((size_t)N * (kObs + 2) + 1) * 4, hipHostMallocDefault));
   HIPCHECK(hipHostMalloc((void**)&E->h_qerr, sizeof(int), hipHostMallocDefault));
@@ -1039,6 +1054,7 @@ void g1_occupancy_report(void) {
   printf("%s (%s): %d CUs, LDS/block %zu B, regs/block %d\n", p.name, p.gcnArchName, p.multiProcessorCount,
          p.sharedMemPerBlock, p.regsPerBlock);
   struct { const char* nm; const void* fn; int threads; size_t smem; } ks[] = {
+      {"k_rollout", rollout_kernel_fn(), kPhysThreads, 0},
       {"k_physics", (const void*)k_physics, kPhysThreads, 0},
       {"k_policy", (const void*)k_policy, kPolicyThreads, policy_smem(PolicyShape{2, {256, 256, 0, 0}, 0})},
       {"k_probe", (const void*)k_probe, kPhysThreads, 0}};
@@ -1090,6 +1106,8 @@ int g1_env_set_policy(void* h, int nlayers, const int* hidden, int activation) {
   E->shape = sh;
   return 0;
 }
+
+long g1_env_device_bytes(void* h) { return ((EnvState*)h)->dev_bytes; }
 
 long g1_env_policy_params(void* h) { return policy_param_count(((EnvState*)h)->shape); }
 

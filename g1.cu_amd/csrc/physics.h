@@ -193,6 +193,15 @@ __device__ __forceinline__ float div_rn(float a, float b, float yb) {
   const float q0 = a * yb;
   return __builtin_fmaf(__builtin_fmaf(-q0, b, a), yb, q0);
 }
+// div_rn for numerators that may be infinite (the observation's normalisation: a state set from
+// outside can hold +-inf velocities): the residual of an infinite q0 is NaN, so q0 itself is
+// returned there, which is the IEEE quotient +-inf for an infinite numerator (and, within an ulp
+// of overflow, the same +-inf or FLT_MAX that any later clamp maps alike).
+__device__ __forceinline__ float div_rn_inf(float a, float b, float yb) {
+  const float q0 = a * yb;
+  const float q = __builtin_fmaf(__builtin_fmaf(-q0, b, a), yb, q0);
+  return __builtin_isinf(q0) ? q0 : q;
+}
 __device__ __forceinline__ float rsqrt_rn(float x) { return rcp_rn(sqrtf(x)); }
 // Correctly rounded square root of x >= 2^-96 (and of +0, +inf): the hardware root s is within
 // one ulp, and the residuals x - s_dn s and x - s_up s of its neighbours select RN(sqrt x). The

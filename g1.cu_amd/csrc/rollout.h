@@ -188,7 +188,7 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
       const float o = obs_value(raw[s], qw, qx, qy, qz, k);
       if (valid && t < a.H) a.O[((long)t * N + w) * kObs + k] = o;
       const float m = (&nmean[s >> 2].x)[s & 3], d = (&ndiv[s >> 2].x)[s & 3], y = (&nrcp[s >> 2].x)[s & 3];
-      z = div_rn(o - m, d, y);
+      z = div_rn_inf(o - m, d, y);
       if (z < -10.f) z = -10.f; else if (z > 10.f) z = 10.f;
     }
     x[s] = z;

@@ -116,4 +116,6 @@ void launch_rollout_kernel(const RolloutArgs& ra, int grid) {
   hipLaunchKernelGGL(k_rollout, dim3((unsigned)grid), dim3(kPhysThreads), 0, 0, ra);
 }
 
+const void* rollout_kernel_fn() { return (const void*)k_rollout; }
+
 }  // namespace g1k

@@ -48,6 +48,7 @@ SIGNATURES = {
     "g1_env_get_state": (None, [_vp, _fp, _fp, _fp, _ip]),
     "g1_env_set_policy": (_c.c_int, [_vp, _c.c_int, _ip, _c.c_int]),
     "g1_env_policy_params": (_c.c_long, [_vp]),
+    "g1_env_device_bytes": (_c.c_long, [_vp]),
     "g1_env_set_contact": (None, [_vp, _c.c_float, _c.c_int]),
     "g1_env_ncon_hist": (None, [_vp, _c.c_int, _c.POINTER(_c.c_ulonglong)]),
     "g1_env_profile": (None, [_vp, _c.c_int]),
@@ -192,6 +193,10 @@ class Env:
         out = (_c.c_ulonglong * 9)()
         lib.g1_env_ncon_hist(self.h, int(enable), out)
         return np.array(out[:], np.int64)
+
+    def device_bytes(self):
+        """Device memory the handle holds (state, queue and staging buffers, packed policies)."""
+        return int(lib.g1_env_device_bytes(self.h))
 
     def check(self):
         """Synchronise and return the work queue's error word (0: none)."""

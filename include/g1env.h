@@ -67,17 +67,24 @@ void g1_rollout_ex(void* h, int H, const float* W, const float* mean, const floa
                    const float* reset_noise);
 
 /* g1_rollout_ex that allocates nothing: no counterpart in the reference. For callers that cannot
- * allocate device memory during the call (code under HIP graph capture, tight serving loops,
- * harnesses that forbid allocation). g1_rollout packs the policy weights into a buffer it grows with
- * hipMalloc; this entry point packs them into a fixed device array of the library (640 Ki floats,
- * 2.5 MiB per GPU, held until the process ends), which fits every shape g1_env_set_policy accepts.
- * Returns 0, or -1 (message on stderr) when no env was created on the current device or the packed
- * policy exceeds the array. All calls on one GPU share the array; the library orders its launches on
- * the null stream, so successive calls do not overlap, and callers must not run two of them
- * concurrently on other streams. Asynchronous, like g1_rollout; no profiling events are recorded. */
+ * allocate device memory during the call (tight serving loops, harnesses that forbid allocation).
+ * g1_rollout packs the policy weights into a buffer it grows with hipMalloc; this entry point packs
+ * them into a fixed device array of the library (640 Ki floats, 2.5 MiB per GPU, held until the
+ * process ends), which fits every shape g1_env_set_policy accepts. Returns 0, or -1 (message on
+ * stderr) when no env was created on the current device or the packed policy exceeds the array.
+ * All calls on one GPU share the array; the library orders its launches on the null stream, so
+ * successive calls do not overlap, and callers must not run two of them concurrently on other
+ * streams. Asynchronous, like g1_rollout; no profiling events are recorded. Not for HIP graph
+ * capture: its launches and its closing error-word copy go to the null stream, and it reads the
+ * previous rollout's error word from host memory on entry. */
 int g1_rollout_noalloc(void* h, int H, const float* W, const float* mean, const float* var, float* O, float* A,
                        float* LP, float* V, float* R, float* D, float* Vlast, const float* act_noise,
                        const float* reset_noise);
+
+/* Bytes of device memory the env holds: its state, work-queue and staging buffers from
+ * g1_env_create, plus the packed-policy buffers that g1_rollout and g1_rollout_ex grow on demand
+ * (g1_rollout_noalloc never does). Not the library's file-scope device arrays. */
+long g1_env_device_bytes(void* h);
 
 /* HOST state get/set: qp [N*36], qv [N*35], pa [N*29] previous action, steps [N]. Blocks. */
 void g1_env_set_state(void* h, const float* qp, const float* qv, const float* pa, const int* steps);

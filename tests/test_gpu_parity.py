@@ -66,9 +66,10 @@ def test_env_qacc_gate_states(g1, orc):
 
 @pytest.mark.parametrize("mu", [0.6, 1.0])
 def test_contact_config_states(g1, orc, mu):
-    """Config-2 states (0..8 penetrating spheres, tangential foot velocity) at pgs=8."""
+    """Config 2 at its full size: 8192 states with 0..8 penetrating spheres and tangential foot
+    velocity, pgs=8."""
     import configs
-    qp, qv, k = configs.config2(lambda q: orc.fk(q, dtype=np.float64), n=2048)
+    qp, qv, k = configs.config2(lambda q: orc.fk(q, dtype=np.float64), n=8192)
     Bdt = orc.bdt(np.float32)
     ref, nref = orc.qacc(qp, qv, Bdt=Bdt, pgs=8, mu=mu, dtype=np.float32, threads=8)
     out, nc = gpu_qacc(g1, qp, qv, pgs=8, mu=mu)

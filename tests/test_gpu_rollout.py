@@ -197,15 +197,15 @@ def test_rollout_teacher_forced_one_launch_shapes(g1, orc, hidden, act):
 
 
 def test_one_launch_rollout_equals_step_by_step(g1):
-    """The one-launch rollout cuts a control step into work items by the work per wave: at N=8192
-    and H=8 every step but the last is one item and the last two (6 and 4 substeps); a launch per
-    control step (H=1) cuts each step into 3,3,2,2. Item boundaries only hand a pair's state over
-    and the policy tiles are the same, so one H=8 launch equals eight H=1 launches bit for bit:
-    every trajectory output, the bootstrap value and the final state (with timeouts and auto-resets
-    inside the horizon)."""
-    N, H = 8192, 8
+    """The one-launch rollout cuts a control step into work items by the work per wave: at the
+    benchmark's shape (N=8192, H=32) every step but the last is one item and the last two (6 and 4
+    substeps); a launch per control step (H=1) cuts each step into 3,3,2,2. Item boundaries only
+    hand a pair's state over and the policy tiles are the same, so one H=32 launch equals 32 H=1
+    launches bit for bit: every trajectory output, the bootstrap value and the final state (with
+    timeouts and auto-resets inside the horizon)."""
+    N, H = 8192, 32
     qp, qv, pa, steps, W, mean, var, an, rn = _setup(N, H, 71)
-    steps[::7] = 993 + np.arange(steps[::7].size) % 7   # timeouts and auto-resets inside the horizon
+    steps[::7] = 969 + np.arange(steps[::7].size) % 31   # timeouts and auto-resets inside the horizon
     with g1.Env(N, substeps=10, pgs_iters=8, seed=1) as env:
         env.set_state(qp, qv, pa, steps)
         one = _rollout(g1, env, W, mean, var, H, an, rn)
@@ -393,6 +393,59 @@ def test_host_step_matches_oracle(g1, orc):
     live = dd == 0
     assert np.array_equal(done, dd) and np.array_equal(rew, rr)
     assert np.array_equal(obs1[live], orc.obs(oq, ov, opa)[live])
+
+
+@pytest.mark.parametrize("path", ["host_step", "rollout"])
+def test_velocity_guard_nan_inf_and_clamp(g1, orc, path):
+    """The env's velocity guard (src/g1_env.cu:154-160: a non-finite velocity becomes 0, then the
+    clamp to +-50) on the GPU, against the oracle bit for bit: worlds start with NaN, +-inf and
+    +-1e4 velocities on base and hinge dofs (g1_env_set_state) beside ordinary ones and take one
+    control step through the host-step path (k_physics) or a one-step rollout (k_rollout). The
+    reference's comparison clamps let NaN through everywhere else, as the kernels do: a NaN hinge
+    velocity makes that step's reward NaN and, in the rollout, the world's observation and action
+    NaN; the guard leaves every velocity finite and within +-50."""
+    import configs
+    N = 64
+    rng = np.random.default_rng(91)
+    qp, qv, pa, steps = configs.reset_states(rng, N)
+    qv = rng.normal(0, 0.5, (N, 35)).astype(np.float32)
+    bad = {0: (3, np.nan), 1: (20, np.nan), 2: (0, 1e4), 3: (12, -1e4), 4: (30, np.inf), 5: (5, -np.inf),
+           6: (7, 60.0), 7: (1, -1e4)}
+    for w, (d, v) in bad.items():
+        qv[w, d] = v
+    act = rng.normal(0, 0.3, (N, 29)).astype(np.float32)
+    rn = rng.uniform(-1, 1, (1, N, 29)).astype(np.float32)
+    W = configs.policy_init(rng)
+    mean, var = np.zeros(100, np.float32), np.ones(100, np.float32)
+    with g1.Env(N, substeps=10, pgs_iters=8, seed=4) as env:
+        env.set_state(qp, qv, pa, steps)
+        if path == "host_step":
+            _, rew, done = env.step(act)
+            A = act
+        else:
+            out = _rollout(g1, env, W, mean, var, 1, act[None], rn)
+            rew, done, A = out["R"][0], out["D"][0], out["A"][0]
+        post = env.get_state()
+    if path == "rollout":
+        # the policy from the same state: a NaN velocity makes the observation and every action of
+        # its world NaN; an infinite or huge one is clamped to +-10 after normalisation
+        ref = orc.rollout(*(x.copy() for x in (qp, qv, pa, steps)), W, mean, var, act[None], rn, 1,
+                          threads=NTHREADS)
+        assert np.array_equal(out["O"][0], ref["O"][0], equal_nan=True)
+        assert np.isnan(A[:2]).all() and np.isnan(ref["A"][0][:2]).all() and np.isfinite(A[2:]).all()
+        assert relerr_rows(A[2:], ref["A"][0][2:]).max() <= TOL
+    # the step's physics driven by the GPU's actions, from the same state; the host step resets
+    # finished worlds with the library's own noise (counter 0: no reset or step before it)
+    import philox_np
+    o = [x.copy() for x in (qp, qv, pa, steps)]
+    rst = rn[0] if path == "rollout" else philox_np.uniform_pm1(4, np.arange(N), 0, philox_np.STREAM_RESET)
+    rr, dd = orc.env_advance(*o, A, rst, threads=NTHREADS)
+    print(f"{path}: rewards of the guarded worlds {rew[:8]}; oracle {rr[:8]}")
+    assert np.array_equal(done, dd) and np.array_equal(rew, rr, equal_nan=True)
+    for a, b in zip(post, o):
+        assert np.array_equal(a, b, equal_nan=a.dtype.kind == "f")
+    assert np.isfinite(post.qvel).all() and np.abs(post.qvel).max() <= 50.0
+    assert np.isnan(rew[1]) and not np.isnan(rew[8:]).any() and dd[:8].any()
 
 
 def test_work_queue_matches_small_launch(g1):

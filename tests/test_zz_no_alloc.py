@@ -2,7 +2,8 @@
 the call) against g1_rollout_ex on identical states and noise: every trajectory buffer and the
 final state bit for bit, on two calls in a row, the second with a smaller input (fewer worlds, a
 shorter horizon and a smaller policy, so the array holds a stale, larger packing from the first
-call)."""
+call). Each no-alloc call runs on a fresh env and leaves the env's device memory where creation put
+it (g1_env_device_bytes), while g1_rollout_ex on a fresh env grows it by its packed policy."""
 import numpy as np
 import pytest
 
@@ -30,6 +31,8 @@ def _case(N, H, hidden, seed):
 
 
 def _run(g1, state, inputs, N, H, hidden, act, noalloc):
+    """One rollout on a fresh env; returns the outputs, the final state and the env's device bytes
+    before and after the call."""
     import torch
     dev = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in inputs]
     with g1.Env(N, substeps=10, pgs_iters=8, seed=3) as env:
@@ -37,21 +40,25 @@ def _run(g1, state, inputs, N, H, hidden, act, noalloc):
         env.set_state(*state)
         traj = g1.Trajectory(H, N)
         ptrs = [g1.dev_ptr(t) for t in (*dev[:3], *traj.tensors(), dev[3], dev[4])]
+        before = env.device_bytes()
         if noalloc:
             assert g1.lib.g1_rollout_noalloc(env.h, H, *ptrs) == 0
         else:
             g1.lib.g1_rollout_ex(env.h, H, *ptrs)
         torch.cuda.synchronize()
+        after = env.device_bytes()
         assert env.check() == 0
-        return traj.numpy(), env.get_state()
+        return traj.numpy(), env.get_state(), (before, after)
 
 
 def test_noalloc_rollout_matches_allocating_rollout(g1):
     cases = [(96, 3, (512, 512, 256), 1, 71), (40, 2, (256, 256), 0, 72)]   # second: smaller everything
     for N, H, hidden, act, seed in cases:
         state, inputs = _case(N, H, hidden, seed)
-        ref, ref_state = _run(g1, state, inputs, N, H, hidden, act, noalloc=False)
-        got, got_state = _run(g1, state, inputs, N, H, hidden, act, noalloc=True)
+        ref, ref_state, (b0, b1) = _run(g1, state, inputs, N, H, hidden, act, noalloc=False)
+        got, got_state, (n0, n1) = _run(g1, state, inputs, N, H, hidden, act, noalloc=True)
+        assert b1 > b0, (N, b0, b1)          # the allocating form packed into a buffer it allocated
+        assert n1 == n0 == b0, (N, n0, n1)   # the no-alloc form allocated nothing
         for f in g1.Trajectory.FIELDS:
             assert np.array_equal(got[f], ref[f]), (N, f)
         for a, b in zip(got_state, ref_state):
