@@ -122,9 +122,13 @@ def measure_copy_bandwidth(mib=COPY_MIB, reps=10):
 
 
 # ---------------------------------------------------------------- hardware counters (rocprofv3)
-def counter_child(config):
+STANDING_N, STANDING_K = 8192, 50   # standing regime: worlds, control steps per bench_phys call (the reference's K)
+
+
+def counter_child(config, workload="rollout"):
     """The profiled program: one copy of COPY_MIB MiB (the calibration dispatch), then one warm-up
-    and one timed rollout of the configuration (in the library's default rollout form)."""
+    and one timed rollout of the configuration (in the library's default rollout form), or for the
+    standing workload two physics-only bench calls of STANDING_K control steps after a reset."""
     import torch
     import configs
     import g1env
@@ -134,6 +138,13 @@ def counter_child(config):
     b.copy_(a)
     torch.cuda.synchronize()
     del a, b
+    if workload == "standing":
+        with g1env.Env(STANDING_N, substeps=10, pgs_iters=8, seed=1) as env:
+            env.reset()
+            for _ in range(2):
+                env.bench_phys(STANDING_K)
+            assert env.check() == 0
+        return
     cfg = configs.ROLLOUT_CONFIGS[config]
     N, H = cfg["N"], cfg["H"]
     W = torch.from_numpy(configs.policy_init(np.random.default_rng(1234), hidden=cfg["hidden"])).cuda()
@@ -156,7 +167,7 @@ def _read_counters(outdir):
     return rows
 
 
-def measure_counters(config, kernel, timeout_s=150):
+def measure_counters(config, kernel, timeout_s=150, workload="rollout"):
     """Runs the counter passes on child processes; returns per-dispatch averages for `kernel` and
     the calibration copy, or None with the reason."""
     exe = shutil.which("rocprofv3")
@@ -167,7 +178,8 @@ def measure_counters(config, kernel, timeout_s=150):
     for name, counters in COUNTER_PASSES:
         outdir = tempfile.mkdtemp(prefix=f"g1bench_{name}_", dir="/tmp")
         cmd = [exe, "--pmc", *counters, "--output-format", "csv", "-d", outdir, "-o", "p", "--",
-               sys.executable, os.path.abspath(__file__), "--counter-child", "--config", str(config)]
+               sys.executable, os.path.abspath(__file__), "--counter-child", "--config", str(config),
+               "--workload", workload]
         try:
             p = subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout_s, capture_output=True, text=True)
         except subprocess.TimeoutExpired:
@@ -205,18 +217,25 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-counters", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--counter-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--workload", choices=["rollout", "standing"], default="rollout",
+                    help="rollout: the fused rollout of --config (the headline); standing: the reference's "
+                         "physics-only bench (scripts/bench_env_phys.py: reset, zero action, g1_env_bench_phys) "
+                         "at N=8192, a step being one call of 50 control steps")
     ap.add_argument("--policy", choices=["random", "trained"], default="random",
                     help="random-init weights (the configuration's definition) or the reference's trained "
                          "checkpoint (g1.cu_amd/data/trained_policy_finish_best.npz: walking contact mix)")
     args = ap.parse_args()
     if args.counter_child:
-        counter_child(args.config)
+        counter_child(args.config, args.workload)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: the rollout shards worlds across GPUs with no exchange, "
               "and this build runs on single-GPU boxes only (--gpus 1).", file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == "standing":
+        standing_main(args)
+        return
     import configs
     cfg = configs.ROLLOUT_CONFIGS[args.config]
     # the library runs a two-hidden-layer policy of at most 256 units as one launch (k_rollout)
@@ -353,6 +372,78 @@ def main():
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(cfg, threads)
+    print(json.dumps(out), flush=True)
+
+
+def counter_summary(counters, kernel, avg_launch_s, phys_flops_launch, bw_meas):
+    """The counter block of the JSON line (per dispatch of `kernel`)."""
+    valu = counters.get("SQ_INSTS_VALU")
+    out = {
+        "source": f"rocprofv3 --pmc, one run of this script's counter child ({counters['dispatches']} {kernel} dispatches)",
+        "hbm_bytes_per_dispatch": counters["traffic_bytes"],
+        "hbm_gbs": counters["traffic_bytes"] / avg_launch_s / 1e9,
+        "hbm_frac_of_bw_meas": counters["traffic_bytes"] / avg_launch_s / 1e9 / bw_meas,
+        "fetch_write_scale": [counters["fetch_scale"], counters["write_scale"]],
+        "valu_busy_frac": counters.get("VALUBusy", float("nan")) / 100.0,
+        "valu_lane_utilization": counters.get("VALUUtilization", float("nan")) / 100.0,
+        "valu_insts_per_dispatch": valu,
+        "valu_issue_frac": valu / (rf.VALU_ISSUE_PEAK * avg_launch_s) if valu else None,
+        "physics_flops_per_valu_lane_slot": phys_flops_launch / (valu * 64) if valu else None,
+        "lds_util_frac": counters.get("LdsUtil", float("nan")) / 100.0,
+        "lds_bank_conflict_frac": counters.get("LDSBankConflict", float("nan")) / 100.0,
+        "lds_insts_per_dispatch": counters.get("SQ_INSTS_LDS")}
+    lds_ld, lds_st = counters.get("SQ_INSTS_LDS_LOAD_BANDWIDTH"), counters.get("SQ_INSTS_LDS_STORE_BANDWIDTH")
+    if lds_ld is not None and lds_st is not None:
+        lds_bytes = (lds_ld + lds_st) * 64.0
+        out.update({"lds_bytes_per_dispatch": lds_bytes, "lds_gbs": lds_bytes / avg_launch_s / 1e9,
+                    "lds_frac": lds_bytes / avg_launch_s / 1e9 / rf.LDS_PEAK_GBS})
+    return out
+
+
+def standing_main(args):
+    """The reference's physics-only benchmark (scripts/bench_env_phys.py:15-24 -> g1_env_bench_phys,
+    k_phys_bench, src/g1_env.cu:343-359): N=8192 worlds reset to the stand pose, zero action, the
+    physics of STANDING_K control steps per call (continuous foot contact, 6-8 contacts per world in
+    most substeps). One JSON line like the rollout's, for k_physics."""
+    counters, note = ((None, "skipped (--no-counters)") if args.no_counters
+                      else measure_counters(3, "k_physics", workload="standing"))
+    import torch
+    import g1env
+    N, K, S, pgs = STANDING_N, STANDING_K, 10, 8
+    env = g1env.Env(N, substeps=S, pgs_iters=pgs, seed=1)
+    env.reset()
+    for _ in range(args.warmup):
+        env.bench_phys(K)
+    env.ncon_hist(enable=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        env.bench_phys(K)   # blocks: one k_physics launch of K control steps
+    wall = time.perf_counter() - t0
+    hist = env.ncon_hist(enable=False)
+    if env.check() != 0:
+        sys.exit("physics work queue error: results undefined")
+    env.close()
+    launch_s = wall / args.steps
+    bw_meas = measure_copy_bandwidth()
+    _, flops_total = rf.physics_work(hist, pgs, control_steps_worlds=N * K * args.steps)
+    flops_launch = flops_total / args.steps
+    achieved = flops_launch / launch_s / 1e12
+    roof = {"bound": "valu", "achieved": achieved, "peak": rf.FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": achieved / rf.FP32_PEAK_TFLOPS, "traffic": counters["traffic_bytes"] if counters else None,
+            "kernel": "k_physics", "avg_launch_ms": launch_s * 1e3, "algorithmic_flops_per_launch": flops_launch,
+            "mean_ncon": float((hist * np.arange(9)).sum() / max(hist.sum(), 1)),
+            "frac_of_unpacked_fp32": achieved / rf.FP32_UNPACKED_TFLOPS, "bw_meas_gbs": bw_meas,
+            "counters": (counter_summary(counters, "k_physics", launch_s, flops_launch, bw_meas) if counters
+                         else {"note": note})}
+    out = {"metric": "physics substeps/sec, standing regime (reference scripts/bench_env_phys.py), N=8192, 1 GPU",
+           "value": N * K * S / launch_s, "unit": "substeps/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": launch_s * 1e3, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "fp32",
+           "data": "stand-pose resets (library Philox noise), zero action",
+           "config": {"workload": f"standing: g1_env_bench_phys N={N} K={K} S={S} pgs={pgs}", "N": N, "K": K,
+                      "substeps": S, "pgs": pgs},
+           "roofline": roof, "ncon_hist": hist.tolist()}
     print(json.dumps(out), flush=True)
 
 

@@ -23,6 +23,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "g1_model_tables.h"
 #include "lanes.h"
 #include "tree.h"
@@ -373,37 +375,34 @@ struct SolveParams {
   bool contact;  // foot-ground contact on/off
 };
 
-// One projected Gauss-Seidel sweep over rows II.. of the lane-held columns, fully unrolled with the
-// rows nested: the first row at or past the wave's largest row count nefc_max branches once to the
-// end of the sweep. Row ii's update f_ii = max(0, -(b_ii + A_ii.f - A_ii,ii f_ii) / A_ii,ii)
-// (reference: src/contact.cuh:159-171) is evaluated by every lane and kept by lane ii; a lane without
-// a row (ii >= its world's count) may take it: its column entries are +0, so its f enters no row
-// sum. The quotient x / A_ii uses the correctly rounded reciprocal y = RN(1/A_ii) and one
-// exact-residual correction: q0 = RN(x y), r = x - A_ii q0 (exact with fma), q = RN(q0 + r y) equals
-// RN(x / A_ii) (Markstein's theorem), the IEEE quotient, on a 3-op dependency chain.
-// W: the rows a world can hold in this wave (nefc_max <= W). W = 16: lanes 16..31 hold zero columns
-// and zero f and the row sums skip their stage (gsum16); W = 4 (at most one contact per world):
-// only lanes 0..3 hold nonzero products and the sums take the butterfly's last two stages (gsum4).
-// Either way only the sign of an exactly-zero sum can differ from the full sum's, and only the
-// row's own lane keeps its update.
+// One projected Gauss-Seidel sweep over rows II.. (reference: src/contact.cuh:159-171), in the
+// row-scaled residual form: lane i holds row i scaled by y_i = RN(1/A_ii) with its diagonal entry 0
+// (a_ij = RN(A_ij y_i); A is symmetric bit for bit, so lane i's column of A is its row) and the
+// row's residual r_i = c_i + sum_j a_ij f_j for the current f, c_i = RN(b_i y_i). Row ii: its lane
+// sets f_ii = max(0, -r_ii); the change d = RN(f new - f old) goes from that lane to every lane of
+// the world (group_bcast), and every lane j adds a_j,ii d to r_j in one fma. Every lane evaluates
+// the update and only lane ii keeps it; a lane without a row (i >= its world's count) holds zero
+// entries, r = c = 0 and f = 0. Straight-line rows; the first row at or past the wave's largest row
+// count nefc_max branches once to the end of the sweep. W: the rows a world can hold in this wave
+// (nefc_max <= W): the change is broadcast over the group (32), its first 16-lane row (16) or its
+// first quad (4); lanes past W hold no row and their r is never read.
 template <int II, int W>
-__device__ __forceinline__ void pgs_sweep(const float (&Acol)[kMaxEfc], float Aii, float yi, float bi, int l,
-                                          int nefc_max, float& fi) {
+__device__ __forceinline__ void pgs_sweep(const float (&Acol)[kMaxEfc], int l, int nefc_max, float& fi, float& ri) {
   if constexpr (II < W) {
     if (II < nefc_max) {
-      // sum_j A[II][j] f_j (lane j holds column j)
-      const float pr = Acol[II] * fi;
-      const float sum = W == 4 ? gsum4(pr) : (W == 16 ? gsum16(pr) : gsum(pr));
-      const float ri = fmaf_(-Aii, fi, bi + sum);
-      const float x = -ri;
-      const float q0 = x * yi;
-      const float fn = __builtin_fmaf(__builtin_fmaf(-q0, Aii, x), yi, q0);
-      const float fnew = fn > 0.f ? fn : 0.f;
-      fi = (l == II) ? fnew : fi;
-      pgs_sweep<II + 1, W>(Acol, Aii, yi, bi, l, nefc_max, fi);
+      const float t = -ri;
+      const float fn = t > 0.f ? t : 0.f;
+      const float d = fn - fi;
+      fi = (l == II) ? fn : fi;
+      ri = fmaf_(Acol[II], group_bcast<II, W>(d), ri);
+      pgs_sweep<II + 1, W>(Acol, l, nefc_max, fi, ri);
     }
   }
 }
+
+// Sweeps between the fresh residuals of the PGS (a fresh residual r_i = c_i + sum_k a_ik f_k, k in
+// order, bounds the rounding the row updates carry over long solves).
+constexpr int kPgsRefresh = 8;
 
 // Free joint of one M^-1 solve column (reference: src/aba_factor.cuh:139-155): D qdd = x_b -
 // S_base.pA_1 with the factored D = L L' in LDS (forward, then backward substitution, each quotient
@@ -1468,40 +1467,49 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       float val = fmaf_(t2, dh2, fmaf_(t1, dh1, t0 * 1.f));
       const bool diag = eq && k2 == ki;
       val = diag ? val + Rci : val;
-      Acol[4 * c2 + k2] = keep ? val : 0.f;
+      Acol[4 * c2 + k2] = (keep && !diag) ? val : 0.f;   // the diagonal is held apart (Aii)
       Aii = (diag && row) ? val : Aii;
     }
   }
   const float bi = row ? s.bvec[l] : 0.f;
 
-  // ---------------- projected Gauss-Seidel (reference: src/contact.cuh:159-171), P.pgs sweeps
+  // ---------------- projected Gauss-Seidel (reference: src/contact.cuh:159-171), P.pgs sweeps, in
+  // the row-scaled residual form of pgs_sweep. A sweep that leaves every f of a world bit-for-bit
+  // unchanged ends that world's solve: without a fresh residual in between, every later sweep would
+  // repeat it exactly (its changes are all +0), and the world takes no fresh residual after it; the
+  // wave stops once both worlds are done.
   float fi = 0.f;
   const float yi = rcp_rn(Aii);
-  // A sweep that leaves every f of the wave bit-for-bit unchanged is a fixed point: every later
-  // sweep would repeat it exactly, so the sweeps stop there with the same result.
-  auto moved = [&](float f0) { return __ballot(__float_as_uint(fi) != __float_as_uint(f0)) != 0ull; };
-  if (nefc_max <= 4) {
+  const float cb = bi * yi;
+  float ri = cb;
+  auto solve = [&](auto wc) {
+    constexpr int W = decltype(wc)::value;
+#pragma unroll
+    for (int ii = 0; ii < W; ++ii) Acol[ii] = Acol[ii] * yi;
+    bool done = false;   // this world's solve has ended
 #pragma unroll 1
     for (int it = 0; it < P.pgs; ++it) {
+      if (it > 0 && it % kPgsRefresh == 0) {
+        // fresh residuals: every lane reads every f of its world
+        s.f[l] = fi;
+        wave_sync();
+        float t = cb;
+#pragma unroll
+        for (int k = 0; k < W; ++k)
+          if (k < nefc_max) t = fmaf_(Acol[k], s.f[k], t);
+        wave_sync();
+        ri = done ? ri : t;
+      }
       const float f0 = fi;
-      pgs_sweep<0, 4>(Acol, Aii, yi, bi, l, nefc_max, fi);
-      if (!moved(f0)) break;
+      pgs_sweep<0, W>(Acol, l, nefc_max, fi, ri);
+      const unsigned long long m = __ballot(__float_as_uint(fi) != __float_as_uint(f0));
+      if (m == 0ull) break;
+      done = done || ((unsigned)(m >> (32 * group_id())) == 0u);
     }
-  } else if (nefc_max <= kGroup / 2) {
-#pragma unroll 1
-    for (int it = 0; it < P.pgs; ++it) {
-      const float f0 = fi;
-      pgs_sweep<0, kGroup / 2>(Acol, Aii, yi, bi, l, nefc_max, fi);
-      if (!moved(f0)) break;
-    }
-  } else {
-#pragma unroll 1
-    for (int it = 0; it < P.pgs; ++it) {
-      const float f0 = fi;
-      pgs_sweep<0, kMaxEfc>(Acol, Aii, yi, bi, l, nefc_max, fi);
-      if (!moved(f0)) break;
-    }
-  }
+  };
+  if (nefc_max <= 4) solve(std::integral_constant<int, 4>());
+  else if (nefc_max <= kGroup / 2) solve(std::integral_constant<int, kGroup / 2>());
+  else solve(std::integral_constant<int, kMaxEfc>());
   __builtin_amdgcn_s_setprio(0);
   if (row) s.f[l] = fi;
   wave_sync();

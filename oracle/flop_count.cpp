@@ -62,6 +62,7 @@ inline F pow_(F x, F y) { ++cnt.trans; return F((float)std::pow((double)x.v, (do
 inline F tanh_(F x) { ++cnt.trans; return F(std::tanh(x.v)); }
 inline F expm1_(F x) { ++cnt.trans; return F(std::expm1(x.v)); }
 inline F exp_(F x) { ++cnt.trans; return F(std::exp(x.v)); }
+inline unsigned long long bits_of(F x) { unsigned u; std::memcpy(&u, &x.v, 4); return u; }
 
 }  // namespace flc
 

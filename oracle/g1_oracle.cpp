@@ -358,9 +358,10 @@ template <class R> void compute_bias(const R* qvel, const Frames<R>& F, R* S, R*
 //  * the contact basis columns (M + dtB)^-1 e_{c,a}: the kernel solves them in the single
 //    right-hand-side form (reference src/aba_factor.cuh:121-165, solveM below), the reference in
 //    its K = 1 multi-RHS form (src/aba_solvem_multi.cuh:21-125, solveM_multi1);
-//  * the PGS row sum sum_j A_ij f_j: the kernel rounds each product and sums the 32 lanes of a
-//    world by an xor butterfly (16, 8, 4, 2, 1), then adds b_i; the reference accumulates
-//    b_i + A_i0 f_0 + ... serially with fused multiply-adds (src/contact.cuh:159-171);
+//  * the PGS row sums: the kernel scales row i by RN(1/A_ii) once and keeps each row's residual
+//    r_i = c_i + sum_{j != i} a_ij f_j up to date by one fused multiply-add per row update (see
+//    solve_pgs); the reference accumulates b_i + A_i0 f_0 + ... serially with fused multiply-adds
+//    and divides by A_ii (src/contact.cuh:159-171);
 //  * the control step's energy and action-change penalty: the kernel sums each actuator's terms
 //    over the substeps on its own lane (lane = body = actuator + 2) and the lanes by the butterfly,
 //    the reference serially over substeps and actuators (src/g1_env.cu:150-151,186-188).
@@ -630,26 +631,67 @@ template <class R> R foot_impedance(R pos) {
   return fma_(y, dmax - dmin, dmin);
 }
 
-// Projected Gauss-Seidel on min 0.5 f'Af + f'b, f >= 0 (reference: src/contact.cuh:159-171)
-// (row sum associated as selected by g_ref_order; n <= 32 in the kernel's association)
+static inline uint64_t bits_of(float x) { uint32_t u; std::memcpy(&u, &x, 4); return u; }
+static inline uint64_t bits_of(double x) { uint64_t u; std::memcpy(&u, &x, 8); return u; }
+
+// Sweeps between the fresh residuals of the kernel's PGS association (solve_pgs).
+constexpr int kPgsRefresh = 8;
+
+// Projected Gauss-Seidel on min 0.5 f'Af + f'b, f >= 0 (reference: src/contact.cuh:159-171):
+// f_i = max(0, -(b_i + sum_{j != i} A_ij f_j) / A_ii), rows in order, `iters` sweeps from f = 0.
+// Reference association (g_ref_order, or n > 32): the row sum b_i + A_i0 f_0 + ... serially in
+// fused multiply-adds, minus A_ii f_i, divided by A_ii.
+// Kernel association (n <= 32): row i is scaled once by y_i = RN(1/A_ii), a_ij = RN(A_ij y_i) off
+// the diagonal (a_ii = 0) and c_i = RN(b_i y_i), and each row keeps its residual
+// r_i = c_i + sum_j a_ij f_j current: r = c at f = 0; a row update sets f_i = max(0, -r_i) and adds
+// a_ji d to every r_j (one fma each, j = 0..31 in the kernel's lanes, d = RN(f_i new - f_i old)).
+// So a row costs no sum and no division. Every kPgsRefresh-th sweep starts from fresh residuals
+// (r_i = c_i, then fma(a_ik, f_k, r_i) over k in order), which bounds the rounding carried by the
+// updates over long solves; and the sweeps stop after the first sweep that changes no f bit for
+// bit. Before a fresh residual that stop changes nothing (the next sweep would repeat the last
+// exactly); after one it is part of this association. Against the reference association: qacc
+// within 5e-6 relative on the gate and config-2 state families at 8 sweeps, and the MuJoCo contact
+// fixture at 2000 sweeps as close as with the reference's sums (tests/test_oracle_fixtures.py,
+// tests/test_gpu_parity.py).
 template <class R> void solve_pgs(const R* A, const R* b, R* f, int n, int iters) {
   for (int i = 0; i < n; ++i) f[i] = 0;
-  for (int it = 0; it < iters; ++it)
-    for (int i = 0; i < n; ++i) {
-      R Aii = A[i * n + i];
-      R ri;
-      if (g_ref_order || n > 32) {
-        ri = b[i];
+  if (g_ref_order || n > 32) {
+    for (int it = 0; it < iters; ++it)
+      for (int i = 0; i < n; ++i) {
+        R Aii = A[i * n + i];
+        R ri = b[i];
         for (int j = 0; j < n; ++j) ri = fma_(A[i * n + j], f[j], ri);
         ri = fma_(-Aii, f[i], ri);
-      } else {
-        R p[32];
-        for (int j = 0; j < 32; ++j) p[j] = j < n ? A[i * n + j] * f[j] : R(0);
-        ri = fma_(-Aii, f[i], b[i] + butterfly32(p));
+        R fi = -ri / Aii;
+        f[i] = fi > R(0) ? fi : R(0);
       }
-      R fi = -ri / Aii;
-      f[i] = fi > R(0) ? fi : R(0);
+    return;
+  }
+  R a[32][32], c[32], r[32];
+  for (int i = 0; i < n; ++i) {
+    const R y = R(1) / A[i * n + i];
+    for (int j = 0; j < n; ++j) a[i][j] = j == i ? R(0) : A[i * n + j] * y;
+    c[i] = b[i] * y;
+    r[i] = c[i];
+  }
+  for (int it = 0; it < iters; ++it) {
+    if (it > 0 && it % kPgsRefresh == 0)
+      for (int i = 0; i < n; ++i) {
+        R t = c[i];
+        for (int k = 0; k < n; ++k) t = fma_(a[i][k], f[k], t);
+        r[i] = t;
+      }
+    bool moved = false;
+    for (int i = 0; i < n; ++i) {
+      const R t = -r[i];
+      const R fn = t > R(0) ? t : R(0);
+      const R d = fn - f[i];
+      if (bits_of(fn) != bits_of(f[i])) moved = true;
+      f[i] = fn;
+      for (int j = 0; j < n; ++j) r[j] = fma_(a[j][i], d, r[j]);
     }
+    if (!moved) break;
+  }
 }
 
 // Intermediates of one contact solve, exposed for debugging and tests.
