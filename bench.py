@@ -8,8 +8,8 @@ A "step" is one fused rollout (one g1_rollout call: H control steps x S substeps
 with the policy weights and frozen statistics already resident in HBM. Prints ONE JSON line.
 
 The dominant kernel is k_rollout (the whole rollout in one launch: physics work items and the
-policy of 16-world tiles) when the policy shape runs in one launch (two hidden layers of at most
-256, config 3), else k_physics (config 4's three-layer policy takes per-step launches). The physics
+policy of 16-world tiles; config 4's three-layer policy runs on the wide tile), or k_physics with
+--per-step (the policy and physics launched once per control step). The physics
 runs out of registers and LDS and is bound by VALU issue, so `achieved` is the launch's algorithmic
 FLOP rate: the reference algorithm's floating-point operations per world-substep by contact count
 (g1.cu_amd/roofline.py, counted by an instrumented oracle) summed over the launch's measured contact
@@ -125,7 +125,7 @@ def measure_copy_bandwidth(mib=COPY_MIB, reps=10):
 STANDING_N, STANDING_K = 8192, 50   # standing regime: worlds, control steps per bench_phys call (the reference's K)
 
 
-def counter_child(config, workload="rollout"):
+def counter_child(config, workload="rollout", per_step=False):
     """The profiled program: one copy of COPY_MIB MiB (the calibration dispatch), then one warm-up
     and one timed rollout of the configuration (in the library's default rollout form), or for the
     standing workload two physics-only bench calls of STANDING_K control steps after a reset."""
@@ -151,6 +151,7 @@ def counter_child(config, workload="rollout"):
     mean, var = torch.zeros(100, device="cuda"), torch.ones(100, device="cuda")
     with g1env.Env(N, substeps=cfg["S"], pgs_iters=cfg["pgs"], seed=1) as env:
         env.set_policy(cfg["hidden"], cfg["act"])
+        env.set_fused(not per_step)
         env.reset()
         traj = g1env.Trajectory(H, N)
         for _ in range(2):
@@ -167,7 +168,7 @@ def _read_counters(outdir):
     return rows
 
 
-def measure_counters(config, kernel, timeout_s=150, workload="rollout"):
+def measure_counters(config, kernel, timeout_s=150, workload="rollout", per_step=False):
     """Runs the counter passes on child processes; returns per-dispatch averages for `kernel` and
     the calibration copy, or None with the reason."""
     exe = shutil.which("rocprofv3")
@@ -179,7 +180,7 @@ def measure_counters(config, kernel, timeout_s=150, workload="rollout"):
         outdir = tempfile.mkdtemp(prefix=f"g1bench_{name}_", dir="/tmp")
         cmd = [exe, "--pmc", *counters, "--output-format", "csv", "-d", outdir, "-o", "p", "--",
                sys.executable, os.path.abspath(__file__), "--counter-child", "--config", str(config),
-               "--workload", workload]
+               "--workload", workload] + (["--per-step"] if per_step else [])
         try:
             p = subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout_s, capture_output=True, text=True)
         except subprocess.TimeoutExpired:
@@ -217,6 +218,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-counters", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--counter-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--per-step", action="store_true",
+                    help="launch the policy and the physics once per control step instead of one k_rollout")
     ap.add_argument("--workload", choices=["rollout", "standing"], default="rollout",
                     help="rollout: the fused rollout of --config (the headline); standing: the reference's "
                          "physics-only bench (scripts/bench_env_phys.py: reset, zero action, g1_env_bench_phys) "
@@ -226,7 +229,7 @@ def main():
                          "checkpoint (g1.cu_amd/data/trained_policy_finish_best.npz: walking contact mix)")
     args = ap.parse_args()
     if args.counter_child:
-        counter_child(args.config, args.workload)
+        counter_child(args.config, args.workload, args.per_step)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: the rollout shards worlds across GPUs with no exchange, "
@@ -239,11 +242,13 @@ def main():
     import configs
     cfg = configs.ROLLOUT_CONFIGS[args.config]
     # the library runs a two-hidden-layer policy of at most 256 units as one launch (k_rollout)
-    one_launch = len(cfg["hidden"]) == 2 and max(cfg["hidden"]) <= 256
+    # every accepted policy shape runs as one launch (k_rollout) unless --per-step asks for the
+    # policy and physics launches per control step
+    one_launch = not args.per_step
     kernel = "k_rollout" if one_launch else "k_physics"
     # counter passes first, while this process has not touched the GPU
     counters, counter_note = ((None, "skipped (--no-counters)") if args.no_counters
-                              else measure_counters(args.config, kernel))
+                              else measure_counters(args.config, kernel, per_step=args.per_step))
 
     import torch
     import g1env
@@ -251,7 +256,7 @@ def main():
     rng = np.random.default_rng(1234)
     env = g1env.Env(N, substeps=S, pgs_iters=pgs, seed=1)
     env.set_policy(cfg["hidden"], cfg["act"])
-    if env.set_fused(True) != one_launch:
+    if env.set_fused(one_launch) != one_launch:
         sys.exit("rollout form differs from the one this script expects")
     env.reset()
     if args.policy == "trained":

@@ -36,9 +36,13 @@ FLAGS = [
 # ms); k_physics and k_policy since the physics lost its force broadcast and select cascades
 # (config 4 rollout 185.4 -> 183.5 ms; with the older physics the same flag had made it 3% slower)
 ILP_FIRST = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
+# k_rollout's policy tiles keep their MFMA accumulators in VGPRs: the physics items need ~230
+# VGPRs, which the policy path does not use at the same time, while accumulators in AGPRs add to
+# that count (the wide tile's 8 groups of accumulators took 48 AGPRs: 278 registers, one wave per SIMD)
+MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 SOURCES = (
     ("g1env.hip", ILP_FIRST),
-    ("rollout_kernel.hip", ILP_FIRST),
+    ("rollout_kernel.hip", ILP_FIRST + MFMA_VGPR),
 )
 
 

@@ -152,6 +152,62 @@ __global__ void k_pack_tiles(TilePackArgs a) {
   a.Wt[idx] = v;
 }
 
+// Pack torch-order weights (W0, b0, .., Wmu, bmu, Wv, bv, log_std) of a policy of nl hidden layers
+// into the wide tile's layout (WideLayout).
+struct WidePackArgs {
+  const float* W; const float* mean; const float* var; float* Wt; WideLayout wl; int hid[kMaxLayers];
+};
+__global__ void k_pack_wide(WidePackArgs a) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const WideLayout& T = a.wl;
+  if (idx >= T.total) return;
+  float v = 0.f;
+  if (idx >= T.nrm_off) {
+    // normalisation constants of feature 4 s + g at [c][g][s] (the divisor as the split policy's)
+    const int rel = (int)(idx - T.nrm_off), c = rel / (4 * kObsSteps), r = rel - c * 4 * kObsSteps;
+    const int g = r / kObsSteps, k = 4 * (r - g * kObsSteps) + g;
+    if (k < kObs) {
+      const float dv = sqrtf(a.var[k] + 1e-8f);
+      v = c == 0 ? a.mean[k] : (c == 1 ? dv : rcp_rn(dv));
+    } else {
+      v = c == 0 ? 0.f : 1.f;
+    }
+  } else {
+    // torch offsets of the layers before Ly, and of the head's parts
+    int Ly = 0;
+    while (Ly < T.nl && idx >= T.woff[Ly + 1]) ++Ly;
+    long oW = 0;
+    int in = kObs;
+    for (int q = 0; q < T.nl && q < Ly; ++q) { oW += (long)a.hid[q] * in + a.hid[q]; in = a.hid[q]; }
+    if (idx >= T.ls_off) {
+      long oh = 0;
+      int hin = kObs;
+      for (int q = 0; q < T.nl; ++q) { oh += (long)a.hid[q] * hin + a.hid[q]; hin = a.hid[q]; }
+      const int i = (int)(idx - T.ls_off);
+      v = i < kAct ? a.W[oh + (long)kAct * hin + kAct + hin + 1 + i] : 0.f;
+    } else {
+      const bool head = Ly == T.nl;
+      const long oWv = oW + (long)kAct * in + kAct;   // head: Wv, then bv after it
+      if (idx >= T.boff[Ly]) {
+        const int row = (int)(idx - T.boff[Ly]);
+        if (!head) v = row < a.hid[Ly] ? a.W[oW + (long)a.hid[Ly] * in + row] : 0.f;
+        else v = row < kAct ? a.W[oW + (long)kAct * in + row] : (row == kAct ? a.W[oWv + in] : 0.f);
+      } else {
+        const long rel = idx - T.woff[Ly];
+        const int e = (int)(rel & 3), lane = (int)((rel >> 2) & 63);
+        const long rq = rel >> 8;
+        const int qd = (int)(rq % T.nQ[Ly]), ot = (int)(rq / T.nQ[Ly]);
+        const int row = 16 * ot + (lane & 15), k = tile_kappa(Ly, 4 * qd + e, lane >> 4);
+        if (k < in) {
+          if (!head) v = row < a.hid[Ly] ? a.W[oW + (long)row * in + k] : 0.f;
+          else v = row < kAct ? a.W[oW + (long)row * in + k] : (row == kAct ? a.W[oWv + k] : 0.f);
+        }
+      }
+    }
+  }
+  a.Wt[idx] = v;
+}
+
 // XCD of each block of a grid shaped like k_physics' (placement check of the work queue)
 __global__ void __launch_bounds__(kPhysThreads) k_xcc(int* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
@@ -521,6 +577,8 @@ struct EnvState {
   unsigned tdone;
   float* Wt;
   long Wt_cap;
+  float* scr;       // wide one-launch policy: per block two activation buffers (WideLayout::maxT * 256 floats each)
+  long scr_cap;
   int* h_qerr;      // pinned copy of qerr, refreshed asynchronously after every rollout
   // per-launch HIP events of the rollout's physics / policy kernels (null stream)
   int prof_on;
@@ -734,11 +792,17 @@ static void poll_queue_error(EnvState* E) {
   check_queue_error(*(volatile int*)E->h_qerr);
 }
 
-// The one-launch rollout covers policies of two hidden layers of at most 256 units each (run at
-// 256-256 with zero padding); other shapes take the split form (policy and physics launches per
-// control step).
-static bool fused_shape(const PolicyShape& sh) {
+// The one-launch rollout runs policies of two hidden layers of at most 256 units each on the
+// register-resident tile (policy_tile, at 256-256 with zero padding) and every other accepted shape
+// (1..3 hidden layers of at most 512 units) on the wide tile (policy_tile_wide, activations staged
+// in global memory). The split form (policy and physics launches per control step) remains for
+// g1_env_set_fused(h, 0) and for g1_rollout_noalloc with a wide shape (the wide tile's activation
+// buffers are allocated by the library).
+static bool narrow_shape(const PolicyShape& sh) {
   return sh.nl == 2 && sh.hid[0] <= kTileMaxHidden && sh.hid[1] <= kTileMaxHidden;
+}
+static bool fused_shape(const PolicyShape& sh, bool noalloc) {
+  return narrow_shape(sh) || !noalloc;
 }
 
 static int tiles_per_queue(int N) {
@@ -752,20 +816,38 @@ static int tiles_per_queue(int N) {
 static void rollout_fused(EnvState* E, int H, const float* W, const float* mean, const float* var, float* O, float* A,
                           float* LP, float* V, float* R, float* D, float* Vlast, const float* act_noise,
                           const float* reset_noise, float* wp, long wp_cap) {
+  const bool wide = !narrow_shape(E->shape);
   const TileLayout tl = tile_layout(E->shape.act);
+  const WideLayout wl = wide_layout(E->shape.nl, E->shape.hid, E->shape.act);
+  const long total = wide ? wl.total : tl.total;
   float* Wt = wp;
   if (!Wt) {
-    if (tl.total > E->Wt_cap) {
+    if (total > E->Wt_cap) {
       if (E->Wt) dev_free(E, E->Wt, E->Wt_cap * sizeof(float));
-      dev_alloc(E, &E->Wt, tl.total * sizeof(float));
-      E->Wt_cap = tl.total;
+      dev_alloc(E, &E->Wt, total * sizeof(float));
+      E->Wt_cap = total;
     }
     Wt = E->Wt;
-  } else if (tl.total > wp_cap) {
+  } else if (total > wp_cap) {
     fail("rollout: tile-packed policy larger than its buffer");
   }
-  TilePackArgs pk{W, mean, var, Wt, tl, E->shape.hid[0], E->shape.hid[1]};
-  hipLaunchKernelGGL(k_pack_tiles, dim3((unsigned)((tl.total + 255) / 256)), dim3(256), 0, 0, pk);
+  float* scr = nullptr;
+  if (wide) {
+    if (wp) fail("rollout: the wide one-launch policy needs the library's activation buffers");
+    const long need = (long)E->pgrid * 2 * wl.maxT * 256;
+    if (need > E->scr_cap) {
+      if (E->scr) dev_free(E, E->scr, E->scr_cap * sizeof(float));
+      dev_alloc(E, &E->scr, need * sizeof(float));
+      E->scr_cap = need;
+    }
+    scr = E->scr;
+    WidePackArgs pk{W, mean, var, Wt, wl, {0, 0, 0, 0}};
+    for (int i = 0; i < E->shape.nl; ++i) pk.hid[i] = E->shape.hid[i];
+    hipLaunchKernelGGL(k_pack_wide, dim3((unsigned)((wl.total + 255) / 256)), dim3(256), 0, 0, pk);
+  } else {
+    TilePackArgs pk{W, mean, var, Wt, tl, E->shape.hid[0], E->shape.hid[1]};
+    hipLaunchKernelGGL(k_pack_tiles, dim3((unsigned)((tl.total + 255) / 256)), dim3(256), 0, 0, pk);
+  }
   HIPCHECK(hipGetLastError());
   RolloutArgs ra{};
   ra.ph = phys_args(E);
@@ -775,7 +857,7 @@ static void rollout_fused(EnvState* E, int H, const float* W, const float* mean,
   a.fbase = E->qdone;
   a.qpar = E->qpar;
   a.xlocal = E->xlocal && !E->fences;
-  ra.po = TileArgs{Wt, tl, act_noise, O, A, LP, V, Vlast, H};
+  ra.po = TileArgs{Wt, tl, act_noise, O, A, LP, V, Vlast, H, wide ? 1 : 0, wl, scr};
   ra.tflags = E->tflags;
   ra.tbase = E->tdone;
   ra.tcount = E->tcount;
@@ -795,7 +877,7 @@ static void rollout_impl(EnvState* E, int H, const float* W, const float* mean, 
                          const float* reset_noise, float* wp = nullptr, long wp_cap = 0) {
   poll_queue_error(E);
   if (H < 0) H = 0;   // no control step; the bootstrap value is still computed (as the reference's k_rollout)
-  if (E->fused && fused_shape(E->shape)) {
+  if (E->fused && fused_shape(E->shape, wp != nullptr)) {
     rollout_fused(E, H, W, mean, var, O, A, LP, V, R, D, Vlast, act_noise, reset_noise, wp, wp_cap);
     return;
   }
@@ -923,7 +1005,8 @@ void g1_env_destroy(void* h) {
   check_queue(E);
   void* bufs[] = {E->qp,       E->qv,      E->pa,        E->steps,   E->rng,  E->dact,
                   E->zero_act, E->bench_r, E->bench_d,   E->ncon_hist, E->Wp,  E->dout,
-                  E->qflags,   E->qctr,    E->qerr,      E->qacc_e,  E->qacc_vx, E->tflags, E->tcount, E->Wt};
+                  E->qflags,   E->qctr,    E->qerr,      E->qacc_e,  E->qacc_vx, E->tflags, E->tcount, E->Wt,
+                  E->scr};
   for (void* b : bufs)
     if (b) HIPCHECK(hipFree(b));
   if (E->h_act) HIPCHECK(hipHostFree(E->h_act));
@@ -1054,7 +1137,8 @@ void g1_occupancy_report(void) {
   printf("%s (%s): %d CUs, LDS/block %zu B, regs/block %d\n", p.name, p.gcnArchName, p.multiProcessorCount,
          p.sharedMemPerBlock, p.regsPerBlock);
   struct { const char* nm; const void* fn; int threads; size_t smem; } ks[] = {
-      {"k_rollout", rollout_kernel_fn(), kPhysThreads, 0},
+      {"k_rollout", rollout_kernel_fn(false), kPhysThreads, 0},
+      {"k_rollout (wide)", rollout_kernel_fn(true), kPhysThreads, 0},
       {"k_physics", (const void*)k_physics, kPhysThreads, 0},
       {"k_policy", (const void*)k_policy, kPolicyThreads, policy_smem(PolicyShape{2, {256, 256, 0, 0}, 0})},
       {"k_probe", (const void*)k_probe, kPhysThreads, 0}};
@@ -1063,7 +1147,7 @@ void g1_occupancy_report(void) {
     HIPCHECK(hipFuncGetAttributes(&fa, k.fn));
     int mb = 0;
     HIPCHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&mb, k.fn, k.threads, k.smem));
-    printf("  %-10s regs=%d scratch=%zuB lds=%zuB maxBlocks/CU=%d waves/CU=%d\n", k.nm, fa.numRegs, fa.localSizeBytes,
+    printf("  %-17s regs=%d scratch=%zuB lds=%zuB maxBlocks/CU=%d waves/CU=%d\n", k.nm, fa.numRegs, fa.localSizeBytes,
            fa.sharedSizeBytes + k.smem, mb, mb * k.threads / 64);
   }
 }
@@ -1162,7 +1246,7 @@ int g1_env_set_fused(void* h, int on) {
   EnvState* E = (EnvState*)h;
   if (on != 0 && on != 1) return -1;
   E->fused = on;
-  return (on && !fused_shape(E->shape)) ? 1 : 0;
+  return (on && !fused_shape(E->shape, false)) ? 1 : 0;
 }
 
 int g1_env_set_handover(void* h, int fences) {

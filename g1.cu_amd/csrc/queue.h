@@ -268,7 +268,7 @@ __device__ __forceinline__ const T& kernarg_reread() {
 
 // Enqueue the one-launch rollout kernel on the null stream (rollout_kernel.hip).
 void launch_rollout_kernel(const RolloutArgs& ra, int grid);
-// k_rollout's function handle (occupancy report).
-const void* rollout_kernel_fn();
+// k_rollout's function handles (occupancy report): the register-resident policy tile, or the wide one.
+const void* rollout_kernel_fn(bool wide);
 
 }  // namespace g1k

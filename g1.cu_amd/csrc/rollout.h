@@ -71,12 +71,55 @@ __host__ __device__ __forceinline__ int tile_kappa(int L, int s, int g) {
   return L == 0 ? 4 * s + g : 16 * (s >> 2) + 4 * g + (s & 3);
 }
 
+// Packed layout of a policy of 1..3 hidden layers of at most 512 units (any activation) for the
+// wide tile (policy_tile_wide), in floats: per layer L (the head last) the weights as
+// [T][q][lane][4] (T: 16-row output tile, q: k-quad of four k-steps, lane (row j = lane mod 16,
+// group g = lane / 16) holds W[16 T + j][kappa(L, 4 q + e, g)] in element e) and the bias in
+// natural row order; then the log standard deviation and the normalisation constants as in
+// TileLayout. A hidden layer's output tiles are padded to a multiple of kWideGroup (zero rows:
+// act(0) = 0 adds exact zeros downstream); the head has kHeadT tiles (mu 0..28, value 29).
+constexpr int kWideMaxLayers = 4;   // hidden layers + head
+constexpr int kWideGroup = 8;       // output tiles a wave accumulates at once (independent chains)
+struct WideLayout {
+  int nl;                           // hidden layers (1..3)
+  int nT[kWideMaxLayers];           // output tiles of layer L
+  int nQ[kWideMaxLayers];           // k-quads of layer L (layer 0: the observation's kObsSteps / 4)
+  long woff[kWideMaxLayers], boff[kWideMaxLayers];
+  long ls_off, nrm_off, total;
+  int maxT;                         // output tiles of the widest hidden layer
+  int act;                          // 0 tanh, 1 ELU
+};
+
+static_assert(kWideGroup % 2 == 0, "hidden layers feed the next layer an even number of k-quads");
+__host__ __device__ inline WideLayout wide_layout(int nl, const int* hid, int act) {
+  WideLayout t{};
+  t.nl = nl;
+  t.act = act;
+  long off = 0;
+  for (int L = 0; L <= nl; ++L) {
+    t.nT[L] = L < nl ? (hid[L] + 16 * kWideGroup - 1) / (16 * kWideGroup) * kWideGroup : kHeadT;
+    t.nQ[L] = L == 0 ? kObsSteps / 4 : t.nT[L - 1];
+    t.woff[L] = off;
+    off += (long)t.nT[L] * t.nQ[L] * 64 * 4;
+    t.boff[L] = off;
+    off += (long)t.nT[L] * 16;
+    if (L < nl && t.nT[L] > t.maxT) t.maxT = t.nT[L];
+  }
+  t.ls_off = off;
+  t.nrm_off = off + 32;
+  t.total = t.nrm_off + 3 * 4 * kObsSteps;
+  return t;
+}
+
 struct TileArgs {
-  const float* Wt;          // packed (TileLayout)
+  const float* Wt;          // packed (TileLayout, or WideLayout when wide)
   TileLayout tl;
   const float* act_noise;   // [H][N][29] or null (Philox)
   float* O; float* A; float* LP; float* V; float* Vlast;
   int H;
+  int wide;                 // 1: the wide tile (policy_tile_wide) on WideLayout wl
+  WideLayout wl;
+  float* scr;               // wide tile: per block, two activation buffers of wl.maxT * 256 floats
 };
 
 // The 16 worlds of tile u of queue q: pairs p = q + 32 (8 u + i), i < 8, worlds 2p and 2p + 1;
@@ -121,29 +164,19 @@ __device__ __forceinline__ float obs_value(float raw, float qw, float qx, float 
 
 constexpr int kTileLds = kTileW * 32 + 2 * kTileMaxHidden;   // LDS floats of one tile's policy
 
-// Policy of control step t (t == H: the bootstrap value only) for the tile's worlds w_j, given by
-// the caller (valid: w_j < N). State is read with `ld` (from the L2: other waves of the launch
-// wrote it). hid: LDS scratch of kTileLds floats: the log-prob terms (kTileW x 32), then the two
-// layers' biases.
-template <int ACT, class LoadT>
-__device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos, const float* qvel, const float* pact,
-                                            const unsigned* rngc, unsigned long long seed, int N, int t, int w,
-                                            bool valid, float* hid, LoadT ld) {
-  // the lane index goes through an opaque asm so that nothing derived from it is hoisted out of the
-  // caller's item loop (where it would stay live beside the physics items' registers)
-  int lane = threadIdx.x & 63;
-  __asm__ volatile("" : "+v"(lane));
-  const int j = lane & 15, g = lane >> 4;
-  const TileLayout& T = a.tl;
+// ---- observation (raw to O, reference: src/g1_env.cu:69-81) and frozen normalisation (:298-302)
+// of a tile's worlds: lane (j, g) forms features 4 s + g of its world, the first layer's B
+// operands x[s]. Every state value is loaded first (one load per feature, all in flight together),
+// then the normalisation constants (nrm: [3][4][kObsSteps] as packed by the tile layouts).
+template <class LoadT>
+__device__ __forceinline__ void tile_observation(const TileArgs& a, const float* nrm, const float* qpos,
+                                                 const float* qvel, const float* pact, int N, int t, int w,
+                                                 bool valid, int lane, LoadT ld, float (&x)[kObsSteps]) {
+  const int g = lane >> 4;
   const int wc = valid ? w : N - 1;
   const float* qp = qpos + (long)wc * kNQ;
   const float* qv = qvel + (long)wc * kNV;
   const float* pa = pact + (long)wc * kAct;
-
-  // ---- observation (raw to O, reference: src/g1_env.cu:69-81) and frozen normalisation
-  // (:298-302): lane (j, g) forms features 4 s + g of its world, the first layer's B operands.
-  // Every state value is loaded first (one load per feature, all in flight together), then the
-  // normalisation constants.
   const float qw = ld(qp + 3), qx = ld(qp + 4), qy = ld(qp + 5), qz = ld(qp + 6);
   // Feature k = 4 s + g comes from one array for every lane of a quad s except at the array
   // boundaries (s = 1, 2, 9, 16): one lane-dependent base per array (qv[k], qp[k - 2], qv[k - 32],
@@ -171,7 +204,7 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
     } else if (k0 + 3 < 96) raw[s] = ld(fa + k0);                          // prev action 1..28
     else raw[s] = ld(fv);                                                  // command and padding (unused)
   }
-  const float4* NC = reinterpret_cast<const float4*>(a.Wt + T.nrm_off + kObsSteps * g);
+  const float4* NC = reinterpret_cast<const float4*>(nrm + kObsSteps * g);
   float4 nmean[kObsSteps / 4], ndiv[kObsSteps / 4], nrcp[kObsSteps / 4];
 #pragma unroll
   for (int q = 0; q < kObsSteps / 4; ++q) {
@@ -179,7 +212,6 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
     ndiv[q] = NC[q + kObsSteps];
     nrcp[q] = NC[q + 2 * kObsSteps];
   }
-  float x[kObsSteps];
 #pragma unroll
   for (int s = 0; s < kObsSteps; ++s) {
     const int k = 4 * s + g;
@@ -193,6 +225,79 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
     }
     x[s] = z;
   }
+}
+
+// ---- the tile's outputs from the head's accumulators hd (rows 4 g + v of head tile ht in lane
+// (j, g), register v): the value (head row 29), then for t < H the sampling and log-prob
+// (reference: src/g1_env.cu:308-318): lane g owns actions 4g..4g+3 and 16+4g..16+4g+3, i.e. the
+// action pairs 2g, 2g+1, 8+2g, 9+2g; both Box-Muller normals of one Philox counter go to the actions
+// of one pair. The log-prob terms go through LDS (lds: kTileW x 32 floats) so that one lane sums
+// each world's 29 terms in action order.
+template <class LoadT>
+__device__ __forceinline__ void tile_outputs(const TileArgs& a, const f32x4 (&hd)[kHeadT], const float* ls,
+                                             const unsigned* rngc, unsigned long long seed, int N, int t, int w,
+                                             bool valid, int lane, float* lds, LoadT ld) {
+  const int j = lane & 15, g = lane >> 4;
+  const int wc = valid ? w : N - 1;
+  // ---- value (head row 29: tile 1, rows 4 g + v with g = 3, v = 1)
+  if (g == 3 && valid) {
+    if (t == a.H) a.Vlast[w] = hd[1][1];
+    else a.V[(long)t * N + w] = hd[1][1];
+  }
+  if (t == a.H) return;
+  const float LOG2PI = 1.8378770664093453f;
+  const unsigned rng = valid ? ld(rngc + wc) : 0u;
+  const long ab = ((long)t * N + w) * kAct;
+#pragma unroll
+  for (int ht = 0; ht < kHeadT; ++ht) {
+#pragma unroll
+    for (int hp = 0; hp < 2; ++hp) {
+      const int i0 = 16 * ht + 4 * g + 2 * hp;   // actions i0, i0 + 1
+      if (i0 < kAct) {
+        float nz[2];
+        if (a.act_noise) {
+          nz[0] = valid ? a.act_noise[ab + i0] : 0.f;
+          nz[1] = (valid && i0 + 1 < kAct) ? a.act_noise[ab + i0 + 1] : 0.f;
+        } else {
+          rng_normal2(seed, wc, rng, kStreamAction, i0 >> 1, nz[0], nz[1]);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int i = i0 + e;
+          if (i < kAct) {
+            const float lsi = ls[i];
+            if (valid) a.A[ab + i] = hd[ht][2 * hp + e] + expf(lsi) * nz[e];
+            lds[j * 32 + i] = -0.5f * nz[e] * nz[e] - lsi - 0.5f * LOG2PI;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (g == 0 && valid) {
+    float lpsum = 0.f;
+    for (int i = 0; i < kAct; ++i) lpsum += lds[j * 32 + i];
+    a.LP[(long)t * N + w] = lpsum;
+  }
+  __syncthreads();
+}
+
+// Policy of control step t (t == H: the bootstrap value only) for the tile's worlds w_j, given by
+// the caller (valid: w_j < N), on the fixed 256-256 shape of TileLayout. State is read with `ld`
+// (from the L2: other waves of the launch wrote it). hid: LDS scratch of kTileLds floats: the
+// log-prob terms (kTileW x 32), then the two layers' biases.
+template <int ACT, class LoadT>
+__device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos, const float* qvel, const float* pact,
+                                            const unsigned* rngc, unsigned long long seed, int N, int t, int w,
+                                            bool valid, float* hid, LoadT ld) {
+  // the lane index goes through an opaque asm so that nothing derived from it is hoisted out of the
+  // caller's item loop (where it would stay live beside the physics items' registers)
+  int lane = threadIdx.x & 63;
+  __asm__ volatile("" : "+v"(lane));
+  const int g = lane >> 4;
+  const TileLayout& T = a.tl;
+  float x[kObsSteps];
+  tile_observation(a, a.Wt + T.nrm_off, qpos, qvel, pact, N, t, w, valid, lane, ld, x);
 
   // ---- the MLP, on the fixed 256-256 shape (narrower layers are padded with zero weights and
   // biases, whose rows give act(0) = 0 and add exact zeros downstream). Layer 0 runs in 16 output
@@ -279,55 +384,118 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
 #pragma unroll
     for (int ht = 0; ht < kHeadT; ++ht) hd[ht] = mfma4(f32x4{wh[ht].x, wh[ht].y, wh[ht].z, wh[ht].w}, h2, hd[ht]);
   }
-  float* lds = hid;
+  tile_outputs(a, hd, a.Wt + T.ls_off, rngc, seed, N, t, w, valid, lane, hid, ld);
+}
 
-  // ---- value (head row 29: tile 1, rows 4 g + v with g = 3, v = 1)
-  if (g == 3 && valid) {
-    if (t == a.H) a.Vlast[w] = hd[1][1];
-    else a.V[(long)t * N + w] = hd[1][1];
-  }
-  if (t == a.H) return;
-
-  // ---- sampling + log-prob (reference: src/g1_env.cu:308-318): lane g owns actions 4g..4g+3 and
-  // 16+4g..16+4g+3, i.e. the action pairs 2g, 2g+1, 8+2g, 9+2g; both Box-Muller normals of one
-  // Philox counter go to the actions of one pair. The log-prob terms go through LDS so that one
-  // lane sums each world's 29 terms in action order.
-  const float LOG2PI = 1.8378770664093453f;
-  const float* ls = a.Wt + T.ls_off;
-  const unsigned rng = valid ? ld(rngc + wc) : 0u;
-  const long ab = ((long)t * N + w) * kAct;
+// One layer of the wide tile: nT output tiles over nQ k-quads of B operands (in: this lane's float4
+// per quad, the previous layer's outputs; layer 0 (kFromRegs): the observation x in registers), G
+// output tiles at a time, each tile's four k-steps interleaved with the other tiles' (G independent
+// accumulation chains). The loads of quad q + 2 are issued after quad q's MFMAs (two register sets,
+// the quad loop unrolled by two), so a quad's loads have a whole quad of MFMAs (G x 4 x 32 cycles)
+// to arrive. Outputs (activated) go to out[T * 64 + lane], or (kHead, nT = G = kHeadT) into hd.
+// (the scheduling pins keep each quad's loads together and in program order, so that a wait for one
+// register set counts only the loads issued before the other set's)
+template <int G>
+__device__ __forceinline__ void wide_load(const float4* Wg, int nQ, int q, const float4* in, int lane, float4 (&w)[G],
+                                          float4& x, bool kFromRegs) {
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int ht = 0; ht < kHeadT; ++ht) {
+  for (int i = 0; i < G; ++i) w[i] = Wg[((long)i * nQ + q) * 64];
+  if (!kFromRegs) x = in[q * 64 + lane];
+  __builtin_amdgcn_sched_barrier(0);
+}
+template <int G>
+__device__ __forceinline__ void wide_mfma(const float4 (&w)[G], const float (&xb)[4], f32x4 (&acc)[G]) {
 #pragma unroll
-    for (int hp = 0; hp < 2; ++hp) {
-      const int i0 = 16 * ht + 4 * g + 2 * hp;   // actions i0, i0 + 1
-      if (i0 < kAct) {
-        float nz[2];
-        if (a.act_noise) {
-          nz[0] = valid ? a.act_noise[ab + i0] : 0.f;
-          nz[1] = (valid && i0 + 1 < kAct) ? a.act_noise[ab + i0 + 1] : 0.f;
-        } else {
-          rng_normal2(seed, wc, rng, kStreamAction, i0 >> 1, nz[0], nz[1]);
-        }
+  for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int i = i0 + e;
-          if (i < kAct) {
-            const float lsi = ls[i];
-            if (valid) a.A[ab + i] = hd[ht][2 * hp + e] + expf(lsi) * nz[e];
-            lds[j * 32 + i] = -0.5f * nz[e] * nz[e] - lsi - 0.5f * LOG2PI;
-          }
-        }
+    for (int i = 0; i < G; ++i)
+      acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32((&w[i].x)[e], xb[e], acc[i], 0, 0, 0);
+}
+template <int ACT, int G, bool kFromRegs, bool kHead>
+__device__ __forceinline__ void wide_layer(const float4* W, const float* bias, int nT, int nQ, const float4* in,
+                                           const float (&x)[kObsSteps], float4* out, f32x4 (&hd)[kHeadT], int lane) {
+  const int g = lane >> 4;
+#pragma unroll 1
+  for (int T0 = 0; T0 < nT; T0 += G) {
+    f32x4 acc[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const float4 bv = *reinterpret_cast<const float4*>(bias + 16 * (T0 + i) + 4 * g);
+      acc[i] = f32x4{bv.x, bv.y, bv.z, bv.w};
+    }
+    const float4* Wg = W + (long)T0 * nQ * 64 + lane;
+    float4 wa[G], wb[G], xa = {0.f, 0.f, 0.f, 0.f}, xb = {0.f, 0.f, 0.f, 0.f};
+    wide_load<G>(Wg, nQ, 0, in, lane, wa, xa, kFromRegs);
+    wide_load<G>(Wg, nQ, 1, in, lane, wb, xb, kFromRegs);
+    if (kFromRegs) {
+      // layer 0: the observation quads in registers, the quad loop fully unrolled
+      constexpr int nq0 = kObsSteps / 4;
+#pragma unroll
+      for (int q = 0; q < nq0; ++q) {
+        float4 (&wc)[G] = (q & 1) ? wb : wa;
+        const float xs[4] = {x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
+        wide_mfma<G>(wc, xs, acc);
+        if (q + 2 < nq0) wide_load<G>(Wg, nQ, q + 2, in, lane, wc, xa, true);
+      }
+    } else {
+      // nQ is even (a hidden layer's output tiles are padded to a multiple of kWideGroup), so the
+      // loop body is two whole quads with no exit between them
+#pragma unroll 1
+      for (int q = 0; q < nQ; q += 2) {
+        const float xs0[4] = {xa.x, xa.y, xa.z, xa.w};
+        wide_mfma<G>(wa, xs0, acc);
+        wide_load<G>(Wg, nQ, q + 2 < nQ ? q + 2 : nQ - 1, in, lane, wa, xa, false);   // the tail reloads
+        const float xs1[4] = {xb.x, xb.y, xb.z, xb.w};
+        wide_mfma<G>(wb, xs1, acc);
+        wide_load<G>(Wg, nQ, q + 3 < nQ ? q + 3 : nQ - 1, in, lane, wb, xb, false);
       }
     }
+    if (kHead) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) hd[i] = acc[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < G; ++i)
+        out[(T0 + i) * 64 + lane] = float4{act_tile<ACT>(acc[i][0]), act_tile<ACT>(acc[i][1]),
+                                           act_tile<ACT>(acc[i][2]), act_tile<ACT>(acc[i][3])};
+    }
   }
-  __syncthreads();
-  if (g == 0 && valid) {
-    float lpsum = 0.f;
-    for (int i = 0; i < kAct; ++i) lpsum += lds[j * 32 + i];
-    a.LP[(long)t * N + w] = lpsum;
-  }
-  __syncthreads();
+}
+
+// Policy of control step t for the tile's worlds on a policy of 1..3 hidden layers of at most 512
+// units (WideLayout), for k_rollout: layer by layer on v_mfma_f32_16x16x4f32 with the weights as A
+// operands and the activations as B operands (lane (j, g): world j, input group g), kWideGroup
+// output tiles at a time. A layer's activated outputs go to this wave's activation buffers in
+// global memory (the L2), each lane storing its four output rows of a tile as one float4 at
+// [T][lane]; they are the next layer's B operands of k-quad T as they stand (the input order
+// kappa(L, s, g) = 16 (s / 4) + 4 g + s mod 4), so every lane reads back only what it wrote. The
+// weights stream from the L2 one quad ahead of their MFMAs. scr: this wave's two buffers of
+// wl.maxT * 256 floats (layers alternate between them); hid: LDS scratch for the log-prob terms.
+template <int ACT, class LoadT>
+__device__ __forceinline__ void policy_tile_wide(const TileArgs& a, const float* qpos, const float* qvel,
+                                                 const float* pact, const unsigned* rngc, unsigned long long seed,
+                                                 int N, int t, int w, bool valid, float* hid, float* scr, LoadT ld) {
+  int lane = threadIdx.x & 63;
+  __asm__ volatile("" : "+v"(lane));
+  const WideLayout& L = a.wl;
+  float x[kObsSteps];
+  tile_observation(a, a.Wt + L.nrm_off, qpos, qvel, pact, N, t, w, valid, lane, ld, x);
+  // buffer b of the two (pointer arithmetic on the kernel argument, so that the accesses compile to
+  // global loads and stores: a flat access would make every wait count the LDS as well)
+  float4* const buf0 = reinterpret_cast<float4*>(scr);
+  const long bstride = (long)L.maxT * 64;
+  f32x4 hd[kHeadT];
+  const float4* W = reinterpret_cast<const float4*>(a.Wt);
+  wide_layer<ACT, kWideGroup, true, false>(W + L.woff[0] / 4, a.Wt + L.boff[0], L.nT[0], L.nQ[0], nullptr, x, buf0,
+                                           hd, lane);
+#pragma unroll 1
+  for (int ly = 1; ly < L.nl; ++ly)
+    wide_layer<ACT, kWideGroup, false, false>(W + L.woff[ly] / 4, a.Wt + L.boff[ly], L.nT[ly], L.nQ[ly],
+                                              buf0 + ((ly - 1) & 1) * bstride, x, buf0 + (ly & 1) * bstride, hd, lane);
+  wide_layer<ACT, kHeadT, false, true>(W + L.woff[L.nl] / 4, a.Wt + L.boff[L.nl], kHeadT, L.nQ[L.nl],
+                                       buf0 + ((L.nl - 1) & 1) * bstride, x, nullptr, hd, lane);
+  tile_outputs(a, hd, a.Wt + L.ls_off, rngc, seed, N, t, w, valid, lane, hid, ld);
 }
 
 }  // namespace g1k

@@ -12,6 +12,10 @@ namespace g1k {
 constexpr size_t kRolloutLds = 2 * sizeof(WorldLds) > sizeof(float) * kTileLds
                                    ? 2 * sizeof(WorldLds) : sizeof(float) * kTileLds;
 
+// kWide: the policy items run the wide tile (policy_tile_wide) instead of the register-resident
+// 256-256 tile; two instantiations, so that each keeps its own register allocation (the physics
+// items of the narrow kernel are not scheduled around the wide tile's accumulators).
+template <bool kWide>
 __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
   __shared__ __align__(16) unsigned char lds_raw[kRolloutLds];
   WorldLds* lds = reinterpret_cast<WorldLds*>(lds_raw);
@@ -44,8 +48,18 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
     const auto ld = [](const auto* ptr) { return ld_l2(ptr); };
     const RolloutArgs& rb = kernarg_reread<RolloutArgs>();
     const PhysArgs& b = rb.ph;
-    if (rb.po.tl.act == 0) policy_tile<0>(rb.po, b.qp, b.qv, b.pa, b.rng, b.seed, b.N, t, w, valid, scratch_lds, ld);
-    else policy_tile<1>(rb.po, b.qp, b.qv, b.pa, b.rng, b.seed, b.N, t, w, valid, scratch_lds, ld);
+    if constexpr (kWide) {
+      // this block's two activation buffers
+      float* scr = rb.po.scr + (long)blockIdx.x * 2 * rb.po.wl.maxT * 256;
+      if (rb.po.wl.act == 0)
+        policy_tile_wide<0>(rb.po, b.qp, b.qv, b.pa, b.rng, b.seed, b.N, t, w, valid, scratch_lds, scr, ld);
+      else
+        policy_tile_wide<1>(rb.po, b.qp, b.qv, b.pa, b.rng, b.seed, b.N, t, w, valid, scratch_lds, scr, ld);
+    } else if (rb.po.tl.act == 0) {
+      policy_tile<0>(rb.po, b.qp, b.qv, b.pa, b.rng, b.seed, b.N, t, w, valid, scratch_lds, ld);
+    } else {
+      policy_tile<1>(rb.po, b.qp, b.qv, b.pa, b.rng, b.seed, b.N, t, w, valid, scratch_lds, ld);
+    }
     release_flag(ra.tflags + qq + kQueues * u, ra.tbase + (unsigned)t + 1u, a.xlocal);
   };
 
@@ -113,9 +127,10 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
 }
 
 void launch_rollout_kernel(const RolloutArgs& ra, int grid) {
-  hipLaunchKernelGGL(k_rollout, dim3((unsigned)grid), dim3(kPhysThreads), 0, 0, ra);
+  if (ra.po.wide) hipLaunchKernelGGL(k_rollout<true>, dim3((unsigned)grid), dim3(kPhysThreads), 0, 0, ra);
+  else hipLaunchKernelGGL(k_rollout<false>, dim3((unsigned)grid), dim3(kPhysThreads), 0, 0, ra);
 }
 
-const void* rollout_kernel_fn() { return (const void*)k_rollout; }
+const void* rollout_kernel_fn(bool wide) { return wide ? (const void*)k_rollout<true> : (const void*)k_rollout<false>; }
 
 }  // namespace g1k

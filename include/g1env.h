@@ -122,10 +122,11 @@ int g1_env_set_handover(void* h, int fences);
 
 /* Rollout form: on = 1 (the default) runs g1_rollout as one persistent launch that interleaves the
  * policy of 16-world tiles with the physics work items; on = 0 launches the policy and the physics
- * once per control step. The one-launch form covers policies of two hidden layers of at most 256
- * units each (run at 256-256 with zero padding); other shapes always take the per-step form.
- * Returns 0, 1 when on = 1 but
- * the current policy shape takes the per-step form, or -1 for an invalid argument. */
+ * once per control step. The one-launch form covers every shape g1_env_set_policy accepts (two
+ * hidden layers of at most 256 units on a register-resident tile, other shapes on a tile that
+ * stages its activations in library-allocated device memory); g1_rollout_noalloc runs the latter
+ * shapes in the per-step form. Returns 0, 1 when on = 1 but the current policy shape takes the
+ * per-step form, or -1 for an invalid argument. */
 int g1_env_set_fused(void* h, int on);
 
 /* Parity probes running the same device code as the rollout on caller states (all DEVICE,

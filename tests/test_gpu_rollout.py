@@ -175,11 +175,14 @@ def test_rollout_teacher_forced_config4_slice(g1, orc):
     _assert_rows(rows)
 
 
-@pytest.mark.parametrize("hidden,act", [((48, 32), 1), ((80, 144), 0), ((100, 60), 0), ((256, 17), 1)])
+@pytest.mark.parametrize("hidden,act", [((48, 32), 1), ((80, 144), 0), ((100, 60), 0), ((256, 17), 1),
+                                        ((512, 512, 256), 1), ((300,), 0), ((64, 48, 32), 1), ((512, 70), 0)])
 def test_rollout_teacher_forced_one_launch_shapes(g1, orc, hidden, act):
-    """The one-launch rollout's policy tile on two-layer shapes other than 256-256, which it runs at
-    256-256 with zero padding: widths that are and are not multiples of 16, ELU and tanh. N=512,
-    4 control steps against the oracle."""
+    """The one-launch rollout's policy tiles on shapes other than 256-256: two layers of at most 256
+    run on the register-resident tile at 256-256 with zero padding (widths that are and are not
+    multiples of 16, ELU and tanh); one to three layers of up to 512 on the wide tile (activations
+    staged in global memory, output tiles padded to multiples of 64 rows), config 4's 512-512-256
+    ELU among them. N=512, 4 control steps against the oracle."""
     import configs
     N, H = 512, 4
     rng = np.random.default_rng(61)

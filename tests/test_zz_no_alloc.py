@@ -3,7 +3,10 @@ the call) against g1_rollout_ex on identical states and noise: every trajectory 
 final state bit for bit, on two calls in a row, the second with a smaller input (fewer worlds, a
 shorter horizon and a smaller policy, so the array holds a stale, larger packing from the first
 call). Each no-alloc call runs on a fresh env and leaves the env's device memory where creation put
-it (g1_env_device_bytes), while g1_rollout_ex on a fresh env grows it by its packed policy."""
+it (g1_env_device_bytes), while g1_rollout_ex on a fresh env grows it by its packed policy. A policy
+wider than two layers of 256 runs the no-alloc call in the per-step form (the one-launch form's wide
+tile needs activation buffers the library allocates), so its g1_rollout_ex comparison takes the
+per-step form too."""
 import numpy as np
 import pytest
 
@@ -37,6 +40,8 @@ def _run(g1, state, inputs, N, H, hidden, act, noalloc):
     dev = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in inputs]
     with g1.Env(N, substeps=10, pgs_iters=8, seed=3) as env:
         env.set_policy(hidden, act)
+        narrow = len(hidden) == 2 and max(hidden) <= 256
+        env.set_fused(narrow)   # the form g1_rollout_noalloc takes for this shape
         env.set_state(*state)
         traj = g1.Trajectory(H, N)
         ptrs = [g1.dev_ptr(t) for t in (*dev[:3], *traj.tensors(), dev[3], dev[4])]
