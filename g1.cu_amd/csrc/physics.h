@@ -929,8 +929,10 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   if (l < 6) {
     // column l of U6 = I^A S_base: translation l < 3 picks column 3 + l of I^A, rotation l >= 3
     // is I^A's angular columns times R1 col (l - 3) (structural zeros skipped, see sbase_dot).
-    // The packed I^A and the rows S[3..5] are read whole (the same addresses on every lane) and
-    // the lane's column is selected in registers.
+    // The packed I^A and the rows S[3..5] are read whole (the same addresses on every lane); the
+    // lane's own operands (its translation column, its rotation row) are read at lane-dependent
+    // addresses rather than selected among registers, which the compiler turned into divergent
+    // branches (an exec-mask diamond per select).
     float IA[21], S3[3][3];
 #pragma unroll
     for (int i = 0; i < 21; ++i) IA[i] = s.u.fac.IA1[i];
@@ -938,14 +940,20 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int k = 0; k < 3; ++k)
 #pragma unroll
       for (int i = 0; i < 3; ++i) S3[k][i] = s.u.fac.S[3 + k][i];
-    float Sc[3];   // row S[l] of a rotation lane (translation lanes: unused)
+    const int rl = l < 3 ? 0 : l - 3;   // the lane's rotation (translation lanes: row 0, unused)
+    const int tl = l < 3 ? l : 0;       // the lane's translation (rotation lanes: 0, unused)
+    float Sc[3];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) Sc[i] = l == 4 ? S3[1][i] : (l == 5 ? S3[2][i] : S3[0][i]);
+    for (int i = 0; i < 3; ++i) Sc[i] = s.u.fac.S[3 + rl][i];
     float U6c[6];
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
       const float rot = fmaf_(IA[symidx(i, 2)], Sc[2], fmaf_(IA[symidx(i, 1)], Sc[1], IA[symidx(i, 0)] * Sc[0]));
-      const float tr = l == 0 ? IA[symidx(i, 3)] : (l == 1 ? IA[symidx(i, 4)] : IA[symidx(i, 5)]);
+      // I^A[i][3 + tl] in the 21-packed upper triangle (i <= 3 + tl for i < 3; (3 + tl, i) else)
+      const int ti = i <= 3 ? i * 6 - (i * (i - 1)) / 2 + (3 + tl - i) : symidx(i, 3);
+      const int tj = i < 3 ? ti : (i <= 3 + tl ? i * 6 - (i * (i - 1)) / 2 + (3 + tl - i)
+                                               : (3 + tl) * 6 - ((3 + tl) * (2 + tl)) / 2 + (i - 3 - tl));
+      const float tr = s.u.fac.IA1[i < 3 ? ti : tj];
       U6c[i] = l < 3 ? tr : rot;
     }
     // D = S_base' U6 (+ armature and dt*damping, both 0 on the free joint)

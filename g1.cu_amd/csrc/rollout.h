@@ -172,7 +172,8 @@ template <class LoadT>
 __device__ __forceinline__ void tile_observation(const TileArgs& a, const float* nrm, const float* qpos,
                                                  const float* qvel, const float* pact, int N, int t, int w,
                                                  bool valid, int lane, LoadT ld, float (&x)[kObsSteps]) {
-  const int g = lane >> 4;
+  const int g = (lane >> 4) & 3;   // (& 3: the lane arrives through an opaque asm; with g's range known
+                                   // the feature tests of obs_value fold for every quad but three)
   const int wc = valid ? w : N - 1;
   const float* qp = qpos + (long)wc * kNQ;
   const float* qv = qvel + (long)wc * kNV;
@@ -237,7 +238,7 @@ template <class LoadT>
 __device__ __forceinline__ void tile_outputs(const TileArgs& a, const f32x4 (&hd)[kHeadT], const float* ls,
                                              const unsigned* rngc, unsigned long long seed, int N, int t, int w,
                                              bool valid, int lane, float* lds, LoadT ld) {
-  const int j = lane & 15, g = lane >> 4;
+  const int j = lane & 15, g = (lane >> 4) & 3;
   const int wc = valid ? w : N - 1;
   // ---- value (head row 29: tile 1, rows 4 g + v with g = 3, v = 1)
   if (g == 3 && valid) {
@@ -294,7 +295,7 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
   // caller's item loop (where it would stay live beside the physics items' registers)
   int lane = threadIdx.x & 63;
   __asm__ volatile("" : "+v"(lane));
-  const int g = lane >> 4;
+  const int g = (lane >> 4) & 3;
   const TileLayout& T = a.tl;
   float x[kObsSteps];
   tile_observation(a, a.Wt + T.nrm_off, qpos, qvel, pact, N, t, w, valid, lane, ld, x);
@@ -415,7 +416,7 @@ __device__ __forceinline__ void wide_mfma(const float4 (&w)[G], const float (&xb
 template <int ACT, int G, bool kFromRegs, bool kHead>
 __device__ __forceinline__ void wide_layer(const float4* W, const float* bias, int nT, int nQ, const float4* in,
                                            const float (&x)[kObsSteps], float4* out, f32x4 (&hd)[kHeadT], int lane) {
-  const int g = lane >> 4;
+  const int g = (lane >> 4) & 3;
 #pragma unroll 1
   for (int T0 = 0; T0 < nT; T0 += G) {
     f32x4 acc[G];
