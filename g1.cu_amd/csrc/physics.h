@@ -469,6 +469,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   __asm__ volatile("" : "+v"(l));
   const LaneModel L = lane_model(l);
   const bool base = (l == 1);
+  // Lane-indexed table reads of the FK rounds and the contact detection, issued with the lane
+  // model so that their latency passes under the hinge sincos instead of stalling the phase that
+  // uses them: the ancestor lanes of every doubling round (one byte per round) and the lane's foot
+  // sphere (local position, invweight0).
+  const unsigned anc = kAncestorWords.w[l];
+  const int sph = l < kNFoot ? l : 0;
+  const V3 foot_lp{MF::foot_lpos[3 * sph], MF::foot_lpos[3 * sph + 1], MF::foot_lpos[3 * sph + 2]};
+  const float foot_w0 = MF::foot_invweight0[sph];
 
   // ---------------- forward kinematics (reference: src/dynamics.cuh:47-88) by ancestor doubling
   // Each lane starts from its body's transform relative to its parent (hinge: translation
@@ -506,7 +514,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     Q4d dq{xq.w, xq.x, xq.y, xq.z};
 #pragma unroll
     for (int r = 0; r < kFkRounds; ++r) {
-      const int an = kAncestors.a[r][l];
+      const int an = (anc >> (8 * r)) & 0xff;
       const Q4d qa{gshfld(dq.w, an), gshfld(dq.x, an), gshfld(dq.y, an), gshfld(dq.z, an)};
       const V3d pa{gshfld(dp.x, an), gshfld(dp.y, an), gshfld(dp.z, an)};
       if (an > 0) {
@@ -524,12 +532,13 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // ---------------- contact detection: lane s = foot sphere s (reference: src/contact.cuh:31-46)
   int ncon = 0;
   if (P.contact) {
-    const int sph = l < kNFoot ? l : 0;
-    const int fb = foot_body[sph];
+    // spheres 0..3 on the left foot, 4..7 on the right
+    static_assert(foot_body[0] == foot_body[kNFoot / 2 - 1] && foot_body[kNFoot / 2] == foot_body[kNFoot - 1],
+                  "foot spheres in two halves");
+    const int fb = sph < kNFoot / 2 ? foot_body[0] : foot_body[kNFoot - 1];
     Q4 fq{gshfl(xq.w, fb), gshfl(xq.x, fb), gshfl(xq.y, fb), gshfl(xq.z, fb)};
     V3 fp{gshfl(xp.x, fb), gshfl(xp.y, fb), gshfl(xp.z, fb)};
-    V3 lp{MF::foot_lpos[3 * sph], MF::foot_lpos[3 * sph + 1], MF::foot_lpos[3 * sph + 2]};
-    V3 c = vadd(fp, qrot(fq, lp));
+    V3 c = vadd(fp, qrot(fq, foot_lp));
     const float pen = c.z - MF::foot_radius;
     const bool hit = (l < kNFoot) && (pen < 0.f);
     const unsigned mask = group_ballot8(hit);
@@ -537,7 +546,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     if (hit) {
       const int idx = __popc(mask & ((1u << l) - 1u));
       s.con[idx][0] = c.x; s.con[idx][1] = c.y; s.con[idx][2] = pen * 0.5f; s.con[idx][3] = pen;
-      s.con_w0[idx] = MF::foot_invweight0[sph];
+      s.con_w0[idx] = foot_w0;
       s.con_leg[idx] = (fb == foot_body[kNFoot - 1]) ? 1 : 0;
     }
   }

@@ -31,6 +31,22 @@ constexpr AncestorTable make_ancestor_table() {
 
 constexpr AncestorTable kAncestors = make_ancestor_table();
 
+// The same table as one 32-bit word per lane, byte r = a[r][b]: one lane-indexed load serves every
+// round of the doubling.
+struct AncestorWords {
+  unsigned w[kTreeLanes];
+};
+
+constexpr AncestorWords make_ancestor_words() {
+  AncestorWords t{};
+  for (int b = 0; b < kTreeLanes; ++b)
+    for (int r = 0; r < kFkRounds; ++r) t.w[b] |= (unsigned)kAncestors.a[r][b] << (8 * r);
+  return t;
+}
+
+constexpr AncestorWords kAncestorWords = make_ancestor_words();
+static_assert(kFkRounds <= 4 && kTreeLanes <= 256, "one byte per round in a 32-bit word");
+
 constexpr bool depth_fits_doubling() {
   for (int b = 0; b < kNBody; ++b)
     if (body_depth[b] >= (1 << kFkRounds)) return false;
