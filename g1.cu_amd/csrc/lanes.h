@@ -132,23 +132,24 @@ __device__ __forceinline__ void chain_rot3(float pc, float& X1, float& X2, float
 }
 
 // Value of lane I of this lane's group, of its 16-lane row or of its quad, in every lane of that
-// unit: W = 32 (I < 32) takes lane I mod 16 of each 16-lane row by DPP row_newbcast into two
-// registers and a v_permlane16_swap, which gives every lane of a group the row holding lane I
-// (rows 0 and 2 of the wave in the first result, 1 and 3 in the second); W = 16 (I < 16) the
-// row_newbcast alone, W = 4 (I < 4) a quad_perm. No LDS round trip.
+// unit: W = 32 (I < 32) first makes both 16-lane rows of each group hold the row with lane I (a
+// v_permlane16_swap of the value with itself: rows 0 and 2 of the wave in the first result, 1 and
+// 3 in the second), then takes lane I mod 16 of each row by DPP row_newbcast; W = 16 (I < 16) the
+// row_newbcast alone, W = 4 (I < 4) a quad_perm. No LDS round trip. The DPP move comes last so
+// that the compiler can fold it into the instruction that uses the value (a v_fmac_f32 with a DPP
+// source operand).
 template <int I, int W>
 __device__ __forceinline__ float group_bcast(float v) {
   static_assert(I < W && (W == 4 || W == 16 || W == 32), "lane of the unit");
   if constexpr (W == 4) {
     return quad_perm<I, I, I, I>(v);
   } else {
-    const int x = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + (I & 15), 0xF, 0xF, false);
-    if constexpr (W == 16) {
-      return __int_as_float(x);
-    } else {
+    int x = __float_as_int(v);
+    if constexpr (W == 32) {
       const auto p = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
-      return __uint_as_float(I < 16 ? p[0] : p[1]);
+      x = (int)(I < 16 ? p[0] : p[1]);
     }
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x150 + (I & 15), 0xF, 0xF, false));
   }
 }
 

@@ -376,29 +376,108 @@ struct SolveParams {
 };
 
 // One projected Gauss-Seidel sweep over rows II.. (reference: src/contact.cuh:159-171), in the
-// row-scaled residual form: lane i holds row i scaled by y_i = RN(1/A_ii) with its diagonal entry 0
-// (a_ij = RN(A_ij y_i); A is symmetric bit for bit, so lane i's column of A is its row) and the
-// row's residual r_i = c_i + sum_j a_ij f_j for the current f, c_i = RN(b_i y_i). Row ii: its lane
-// sets f_ii = max(0, -r_ii); the change d = RN(f new - f old) goes from that lane to every lane of
-// the world (group_bcast), and every lane j adds a_j,ii d to r_j in one fma. Every lane evaluates
-// the update and only lane ii keeps it; a lane without a row (i >= its world's count) holds zero
-// entries, r = c = 0 and f = 0. Straight-line rows; the first row at or past the wave's largest row
-// count nefc_max branches once to the end of the sweep. W: the rows a world can hold in this wave
-// (nefc_max <= W): the change is broadcast over the group (32), its first 16-lane row (16) or its
-// first quad (4); lanes past W hold no row and their r is never read.
+// row-scaled residual form: row i is held scaled by y_i = RN(1/A_ii) with its diagonal entry 0
+// (a_ij = RN(A_ij y_i); A is symmetric bit for bit, so lane i's column of A is its row) together
+// with its residual r_i = c_i + sum_j a_ij f_j for the current f, c_i = RN(b_i y_i). Row ii: its
+// lane sets f_ii = max(0, -r_ii); the change d = RN(f new - f old) goes from that lane to every
+// lane of the world, and every row j adds a_j,ii d to r_j in one fma. Every lane evaluates the
+// update and only row ii's lanes keep it; a row past its world's count holds zero entries,
+// r = c = 0 and f = 0. Straight-line rows; rows come four to a contact (the wave's largest row
+// count nefc_max is a multiple of 4), so the sweep tests nefc_max at every fourth row and branches
+// once to its end. W: the rows a world can hold in this wave (nefc_max <= W): lane i holds row i
+// and the change is broadcast over its first 16-lane row (16) or its quad (4); for W = 32 see
+// pgs_row_pair.
+//
+// A row in VALU code (W = 16): fn = max(-r, 0), d = fn - f, f = fn on row II's lanes (a lane
+// mask), then r += a d with d taken from lane II of the 16-lane row by DPP row_newbcast inside the
+// fma (v_fmac_f32 with a DPP source operand): 4 VALU. Written out because the compiler keeps the
+// DPP move apart from an fma (it forms the two-operand v_fmac_f32 only after its DPP combining)
+// and, with the fma written out alone, adds a canonicalising max before max(-r, 0); these are the
+// compiler's own instructions for the operations, so the values are the same. The s_nop and the
+// v_cndmask before the DPP read give the two wait states it needs after the VALU write of its
+// source. max(-r, 0) is 0 for a NaN r (the quiet NaNs of arithmetic), as t > 0 ? t : 0 is.
+// `lanes`: the row's lanes, lane II of every 16-lane row (a mask built from an opaque base in each
+// sweep: as 32 constants the compiler holds the masks in scalar registers across the sweep loop
+// and spills them).
 template <int II, int W>
-__device__ __forceinline__ void pgs_sweep(const float (&Acol)[kMaxEfc], int l, int nefc_max, float& fi, float& ri) {
+__device__ __forceinline__ void pgs_row(float a, int l, unsigned long long lanes, float& fi, float& ri) {
+  static_assert(W == 4 || W == 16, "rows of a quad or of a 16-lane row");
+  if constexpr (W == 4) {
+    const float t = -ri;
+    const float fn = t > 0.f ? t : 0.f;
+    const float d = fn - fi;
+    fi = (l == II) ? fn : fi;
+    ri = fmaf_(a, group_bcast<II, W>(d), ri);
+  } else {
+    float fn, d;
+    __asm__("v_max_f32_e64 %2, -%1, 0\n\t"
+            "v_sub_f32_e32 %3, %2, %0\n\t"
+            "v_cndmask_b32_e64 %0, %0, %2, %5\n\t"
+            "s_nop 0\n\t"
+            "v_fmac_f32_dpp %1, %3, %4 row_newbcast:%6 row_mask:0xf bank_mask:0xf"
+            : "+v"(fi), "+v"(ri), "=&v"(fn), "=&v"(d)
+            : "v"(a), "s"(lanes), "n"(II & 15));
+  }
+}
+
+template <int II, int W>
+__device__ __forceinline__ void pgs_sweep(const float (&Acol)[kMaxEfc], int l, unsigned long long lanes0, int nefc_max,
+                                          float& fi, float& ri) {
   if constexpr (II < W) {
-    if (II < nefc_max) {
-      const float t = -ri;
-      const float fn = t > 0.f ? t : 0.f;
-      const float d = fn - fi;
-      fi = (l == II) ? fn : fi;
-      ri = fmaf_(Acol[II], group_bcast<II, W>(d), ri);
-      pgs_sweep<II + 1, W>(Acol, l, nefc_max, fi, ri);
+    if (II % 4 != 0 || II < nefc_max) {
+      pgs_row<II, W>(Acol[II], l, lanes0 << II, fi, ri);
+      pgs_sweep<II + 1, W>(Acol, l, lanes0, nefc_max, fi, ri);
     }
   }
 }
+
+// The sweep for worlds of up to 32 rows in paired-row form: lane l of a group holds two rows of its
+// world, lo = l mod 16 and hi = 16 + l mod 16 (their scaled rows p and q, residuals and f), and both
+// 16-lane rows of the group hold the same copy. Row II's change d then sits in lane II mod 16 of
+// every 16-lane row, so one DPP row_newbcast inside each of the two fmas (r_lo += p_II d,
+// r_hi += q_II d) broadcasts it: 5 VALU per row, where one row per lane needs a cross-row exchange
+// (v_permlane16_swap, its register copy and wait states) on every row. Same operations in the same
+// order as one row per lane, so the same values.
+template <int II>
+__device__ __forceinline__ void pgs_row_pair(float p, float q, unsigned long long lanes, float& fown, float& rlo,
+                                             float& rhi) {
+  float fn, d;
+  if constexpr (II < 16) {
+    __asm__("v_max_f32_e64 %3, -%1, 0\n\t"
+            "v_sub_f32_e32 %4, %3, %0\n\t"
+            "v_cndmask_b32_e64 %0, %0, %3, %7\n\t"
+            "s_nop 0\n\t"
+            "v_fmac_f32_dpp %1, %4, %5 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %2, %4, %6 row_newbcast:%8 row_mask:0xf bank_mask:0xf"
+            : "+v"(fown), "+v"(rlo), "+v"(rhi), "=&v"(fn), "=&v"(d)
+            : "v"(p), "v"(q), "s"(lanes), "n"(II & 15));
+  } else {
+    __asm__("v_max_f32_e64 %3, -%2, 0\n\t"
+            "v_sub_f32_e32 %4, %3, %0\n\t"
+            "v_cndmask_b32_e64 %0, %0, %3, %7\n\t"
+            "s_nop 0\n\t"
+            "v_fmac_f32_dpp %1, %4, %5 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %2, %4, %6 row_newbcast:%8 row_mask:0xf bank_mask:0xf"
+            : "+v"(fown), "+v"(rlo), "+v"(rhi), "=&v"(fn), "=&v"(d)
+            : "v"(p), "v"(q), "s"(lanes), "n"(II & 15));
+  }
+}
+
+template <int II>
+__device__ __forceinline__ void pgs_sweep_pair(const float (&P)[kMaxEfc], const float (&Q)[kMaxEfc],
+                                               unsigned long long lanes0, int nefc_max, float& flo, float& fhi,
+                                               float& rlo, float& rhi) {
+  if constexpr (II < kMaxEfc) {
+    if (II % 4 != 0 || II < nefc_max) {
+      if constexpr (II < 16) pgs_row_pair<II>(P[II], Q[II], lanes0 << II, flo, rlo, rhi);
+      else pgs_row_pair<II>(P[II], Q[II], lanes0 << (II - 16), fhi, rlo, rhi);
+      pgs_sweep_pair<II + 1>(P, Q, lanes0, nefc_max, flo, fhi, rlo, rhi);
+    }
+  }
+}
+
+// Lane 0 of every 16-lane row: the row lanes of a sweep's first row (pgs_row, pgs_row_pair).
+constexpr unsigned long long kPgsLanes0 = 0x0001000100010001ull;
 
 // Sweeps between the fresh residuals of the PGS (a fresh residual r_i = c_i + sum_k a_ik f_k, k in
 // order, bounds the rounding the row updates carry over long solves).
@@ -1518,15 +1597,67 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         ri = done ? ri : t;
       }
       const float f0 = fi;
-      pgs_sweep<0, W>(Acol, l, nefc_max, fi, ri);
+      unsigned long long lanes0 = kPgsLanes0;
+      __asm__ volatile("" : "+s"(lanes0));
+      pgs_sweep<0, W>(Acol, l, lanes0, nefc_max, fi, ri);
       const unsigned long long m = __ballot(__float_as_uint(fi) != __float_as_uint(f0));
       if (m == 0ull) break;
       done = done || ((unsigned)(m >> (32 * group_id())) == 0u);
     }
   };
+  // up to 32 rows: the paired-row form of pgs_sweep_pair (lane l: rows l mod 16 and 16 + l mod 16)
+  auto solve_pairs = [&]() {
+#pragma unroll
+    for (int ii = 0; ii < kMaxEfc; ++ii) Acol[ii] = Acol[ii] * yi;
+    // A v_permlane16_swap of a value with itself gives every lane of a group the value of lane
+    // l mod 16 of the group's first 16-lane row (first result) and of its second row (second).
+    auto split = [](float v, float& lo, float& hi) {
+      const auto pq = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      lo = __uint_as_float(pq[0]);
+      hi = __uint_as_float(pq[1]);
+    };
+    float Pr[kMaxEfc], Qr[kMaxEfc];   // entries (lo, k) and (hi, k) of the scaled A
+#pragma unroll
+    for (int k = 0; k < kMaxEfc; ++k) {
+      if (k % 4 == 0 && k >= nefc_max) break;   // rows past nefc_max are never read
+      split(Acol[k], Pr[k], Qr[k]);
+    }
+    float clo, chi;
+    split(cb, clo, chi);
+    float flo = 0.f, fhi = 0.f, rlo = clo, rhi = chi;
+    bool done = false;   // this world's solve has ended
+#pragma unroll 1
+    for (int it = 0; it < P.pgs; ++it) {
+      if (it > 0 && it % kPgsRefresh == 0) {
+        // fresh residuals: every lane reads every f of its world (row l from lane l's copy)
+        s.f[l] = l < kGroup / 2 ? flo : fhi;
+        wave_sync();
+        float tlo = clo, thi = chi;
+#pragma unroll
+        for (int k = 0; k < kMaxEfc; ++k)
+          if (k < nefc_max) {
+            const float fk = s.f[k];
+            tlo = fmaf_(Pr[k], fk, tlo);
+            thi = fmaf_(Qr[k], fk, thi);
+          }
+        wave_sync();
+        rlo = done ? rlo : tlo;
+        rhi = done ? rhi : thi;
+      }
+      const float flo0 = flo, fhi0 = fhi;
+      unsigned long long lanes0 = kPgsLanes0;
+      __asm__ volatile("" : "+s"(lanes0));
+      pgs_sweep_pair<0>(Pr, Qr, lanes0, nefc_max, flo, fhi, rlo, rhi);
+      const unsigned long long m = __ballot(__float_as_uint(flo) != __float_as_uint(flo0) ||
+                                            __float_as_uint(fhi) != __float_as_uint(fhi0));
+      if (m == 0ull) break;
+      done = done || ((unsigned)(m >> (32 * group_id())) == 0u);
+    }
+    fi = l < kGroup / 2 ? flo : fhi;   // row l
+  };
   if (nefc_max <= 4) solve(std::integral_constant<int, 4>());
   else if (nefc_max <= kGroup / 2) solve(std::integral_constant<int, kGroup / 2>());
-  else solve(std::integral_constant<int, kMaxEfc>());
+  else solve_pairs();
   __builtin_amdgcn_s_setprio(0);
   if (row) s.f[l] = fi;
   wave_sync();
