@@ -203,7 +203,8 @@ def measure_counters(config, kernel, timeout_s=150, workload="rollout", per_step
         return None, "counter passes did not report the physics or copy dispatches"
     kib = COPY_MIB * 1024.0
     scale_f, scale_w = kib / copy["FETCH_SIZE"], kib / copy["WRITE_SIZE"]
-    phys["traffic_bytes"] = (phys["FETCH_SIZE"] * scale_f + phys["WRITE_SIZE"] * scale_w) * 1024.0
+    phys["fetch_bytes"], phys["write_bytes"] = phys["FETCH_SIZE"] * scale_f * 1024.0, phys["WRITE_SIZE"] * scale_w * 1024.0
+    phys["traffic_bytes"] = phys["fetch_bytes"] + phys["write_bytes"]
     phys["fetch_scale"], phys["write_scale"] = scale_f, scale_w
     phys["dispatches"] = len(res["physics"]["FETCH_SIZE"])
     return phys, None
@@ -293,6 +294,13 @@ def main():
     substeps_per_s = N * H * S / (wall / args.steps)
 
     bw_meas = measure_copy_bandwidth()
+    # Compulsory HBM bytes of one rollout: the trajectory written once (O [H,N,100], A [H,N,29],
+    # LP/V/R/D [H,N], Vlast [N]), the env state read and written once (qpos 36, qvel 35, previous
+    # action 29, step and noise counters), the policy (weights and biases, obs mean and variance) read
+    # once; library noise, so no noise arrays.
+    n_weights = sum(i * o + o for i, o in zip((100,) + tuple(cfg["hidden"]), tuple(cfg["hidden"]) + (30,)))
+    compulsory = 4.0 * (N * H * (g1env.OBS_DIM + g1env.ACT_DIM + 4) + N + 2 * N * (g1env.NQ + g1env.NV + g1env.ACT_DIM + 2)
+                        + n_weights + 200)
     launches = max(pr["physics_launches"], 1)
     avg_launch_s = pr["physics_ms"] / launches * 1e-3
     bytes_total, flops_total = rf.physics_work(hist, pgs, control_steps_worlds=N * H * args.steps)
@@ -324,6 +332,10 @@ def main():
         roof["counters"] = {
             "source": f"rocprofv3 --pmc, one-rollout run of this script ({counters['dispatches']} {kernel} dispatches)",
             "hbm_bytes_per_dispatch": counters["traffic_bytes"],
+            "hbm_read_bytes_per_dispatch": counters["fetch_bytes"],
+            "hbm_write_bytes_per_dispatch": counters["write_bytes"],
+            "hbm_compulsory_bytes": compulsory,
+            "hbm_over_compulsory": counters["traffic_bytes"] / compulsory,
             "hbm_gbs": counters["traffic_bytes"] / avg_launch_s / 1e9,
             "hbm_frac_of_bw_meas": counters["traffic_bytes"] / avg_launch_s / 1e9 / bw_meas,
             "fetch_write_scale": [counters["fetch_scale"], counters["write_scale"]],
@@ -386,6 +398,8 @@ def counter_summary(counters, kernel, avg_launch_s, phys_flops_launch, bw_meas):
     out = {
         "source": f"rocprofv3 --pmc, one run of this script's counter child ({counters['dispatches']} {kernel} dispatches)",
         "hbm_bytes_per_dispatch": counters["traffic_bytes"],
+        "hbm_read_bytes_per_dispatch": counters["fetch_bytes"],
+        "hbm_write_bytes_per_dispatch": counters["write_bytes"],
         "hbm_gbs": counters["traffic_bytes"] / avg_launch_s / 1e9,
         "hbm_frac_of_bw_meas": counters["traffic_bytes"] / avg_launch_s / 1e9 / bw_meas,
         "fetch_write_scale": [counters["fetch_scale"], counters["write_scale"]],
