@@ -79,7 +79,7 @@ __host__ __device__ __forceinline__ int tile_kappa(int L, int s, int g) {
 // TileLayout. A hidden layer's output tiles are padded to a multiple of kWideGroup (zero rows:
 // act(0) = 0 adds exact zeros downstream); the head has kHeadT tiles (mu 0..28, value 29).
 constexpr int kWideMaxLayers = 4;   // hidden layers + head
-constexpr int kWideGroup = 8;       // output tiles a wave accumulates at once (independent chains)
+constexpr int kWideGroup = 4;       // output tiles a wave accumulates at once (independent chains)
 struct WideLayout {
   int nl;                           // hidden layers (1..3)
   int nT[kWideMaxLayers];           // output tiles of layer L
@@ -90,7 +90,7 @@ struct WideLayout {
   int act;                          // 0 tanh, 1 ELU
 };
 
-static_assert(kWideGroup % 2 == 0, "hidden layers feed the next layer an even number of k-quads");
+static_assert(kWideGroup % 4 == 0, "hidden layers feed the next layer a multiple of 4 k-quads");
 __host__ __device__ inline WideLayout wide_layout(int nl, const int* hid, int act) {
   WideLayout t{};
   t.nl = nl;
@@ -391,11 +391,13 @@ __device__ __forceinline__ void policy_tile(const TileArgs& a, const float* qpos
 // One layer of the wide tile: nT output tiles over nQ k-quads of B operands (in: this lane's float4
 // per quad, the previous layer's outputs; layer 0 (kFromRegs): the observation x in registers), G
 // output tiles at a time, each tile's four k-steps interleaved with the other tiles' (G independent
-// accumulation chains). The loads of quad q + 2 are issued after quad q's MFMAs (two register sets,
-// the quad loop unrolled by two), so a quad's loads have a whole quad of MFMAs (G x 4 x 32 cycles)
-// to arrive. Outputs (activated) go to out[T * 64 + lane], or (kHead, nT = G = kHeadT) into hd.
-// (the scheduling pins keep each quad's loads together and in program order, so that a wait for one
-// register set counts only the loads issued before the other set's)
+// accumulation chains). Layer 0 loads quad q + 2 after quad q's MFMAs (two register sets); the
+// other layers load quad q + 4 (four register sets, the quad loop unrolled by four), so a quad's
+// loads have three quads of MFMAs (3 x G x 4 x 32 cycles) to arrive. Outputs (activated) go to
+// out[T * 64 + lane], or (kHead, nT = G = kHeadT) into hd. (the scheduling pins keep each quad's
+// loads together and in program order, so that a wait for one register set counts only the loads
+// issued before the later sets'; without them the compiler hoists every load of the unrolled body
+// to its top, past the 256-VGPR budget)
 template <int G>
 __device__ __forceinline__ void wide_load(const float4* Wg, int nQ, int q, const float4* in, int lane, float4 (&w)[G],
                                           float4& x, bool kFromRegs) {
@@ -440,16 +442,26 @@ __device__ __forceinline__ void wide_layer(const float4* W, const float* bias, i
         if (q + 2 < nq0) wide_load<G>(Wg, nQ, q + 2, in, lane, wc, xa, true);
       }
     } else {
-      // nQ is even (a hidden layer's output tiles are padded to a multiple of kWideGroup), so the
-      // loop body is two whole quads with no exit between them
+      // four register sets, each reloaded with the quad four ahead once its MFMAs are issued; nQ is
+      // a multiple of 4 (a hidden layer's output tiles are padded to a multiple of kWideGroup), so
+      // the loop body is four whole quads with no exit between them
+      float4 wc[G], wd[G], xc = {0.f, 0.f, 0.f, 0.f}, xd = {0.f, 0.f, 0.f, 0.f};
+      wide_load<G>(Wg, nQ, 2, in, lane, wc, xc, false);
+      wide_load<G>(Wg, nQ, 3, in, lane, wd, xd, false);
 #pragma unroll 1
-      for (int q = 0; q < nQ; q += 2) {
+      for (int q = 0; q < nQ; q += 4) {
         const float xs0[4] = {xa.x, xa.y, xa.z, xa.w};
         wide_mfma<G>(wa, xs0, acc);
-        wide_load<G>(Wg, nQ, q + 2 < nQ ? q + 2 : nQ - 1, in, lane, wa, xa, false);   // the tail reloads
+        wide_load<G>(Wg, nQ, q + 4 < nQ ? q + 4 : nQ - 1, in, lane, wa, xa, false);   // the tail reloads
         const float xs1[4] = {xb.x, xb.y, xb.z, xb.w};
         wide_mfma<G>(wb, xs1, acc);
-        wide_load<G>(Wg, nQ, q + 3 < nQ ? q + 3 : nQ - 1, in, lane, wb, xb, false);
+        wide_load<G>(Wg, nQ, q + 5 < nQ ? q + 5 : nQ - 1, in, lane, wb, xb, false);
+        const float xs2[4] = {xc.x, xc.y, xc.z, xc.w};
+        wide_mfma<G>(wc, xs2, acc);
+        wide_load<G>(Wg, nQ, q + 6 < nQ ? q + 6 : nQ - 1, in, lane, wc, xc, false);
+        const float xs3[4] = {xd.x, xd.y, xd.z, xd.w};
+        wide_mfma<G>(wd, xs3, acc);
+        wide_load<G>(Wg, nQ, q + 7 < nQ ? q + 7 : nQ - 1, in, lane, wd, xd, false);
       }
     }
     if (kHead) {
