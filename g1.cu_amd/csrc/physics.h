@@ -328,8 +328,72 @@ struct LaneModel {
   float kp, kd, clo, chi, flo, fhi, qstand, bdt, arm;
 };
 
+// The model constants world_qacc reads on every call, as one row per lane of a world group (the
+// values lane_model gives the lane: body 0's where the lane has no body, actuator 0's where it has
+// no hinge) plus the lane's FK ancestor word and foot sphere: one table base and immediate offsets
+// for every field, where a table per field took a base of its own (three scalar instructions) and a
+// 64-bit lane address each, every substep.
+struct alignas(16) LaneRow {
+  float bpos[3], bquat[4], ipos[3], iquat[4], inert[3], axis[3];
+  float mass, bdt;              // body mass; dt k_d of the lane's actuator
+  unsigned anc;                 // ancestor lanes of the FK rounds, one byte per round (tree.h)
+  float foot_lp[3], foot_w0;    // the lane's foot sphere (sphere 0 on lanes >= kNFoot)
+  float pad;
+};
+static_assert(sizeof(LaneRow) == 112, "seven 16-byte loads per row");
+struct LaneRows {
+  LaneRow r[kGroup];
+};
+constexpr LaneRows make_lane_rows() {
+  LaneRows t{};
+  for (int l = 0; l < kGroup; ++l) {
+    LaneRow& x = t.r[l];
+    const bool body = l >= 1 && l < kNBody, hinge = l >= 2 && l < kNBody;
+    const int b = body ? l : 0, j = body ? b - 1 : 0, i = hinge ? b - 2 : 0;
+    for (int k = 0; k < 3; ++k) {
+      x.bpos[k] = MF::body_pos[3 * b + k];
+      x.ipos[k] = MF::body_ipos[3 * b + k];
+      x.inert[k] = MF::body_inertia[3 * b + k];
+      x.axis[k] = MF::jnt_axis[3 * j + k];
+    }
+    for (int k = 0; k < 4; ++k) {
+      x.bquat[k] = MF::body_quat[4 * b + k];
+      x.iquat[k] = MF::body_iquat[4 * b + k];
+    }
+    x.mass = MF::body_mass[b];
+    x.bdt = MF::dt * MF::act_kd[i];   // the single fp32 product lane_model forms
+    x.anc = kAncestorWords.w[l];
+    const int sph = l < kNFoot ? l : 0;
+    for (int k = 0; k < 3; ++k) x.foot_lp[k] = MF::foot_lpos[3 * sph + k];
+    x.foot_w0 = MF::foot_invweight0[sph];
+    x.pad = 0.f;
+  }
+  return t;
+}
+constexpr LaneRows kLaneRows = make_lane_rows();
+
+// Row l from one address (16-byte loads of the used words): the table base goes through an opaque copy (with
+// the address visible the compiler folds field offsets into the base's relocation and gives each
+// group of fields a base and a 64-bit lane address of its own) and the lane index is unsigned (a
+// 32-bit row offset).
+__device__ __forceinline__ LaneRow lane_row(int l) {
+  static_assert(sizeof(LaneRow) % 16 == 0, "whole 16-byte words per row");
+  typedef const __attribute__((address_space(1))) char* GlobalBytes;   // global loads, not flat ones
+  typedef const __attribute__((address_space(1))) float* GlobalFloats;
+  GlobalBytes base = (GlobalBytes)(reinterpret_cast<const char*>(&kLaneRows.r[0]));
+  __asm__("" : "+s"(base));
+  GlobalFloats p = (GlobalFloats)(base + (unsigned)l * sizeof(LaneRow));
+  float w[sizeof(LaneRow) / 4];
+#pragma unroll
+  for (int k = 0; k < (int)(sizeof(LaneRow) / 4); ++k) w[k] = p[k];
+  LaneRow R;
+  __builtin_memcpy(&R, w, sizeof(LaneRow));
+  return R;
+}
+
 __device__ __forceinline__ LaneModel lane_model(int l) {
   LaneModel L;
+  const LaneRow R = lane_row(l);
   L.l = l;
   L.body = (l >= 1 && l < kNBody);
   L.hinge = (l >= 2 && l < kNBody);
@@ -342,20 +406,19 @@ __device__ __forceinline__ LaneModel lane_model(int l) {
   L.c0 = (L.nchild > 0) ? c0 : l;
   L.c1 = (L.nchild > 1) ? c1 : l;
   L.c2 = (L.nchild > 2) ? c2 : l;
-  L.bpos = {MF::body_pos[3 * b], MF::body_pos[3 * b + 1], MF::body_pos[3 * b + 2]};
-  L.bquat = {MF::body_quat[4 * b], MF::body_quat[4 * b + 1], MF::body_quat[4 * b + 2], MF::body_quat[4 * b + 3]};
-  L.ipos = {MF::body_ipos[3 * b], MF::body_ipos[3 * b + 1], MF::body_ipos[3 * b + 2]};
-  L.iquat = {MF::body_iquat[4 * b], MF::body_iquat[4 * b + 1], MF::body_iquat[4 * b + 2], MF::body_iquat[4 * b + 3]};
-  L.inert = {MF::body_inertia[3 * b], MF::body_inertia[3 * b + 1], MF::body_inertia[3 * b + 2]};
-  L.mass = MF::body_mass[b];
-  const int j = L.body ? b - 1 : 0;   // one joint per moving body (generator-checked)
-  L.axis = {MF::jnt_axis[3 * j], MF::jnt_axis[3 * j + 1], MF::jnt_axis[3 * j + 2]};
+  L.bpos = {R.bpos[0], R.bpos[1], R.bpos[2]};
+  L.bquat = {R.bquat[0], R.bquat[1], R.bquat[2], R.bquat[3]};
+  L.ipos = {R.ipos[0], R.ipos[1], R.ipos[2]};
+  L.iquat = {R.iquat[0], R.iquat[1], R.iquat[2], R.iquat[3]};
+  L.inert = {R.inert[0], R.inert[1], R.inert[2]};
+  L.mass = R.mass;
+  L.axis = {R.axis[0], R.axis[1], R.axis[2]};   // one joint per moving body (generator-checked)
   const int i = L.hinge ? b - 2 : 0;
   L.kp = MF::act_kp[i]; L.kd = MF::act_kd[i];
   L.clo = MF::act_ctrl_lo[i]; L.chi = MF::act_ctrl_hi[i];
   L.flo = MF::act_frc_lo[i]; L.fhi = MF::act_frc_hi[i];
   L.qstand = L.hinge ? MF::qpos_stand[b + 5] : 0.f;
-  L.bdt = MF::dt * MF::act_kd[i];
+  L.bdt = R.bdt;
   L.arm = L.hinge ? MF::dof_armature[b + 4] : 0.f;
   return L;
 }
@@ -548,14 +611,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   __asm__ volatile("" : "+v"(l));
   const LaneModel L = lane_model(l);
   const bool base = (l == 1);
-  // Lane-indexed table reads of the FK rounds and the contact detection, issued with the lane
-  // model so that their latency passes under the hinge sincos instead of stalling the phase that
-  // uses them: the ancestor lanes of every doubling round (one byte per round) and the lane's foot
-  // sphere (local position, invweight0).
-  const unsigned anc = kAncestorWords.w[l];
+  // The lane's FK ancestor word (one byte per doubling round) and foot sphere (local position,
+  // invweight0), read from its row with the lane model, so that their latency passes under the
+  // hinge sincos instead of stalling the phase that uses them.
+  const LaneRow R = lane_row(l);
+  const unsigned anc = R.anc;
   const int sph = l < kNFoot ? l : 0;
-  const V3 foot_lp{MF::foot_lpos[3 * sph], MF::foot_lpos[3 * sph + 1], MF::foot_lpos[3 * sph + 2]};
-  const float foot_w0 = MF::foot_invweight0[sph];
+  const V3 foot_lp{R.foot_lp[0], R.foot_lp[1], R.foot_lp[2]};
+  const float foot_w0 = R.foot_w0;
 
   // ---------------- forward kinematics (reference: src/dynamics.cuh:47-88) by ancestor doubling
   // Each lane starts from its body's transform relative to its parent (hinge: translation
