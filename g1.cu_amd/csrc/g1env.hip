@@ -97,7 +97,7 @@ __global__ void __launch_bounds__(kPhysThreads) k_physics(PhysArgs a) {
     const int k = (unsigned)j < nreg ? j / nch : a.K - 1;
     const int c = j - k * nch;
     if (j > 0) wait_flag(a.flags + p, a.fbase + (unsigned)j, a.qerr, a.xlocal);
-    physics_item(kernarg_reread<PhysArgs>(), s, L, g, l, p, k, c, hcnt);
+    physics_item(kernarg_reread<PhysArgs>(), s, L, g, l, 2 * p + g, k, c, hcnt);
     release_flag(a.flags + p, a.fbase + (unsigned)j + 1u, a.xlocal);
   }
   if (a.ncon_hist && l < 9 && hcnt) atomicAdd(&a.ncon_hist[l], (unsigned long long)hcnt);
@@ -574,6 +574,8 @@ struct EnvState {
   int fused;        // 1: g1_rollout runs k_rollout when the policy shape allows it
   unsigned* tflags;
   unsigned* tcount;
+  unsigned long long* tperm;   // per tile: the pairing of its worlds in the current step
+  unsigned char* cflag;        // per world: contacts at the last substep of its last control step
   unsigned tdone;
   float* Wt;
   long Wt_cap;
@@ -861,6 +863,8 @@ static void rollout_fused(EnvState* E, int H, const float* W, const float* mean,
   ra.tflags = E->tflags;
   ra.tbase = E->tdone;
   ra.tcount = E->tcount;
+  ra.tperm = E->tperm;
+  a.cflag = E->cflag;
   const bool prof = E->prof_on != 0 && !wp;
   if (prof) prof_mark(E->ev_phys, E->n_phys);
   launch_rollout_kernel(ra, E->pgrid);
@@ -955,6 +959,9 @@ void* g1_env_create(int N, int substeps, int pgs_iters, unsigned long seed) {
   HIPCHECK(hipMemset(E->tflags, 0, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
   dev_alloc(E, &E->tcount, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned));
   HIPCHECK(hipMemset(E->tcount, 0, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned)));
+  dev_alloc(E, &E->tperm, (size_t)kQueues * tiles_per_queue(N) * sizeof(unsigned long long));   // set by each launch
+  dev_alloc(E, &E->cflag, (size_t)N);
+  HIPCHECK(hipMemset(E->cflag, 0, (size_t)N));
   E->tdone = 0;
   E->fused = 1;
   {
@@ -1005,8 +1012,8 @@ void g1_env_destroy(void* h) {
   check_queue(E);
   void* bufs[] = {E->qp,       E->qv,      E->pa,        E->steps,   E->rng,  E->dact,
                   E->zero_act, E->bench_r, E->bench_d,   E->ncon_hist, E->Wp,  E->dout,
-                  E->qflags,   E->qctr,    E->qerr,      E->qacc_e,  E->qacc_vx, E->tflags, E->tcount, E->Wt,
-                  E->scr};
+                  E->qflags,   E->qctr,    E->qerr,      E->qacc_e,  E->qacc_vx, E->tflags, E->tcount, E->tperm,
+                  E->cflag,    E->Wt,      E->scr};
   for (void* b : bufs)
     if (b) HIPCHECK(hipFree(b));
   if (E->h_act) HIPCHECK(hipHostFree(E->h_act));

@@ -37,6 +37,8 @@ struct PhysArgs {
   int cst[kMaxChunks + 1];         //   chunk c = substeps [cst[c], cst[c + 1]), cst[nch] = S
   int nchl;                        // the same for the launch's last control step (k = K - 1)
   int cstl[kMaxChunks + 1];
+  unsigned char* cflag;            // [N] or null: 1 where the world had contacts at the last substep
+                                   //   of its last completed control step (k_rollout's tile pairing)
 };
 
 constexpr int kPhysThreads = 64;   // one wave64 = two 32-lane world groups
@@ -95,11 +97,10 @@ __device__ __forceinline__ void release_flag(unsigned* flag, unsigned value, int
 // src/g1_env.cu:118-212, the k_rollout substep loop :319-325). Every input a previous item or launch
 // wrote is read from the L2 (the actions too: in k_rollout the policy items of the same launch
 // write them).
-__device__ __forceinline__ void physics_item(const PhysArgs& a, WorldLds& s, const LaneModel& L, int g, int l, int p,
+__device__ __forceinline__ void physics_item(const PhysArgs& a, WorldLds& s, const LaneModel& L, int g, int l, int w,
                                              int k, int c, unsigned& hcnt) {
   const int ai = L.hinge ? L.b - 2 : 0;
   const SolveParams P{a.pgs, a.mu, true, true};
-  const int w = 2 * p + g;
   const bool wvalid = w < a.N;
   const int wc = wvalid ? w : a.N - 1;   // an odd N's last group repeats world N - 1 and stores nothing
 
@@ -126,6 +127,7 @@ __device__ __forceinline__ void physics_item(const PhysArgs& a, WorldLds& s, con
   const bool lastk = k == a.K - 1;   // the launch's last control step has a chunk table of its own
   const int nck = lastk ? a.nchl : a.nch;
   const int s0 = lastk ? a.cstl[c] : a.cst[c], s1 = lastk ? a.cstl[c + 1] : a.cst[c + 1];
+  int nc_last = 0;   // the world's contacts at its last substep
 #pragma unroll 1
   for (int sub = s0; sub < s1; ++sub) {
     float jtau = 0.f;
@@ -139,6 +141,7 @@ __device__ __forceinline__ void physics_item(const PhysArgs& a, WorldLds& s, con
     float bqacc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, jqacc = 0.f;
     const int nc = world_qacc(l, s, st, jtau, P, bqacc, jqacc);
     hcnt += (l == nc && wvalid) ? 1u : 0u;
+    nc_last = nc;
     integrate_lane(L, st, bqacc, jqacc, true);
     vx_sum += st.bqd[0];
   }
@@ -191,6 +194,8 @@ __device__ __forceinline__ void physics_item(const PhysArgs& a, WorldLds& s, con
     }
     rng += 1;
     if (wvalid) {
+      // contacts at the last substep, or a reset to the stand pose (feet on the ground)
+      if (a.cflag && l == 0) a.cflag[w] = (nc_last > 0 || d_flag) ? 1 : 0;
       if (l == 1) {
         const long o = (long)(a.t0 + k * a.rstep) * a.N + w;
         a.R[o] = r;
@@ -252,6 +257,8 @@ struct RolloutArgs {
   unsigned tbase;           // value every tile flag holds when this launch starts
   unsigned* tcount;         // [kQueues * tiles per queue] pairs of a tile done with the current step
                             // (zero between launches)
+  unsigned long long* tperm;   // [kQueues * tiles per queue] the tile's pairing of the current step:
+                               //   nibble 2 i + g = the world slot that group g of pair slot i runs
 };
 
 // A kernel's by-value argument block (its only argument, at offset 0 of the kernarg segment),

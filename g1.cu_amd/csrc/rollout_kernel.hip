@@ -60,6 +60,29 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
     } else {
       policy_tile<1>(rb.po, b.qp, b.qv, b.pa, b.rng, b.seed, b.N, t, w, valid, scratch_lds, ld);
     }
+    // The tile's pairing for step t: the worlds that had contacts at the last substep of step t - 1
+    // first (a stable partition of the 16 slots), so that consecutive slots form the pairs: a wave
+    // runs the contact pipeline when either of its worlds has contacts, and contact at the end of a
+    // step predicts it in the next (fixed pairs run it in ~70% of config 3's pair-substeps, these
+    // ~64%). Which two worlds share a wave changes no result. Step 0 and partial tiles keep the
+    // fixed pairs (slot 2 i + g runs group g of pair slot i).
+    if (rb.tperm) {
+      unsigned long long pm = 0xFEDCBA9876543210ull;
+      if (t > 0 && np == kTilePairs && tile_world(qq, u, 2 * kTilePairs - 1, kQueues) < b.N) {
+        const bool in = ld_l2(b.cflag + w) != 0;
+        const unsigned mask16 = (1u << jw) - 1u;
+        const unsigned bal = (unsigned)__ballot(in) & 0xFFFFu;   // lanes 0..15: slots 0..15
+        const int pos = in ? __popc(bal & mask16) : __popc(bal) + __popc(~bal & mask16);
+        unsigned lo = pos < 8 ? (unsigned)jw << (4 * pos) : 0u, hi = pos >= 8 ? (unsigned)jw << (4 * (pos - 8)) : 0u;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+          lo |= __shfl_xor(lo, o, 16);
+          hi |= __shfl_xor(hi, o, 16);
+        }
+        pm = ((unsigned long long)hi << 32) | lo;
+      }
+      if (threadIdx.x == 0) rb.tperm[qq + kQueues * u] = pm;
+    }
     release_flag(ra.tflags + qq + kQueues * u, ra.tbase + (unsigned)t + 1u, a.xlocal);
   };
 
@@ -101,7 +124,14 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
       int lo = l;
       __asm__ volatile("" : "+v"(lo));
       const LaneModel L = lane_model(lo);
-      physics_item(kernarg_reread<RolloutArgs>().ph, s, L, g, l, p, t, c, hcnt);
+      // this group's world: slot (pairing nibble 2 i + g) of the pair's tile, i = m mod 8
+      const RolloutArgs& rb = kernarg_reread<RolloutArgs>();
+      int w = 2 * p + g;
+      if (rb.tperm) {
+        const unsigned long long pm = ld_l2(rb.tperm + qc + kQueues * u);
+        w = tile_world(qc, u, (int)((pm >> (4 * (2 * (m % kTilePairs) + g))) & 15ull), kQueues);
+      }
+      physics_item(rb.ph, s, L, g, l, w, t, c, hcnt);
     }
     release_flag(a.flags + p, a.fbase + (unsigned)jj + 1u, a.xlocal);
     if (c == nck - 1) {

@@ -202,10 +202,13 @@ def test_rollout_teacher_forced_one_launch_shapes(g1, orc, hidden, act):
 def test_one_launch_rollout_equals_step_by_step(g1):
     """The one-launch rollout cuts a control step into work items by the work per wave: at the
     benchmark's shape (N=8192, H=32) every step but the last is one item and the last two (6 and 4
-    substeps); a launch per control step (H=1) cuts each step into 3,3,2,2. Item boundaries only
-    hand a pair's state over and the policy tiles are the same, so one H=32 launch equals 32 H=1
-    launches bit for bit: every trajectory output, the bootstrap value and the final state (with
-    timeouts and auto-resets inside the horizon)."""
+    substeps); a launch per control step (H=1) cuts each step into 3,3,2,2. From its second step on
+    the one launch also pairs each tile's worlds by their contact state (the worlds in contact at
+    the end of the previous step share waves), while a launch's first step keeps the fixed pairs.
+    Item boundaries only hand a pair's state over, which two worlds share a wave changes no result,
+    and the policy tiles are the same, so one H=32 launch equals 32 H=1 launches bit for bit: every
+    trajectory output, the bootstrap value and the final state (with timeouts and auto-resets inside
+    the horizon)."""
     N, H = 8192, 32
     qp, qv, pa, steps, W, mean, var, an, rn = _setup(N, H, 71)
     steps[::7] = 969 + np.arange(steps[::7].size) % 31   # timeouts and auto-resets inside the horizon
