@@ -37,8 +37,9 @@ struct PhysArgs {
   int cst[kMaxChunks + 1];         //   chunk c = substeps [cst[c], cst[c + 1]), cst[nch] = S
   int nchl;                        // the same for the launch's last control step (k = K - 1)
   int cstl[kMaxChunks + 1];
-  unsigned char* cflag;            // [N] or null: 1 where the world had contacts at the last substep
-                                   //   of its last completed control step (k_rollout's tile pairing)
+  unsigned char* cflag;            // [N] or null: the world's contacts at the last substep of its
+                                   //   last completed control step, 9 after an auto-reset (k_rollout's
+                                   //   tile pairing)
 };
 
 constexpr int kPhysThreads = 64;   // one wave64 = two 32-lane world groups
@@ -194,8 +195,8 @@ __device__ __forceinline__ void physics_item(const PhysArgs& a, WorldLds& s, con
     }
     rng += 1;
     if (wvalid) {
-      // contacts at the last substep, or a reset to the stand pose (feet on the ground)
-      if (a.cflag && l == 0) a.cflag[w] = (nc_last > 0 || d_flag) ? 1 : 0;
+      // contacts at the last substep, or 9 after a reset to the stand pose (both feet down)
+      if (a.cflag && l == 0) a.cflag[w] = (unsigned char)(d_flag ? 9 : nc_last);
       if (l == 1) {
         const long o = (long)(a.t0 + k * a.rstep) * a.N + w;
         a.R[o] = r;

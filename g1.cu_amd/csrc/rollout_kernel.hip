@@ -60,19 +60,26 @@ __global__ void __launch_bounds__(kPhysThreads) k_rollout(RolloutArgs ra) {
     } else {
       policy_tile<1>(rb.po, b.qp, b.qv, b.pa, b.rng, b.seed, b.N, t, w, valid, scratch_lds, ld);
     }
-    // The tile's pairing for step t: the worlds that had contacts at the last substep of step t - 1
-    // first (a stable partition of the 16 slots), so that consecutive slots form the pairs: a wave
-    // runs the contact pipeline when either of its worlds has contacts, and contact at the end of a
-    // step predicts it in the next (fixed pairs run it in ~70% of config 3's pair-substeps, these
-    // ~64%). Which two worlds share a wave changes no result. Step 0 and partial tiles keep the
-    // fixed pairs (slot 2 i + g runs group g of pair slot i).
+    // The tile's pairing for step t: its 16 slots in descending order of their worlds' contact
+    // counts at the last substep of step t - 1 (a stable sort; 9 after an auto-reset), so that
+    // consecutive slots form the pairs: a wave runs the contact pipeline when either of its worlds
+    // has contacts, at a cost that grows with the larger count, and the counts at the end of a step
+    // predict the next (fixed pairs run it in ~70% of config 3's pair-substeps, these ~63%). Which
+    // two worlds share a wave changes no result. Step 0 and partial tiles keep the fixed pairs
+    // (slot 2 i + g runs group g of pair slot i).
     if (rb.tperm) {
       unsigned long long pm = 0xFEDCBA9876543210ull;
       if (t > 0 && np == kTilePairs && tile_world(qq, u, 2 * kTilePairs - 1, kQueues) < b.N) {
-        const bool in = ld_l2(b.cflag + w) != 0;
+        const int key = min((int)ld_l2(b.cflag + w), 9);
         const unsigned mask16 = (1u << jw) - 1u;
-        const unsigned bal = (unsigned)__ballot(in) & 0xFFFFu;   // lanes 0..15: slots 0..15
-        const int pos = in ? __popc(bal & mask16) : __popc(bal) + __popc(~bal & mask16);
+        // position = slots with a larger key + earlier slots with the same key (lanes 0..15 hold
+        // slots 0..15; the other lanes repeat them)
+        int pos = 0;
+#pragma unroll
+        for (int v = 0; v <= 9; ++v) {
+          const unsigned bv = (unsigned)__ballot(key == v) & 0xFFFFu;
+          pos += v > key ? __popc(bv) : (v == key ? __popc(bv & mask16) : 0);
+        }
         unsigned lo = pos < 8 ? (unsigned)jw << (4 * pos) : 0u, hi = pos >= 8 ? (unsigned)jw << (4 * (pos - 8)) : 0u;
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) {
