@@ -290,31 +290,35 @@ __device__ __forceinline__ float foot_impedance(float pos) {
 }
 
 // ---------------------------------------------------------------- per-world LDS
+// Every array starts on a 16-byte boundary: adjacent float reads and writes then combine into
+// 8- and 16-byte LDS instructions, which take 16-bit immediate offsets from the world's base
+// address; two 4-byte ones combined into a read2/write2 take 8-bit offsets (in words, at most 1020
+// bytes), and past that each pair got an address of its own (a vector add per pair).
 struct WorldLds {
   union {
     struct {
-      float S[kNV][6];      // motion axes (world axes about the pelvis origin)
-      float U[kNBody][6];   // hinge factor columns I^A S
-      float invD[kNBody];   // hinge 1/(S'I^A S + armature + dt kd)
-      float Dfac[36];       // Cholesky factor of the free-joint 6x6 block
-      float Dinv[6];        // RN(1 / diagonal of Dfac)
-      float us[kNBody];     // hinge bias u = x - S.pA of the smooth solve
-      float IA1[21];        // articulated inertia of the pelvis (packed)
-      float Dm[36];         // free-joint 6x6 block before factoring
+      alignas(16) float S[kNV][6];      // motion axes (world axes about the pelvis origin)
+      alignas(16) float U[kNBody][6];   // hinge factor columns I^A S
+      alignas(16) float invD[kNBody];   // hinge 1/(S'I^A S + armature + dt kd)
+      alignas(16) float Dfac[36];       // Cholesky factor of the free-joint 6x6 block
+      alignas(16) float Dinv[6];        // RN(1 / diagonal of Dfac)
+      alignas(16) float us[kNBody];     // hinge bias u = x - S.pA of the smooth solve
+      alignas(16) float IA1[21];        // articulated inertia of the pelvis (packed)
+      alignas(16) float Dm[36];         // free-joint 6x6 block before factoring
     } fac;
-    float G[kPairs][9];     // 3x3 Gram blocks of contact pairs c <= c' (after the solves)
+    alignas(16) float G[kPairs][9];     // 3x3 Gram blocks of contact pairs c <= c' (after the solves)
   } u;
-  float qvel[kNV + 1];
-  float Mm[kCols][kMmStride];          // solve outputs: column 0 = qacc_smooth, 1+3c+a = M^-1 e_{c,a}
-  float Eb[kNFoot][3][kContactDofs];   // contact basis rows over the contact's 12 ancestor dofs
-  float con[kNFoot][4];                // contact point x, y, z (= pen/2), penetration
-  float con_w0[kNFoot];                // invweight0 of the foot body
-  int con_leg[kNFoot];                 // 0: left foot (body 7), 1: right foot (body 13)
-  float bvec[kMaxEfc];
-  float aref[kMaxEfc];
-  float Rc[kNFoot];
-  float f[kMaxEfc];
-  float qacc[kNV + 1];
+  alignas(16) float qvel[kNV + 1];
+  alignas(16) float Mm[kCols][kMmStride];          // solve outputs: column 0 = qacc_smooth, 1+3c+a = M^-1 e_{c,a}
+  alignas(16) float Eb[kNFoot][3][kContactDofs];   // contact basis rows over the contact's 12 ancestor dofs
+  alignas(16) float con[kNFoot][4];                // contact point x, y, z (= pen/2), penetration
+  alignas(16) float con_w0[kNFoot];                // invweight0 of the foot body
+  alignas(16) int con_leg[kNFoot];                 // 0: left foot (body 7), 1: right foot (body 13)
+  alignas(16) float bvec[kMaxEfc];
+  alignas(16) float aref[kMaxEfc];
+  alignas(16) float Rc[kNFoot];
+  alignas(16) float f[kMaxEfc];
+  alignas(16) float qacc[kNV + 1];
 };
 
 // ---------------------------------------------------------------- per-lane model constants
