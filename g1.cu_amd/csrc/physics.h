@@ -37,6 +37,8 @@ using MF = ModelT<float>;
 constexpr int kCols = 1 + 3 * kNFoot;  // smooth column + 3 basis columns per contact
 constexpr int kChainSolveCon = 2;      // contacts per world up to which the M^-1 solves use the chain layout
 constexpr int kMmStride = 37;          // odd stride: column-parallel LDS reads are conflict-free
+constexpr int kRow = 8;              // row stride of the motion axes S and factor columns U (6 used):
+                                     // 16-byte rows, read whole by 16-byte LDS instructions
 constexpr int kPairs = kNFoot * (kNFoot + 1) / 2;
 
 struct V3 { float x, y, z; };
@@ -297,8 +299,8 @@ __device__ __forceinline__ float foot_impedance(float pos) {
 struct WorldLds {
   union {
     struct {
-      alignas(16) float S[kNV][6];      // motion axes (world axes about the pelvis origin)
-      alignas(16) float U[kNBody][6];   // hinge factor columns I^A S
+      alignas(16) float S[kNV][kRow];      // motion axes (world axes about the pelvis origin)
+      alignas(16) float U[kNBody][kRow];   // hinge factor columns I^A S
       alignas(16) float invD[kNBody];   // hinge 1/(S'I^A S + armature + dt kd)
       alignas(16) float Dfac[36];       // Cholesky factor of the free-joint 6x6 block
       alignas(16) float Dinv[6];        // RN(1 / diagonal of Dfac)
@@ -806,7 +808,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     float* const pA = A6 + 6 * c_off + crow;
     float nS[5], nq;
     auto ld = [&](int r) {
-      nS[0] = pS0[6 * r]; nS[1] = pS1[6 * r]; nS[2] = pS2[6 * r]; nS[3] = pS3[6 * r]; nS[4] = pS4[6 * r];
+      nS[0] = pS0[kRow * r]; nS[1] = pS1[kRow * r]; nS[2] = pS2[kRow * r]; nS[3] = pS3[kRow * r]; nS[4] = pS4[kRow * r];
       nq = pq[r];
     };
     ld(2);
@@ -983,7 +985,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   auto prefetch = [&](int cd) {
     const int b = chain_body(cd);
 #pragma unroll
-    for (int j = 0; j < 6; ++j) { Sn[j] = pSc[6 * cd + j]; In[j] = pIc[j][21 * cd]; }
+    for (int j = 0; j < 6; ++j) { Sn[j] = pSc[kRow * cd + j]; In[j] = pIc[j][21 * cd]; }
     xn = pUs[cd];
     kn = gshfl(L.bdt, b);
   };
@@ -1025,7 +1027,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       Dlr[j] = dl;
       cs[j] = c;
     }
-    if (act && crow < 6) pUc[6 * cd] = ur;
+    if (act && crow < 6) pUc[kRow * cd] = ur;
     if (act && crow == 0) { pDc[cd] = invD; pUs[cd] = u; }
   };
   // Issue priority (s_setprio): two waves share a SIMD, and the phases that are dependency chains
@@ -1306,7 +1308,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       float nS[6], nU[6], nD, nE;
       auto ld = [&](int d) {
 #pragma unroll
-        for (int k = 0; k < 6; ++k) { nS[k] = pS[6 * d + k]; nU[k] = pU[6 * d + k]; }
+        for (int k = 0; k < 6; ++k) { nS[k] = pS[kRow * d + k]; nU[k] = pU[kRow * d + k]; }
         nD = pD[d];
         nE = eb[7 - d];   // xrhs(d + loff + 4) before its select (both legs: entry 7 - d)
       };
@@ -1358,7 +1360,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       float nS[6], nU[6], nD, nUs;
       auto ld = [&](int d) {
 #pragma unroll
-        for (int k = 0; k < 6; ++k) { nS[k] = pS[6 * d + k]; nU[k] = pU[6 * d + k]; }
+        for (int k = 0; k < 6; ++k) { nS[k] = pS[kRow * d + k]; nU[k] = pU[kRow * d + k]; }
         nD = pD[d];
         nUs = pUs[d];
       };
