@@ -61,13 +61,13 @@ __device__ __forceinline__ float gsum4(float v) {
   return v;
 }
 
-// maximum of an int over the whole wave (both groups): uniform trip counts for loops whose
-// length depends on per-world data
-__device__ __forceinline__ int wave_max(int v) {
-  int o = __shfl_xor(v, 32, 64);
-  // wave-uniform by construction: hand it to the scalar unit so the loops and branches it bounds
-  // compile to scalar compares instead of exec-mask regions
-  return __builtin_amdgcn_readfirstlane(v > o ? v : o);
+// maximum over the wave's two worlds of an int that is uniform within each 32-lane group (a
+// per-world count): uniform trip counts for loops whose length depends on per-world data. Read from
+// lanes 0 and 32 into scalar registers (no cross-lane LDS round trip), so that the loops and
+// branches it bounds compile to scalar compares instead of exec-mask regions.
+__device__ __forceinline__ int groups_max(int v) {
+  const int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 32);
+  return a > b ? a : b;
 }
 
 // Value of lane I of this lane's aligned 8-lane chain. (Two DPP moves instead of one ds_swizzle:

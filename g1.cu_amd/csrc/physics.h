@@ -700,7 +700,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   }
   // (detected right after FK: the contact count decides below who computes the smooth solve's
   // base and root -> leaf parts; the LDS writes are read after the later barriers)
-  const int ncon_max = wave_max(ncon);
+  const int ncon_max = groups_max(ncon);
 
   // ---------------- motion axes (reference: src/aba_bias.cuh:25-43)
   V3 sw{0.f, 0.f, 0.f}, sv{0.f, 0.f, 0.f};   // hinge axis (angular; linear)
@@ -924,11 +924,17 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // order), so the factor's sweep only reads x_b.
   {
     float* const pF = Fo + 6 * c_off + rowc;
+    // every level's own force read before the sweep (each level reads its own slot once, before
+    // it stores it): the reads go out together instead of one LDS round trip per level, which the
+    // stores' branches kept the scheduler from overlapping
+    float Fl[kMaxDepth + 1];
+#pragma unroll
+    for (int cd = kMaxDepth; cd >= 2; --cd) Fl[cd] = pF[6 * cd];
     float Fc = 0.f;   // component rowc of the last body's subtree force
 #pragma unroll
     for (int cd = kMaxDepth; cd >= 2; --cd) {
       const bool act = cd >= c_lo && cd <= c_hi;
-      float F = pF[6 * cd];
+      float F = Fl[cd];
       if (cd == kTorsoDepth) {
         // the right arm (chain 3) ends at depth 5; its force joins the torso (chain 2) first
         const float g24 = from_next_chain(Fc);
