@@ -941,7 +941,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         F = grp == 2 ? F + g24 : F;
       }
       F = cd == c_hi ? F : F + Fc;
-      if (act && crow < 6) pF[6 * cd] = F;
+      // lanes 6 and 7 of a chain repeat row 5 (rowc) and store the same value to the same slot
+      if (act) pF[6 * cd] = F;
       Fc = F;
     }
     // pelvis, component r on lane r of chain 0 (chain 2's and chain 1's roots reach chain 0's
@@ -988,12 +989,19 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   float* const pUc = &s.u.fac.U[c_off][crow];
   float* const pDc = &s.u.fac.invD[c_off];
   float* const pUs = &s.u.fac.us[c_off];
+  // two levels in flight: level cd computes from (Sn, In, xn, kn) while the next level's inputs
+  // (Sm, Im, xm, km) arrive and the one after it is requested
+  float Sm[6], Im[6], xm, km;
   auto prefetch = [&](int cd) {
     const int b = chain_body(cd);
 #pragma unroll
-    for (int j = 0; j < 6; ++j) { Sn[j] = pSc[kRow * cd + j]; In[j] = pIc[j][21 * cd]; }
-    xn = pUs[cd];
-    kn = gshfl(L.bdt, b);
+    for (int j = 0; j < 6; ++j) { Sn[j] = Sm[j]; In[j] = Im[j]; }
+    xn = xm;
+    kn = km;
+#pragma unroll
+    for (int j = 0; j < 6; ++j) { Sm[j] = pSc[kRow * cd + j]; Im[j] = pIc[j][21 * cd]; }
+    xm = pUs[cd];
+    km = gshfl(L.bdt, b);
   };
   // one level of the chains; `junction` adds the right arm's downdate and bias force (gD, gc)
   // to the torso before its own child's
@@ -1012,12 +1020,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       IAr[j] = leaf ? v : v + Dlr[j];
       pA[j] = leaf ? 0.f : (junction ? gc[j] + cs[j] : cs[j]);
     }
+    // the inputs of two levels down, as soon as this level's are taken (depths 1 and 0 load
+    // bodies that are never used)
+    prefetch(cd - 2);
     float ur = 0.f;
 #pragma unroll
     for (int j = 0; j < 6; ++j) ur = fmaf_(IAr[j], Sd[j], ur);
     const float Ub[6] = {chain_bcast<0>(ur), chain_bcast<1>(ur), chain_bcast<2>(ur),
                          chain_bcast<3>(ur), chain_bcast<4>(ur), chain_bcast<5>(ur)};
-    prefetch(cd - 1);   // (cd - 1 == 1 loads body 2 again; unused)
     float D = dot6(Sd, Ub) + arm;
     if (P.damped) D += bdt;
     const float invD = rcp_rn(D);
@@ -1033,7 +1043,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       Dlr[j] = dl;
       cs[j] = c;
     }
-    if (act && crow < 6) pUc[kRow * cd] = ur;
+    // lanes 6 and 7 of a chain store into the row's padding (columns 6, 7 are never read)
+    if (act) pUc[kRow * cd] = ur;
     if (act && crow == 0) { pDc[cd] = invD; pUs[cd] = u; }
   };
   // Issue priority (s_setprio): two waves share a SIMD, and the phases that are dependency chains
@@ -1043,6 +1054,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // alone 12.64).
   __builtin_amdgcn_s_setprio(1);
   prefetch(kMaxDepth);
+  prefetch(kMaxDepth - 1);
   const float none[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int cd = kMaxDepth; cd > kTorsoDepth; --cd) level(cd, false, none, none);
