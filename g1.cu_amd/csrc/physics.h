@@ -311,8 +311,15 @@ struct WorldLds {
     alignas(16) float G[kPairs][9];     // 3x3 Gram blocks of contact pairs c <= c' (after the solves)
   } u;
   alignas(16) float qvel[kNV + 1];
-  alignas(16) float Mm[kCols][kMmStride];          // solve outputs: column 0 = qacc_smooth, 1+3c+a = M^-1 e_{c,a}
-  alignas(16) float Eb[kNFoot][3][kContactDofs];   // contact basis rows over the contact's 12 ancestor dofs
+  union {
+    struct {
+      alignas(16) float Mm[kCols][kMmStride];          // solve outputs: column 0 = qacc_smooth, 1+3c+a = M^-1 e_{c,a}
+      alignas(16) float Eb[kNFoot][3][kContactDofs];   // contact basis rows over the contact's 12 ancestor dofs
+    };
+    // body spatial inertias as full 6x6 rows (row r of body b: six floats at I6r[b][r]), from the
+    // body-inertia phase to the end of the factor, before the solves write Mm and PASS 1 Eb
+    alignas(16) float I6r[kNBody][6][6];
+  };
   alignas(16) float con[kNFoot][4];                // contact point x, y, z (= pen/2), penetration
   alignas(16) float con_w0[kNFoot];                // invweight0 of the foot body
   alignas(16) int con_leg[kNFoot];                 // 0: left foot (body 7), 1: right foot (body 13)
@@ -711,6 +718,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const int d = L.b + 4;
     s.u.fac.S[d][0] = sw.x; s.u.fac.S[d][1] = sw.y; s.u.fac.S[d][2] = sw.z;
     s.u.fac.S[d][3] = sv.x; s.u.fac.S[d][4] = sv.y; s.u.fac.S[d][5] = sv.z;
+    s.u.fac.S[d][6] = L.bdt;   // the row's padding carries the factor's dt kd (column 7: x_b)
     s.qvel[d] = st.jqd;
   }
   if (base) {
@@ -878,12 +886,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     Fw = {Iaw.x + cw.x, Iaw.y + cw.y, Iaw.z + cw.z};
     Fv = {Iav.x + cv.x, Iav.y + cv.y, Iav.z + cv.z};
   }
-  // ---------------- body spatial inertia about the pelvis origin, 21-packed (reference:
-  // src/aba_factor.cuh:51-76), staged in LDS for the chain-parallel factor. The solve-output
-  // region (Mm) is free until the factor is done and holds it.
-  static_assert(kCols * kMmStride >= kNBody * 27, "I6 and force staging fit the solve-output region");
-  float* const I6 = &s.Mm[0][0];
-  float* const Fo = I6 + kNBody * 21;      // [kNBody][6] each body's own RNE force (w, v)
+  // ---------------- body spatial inertia about the pelvis origin (reference:
+  // src/aba_factor.cuh:51-76), staged in LDS for the chain-parallel factor as full rows: entry
+  // (i, j) holds the packed upper-triangle value (min(i, j), max(i, j)), the reference's 21 numbers,
+  // so that a factor lane reads its row with three 8-byte reads instead of six scattered ones.
+  // The bodies' own forces go to the hinge-factor column rows (U), which the factor overwrites only
+  // for the hinge bodies 2..30: the pelvis' subtree force (row 1) is read after the factor.
+  static_assert(sizeof(float) * kNBody * kRow >= sizeof(float) * kNBody * 6, "force staging fits U");
+  float* const Fo = &s.u.fac.U[0][0];     // [kNBody][6] each body's own RNE force (w, v)
   if (L.body) {
     Fo[6 * L.b + 0] = Fw.x; Fo[6 * L.b + 1] = Fw.y; Fo[6 * L.b + 2] = Fw.z;
     Fo[6 * L.b + 3] = Fv.x; Fo[6 * L.b + 4] = Fv.y; Fo[6 * L.b + 5] = Fv.z;
@@ -910,7 +920,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
     for (int i = 0; i < 6; ++i)
 #pragma unroll
-      for (int j = i; j < 6; ++j) I6[L.b * 21 + symidx(i, j)] = M6[i * 6 + j];
+      for (int j = 0; j < 6; ++j) s.I6r[L.b][i][j] = M6[(i <= j ? i : j) * 6 + (i <= j ? j : i)];
   }
   wave_sync();   // S, I6 and the own forces of every body in LDS
 
@@ -957,7 +967,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     float bias = Sb[0] * Fb[0];
 #pragma unroll
     for (int j = 1; j < 6; ++j) bias = fmaf_(Sb[j], Fb[j], bias);
-    s.u.fac.us[L.b] = -bias + jtau;   // x_b; the factor replaces it by u_b = x_b - S_b.pA_b
+    s.u.fac.S[L.b + 4][7] = -bias + jtau;   // x_b, beside the axis for the factor, which stores u_b = x_b - S_b.pA_b
   }
   wave_sync();
 
@@ -975,33 +985,31 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // symmetric downdate equals the packed entries bit for bit.
   float Dlr[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // row `crow` of the last body's downdate
   float cs[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};    // last body's pA + U u / D (all six components)
-  // the next level's body inputs (motion axis, I6 row, right-hand side x_b, armature, dt kd; the
-  // last two live on lane b and come by shuffle), loaded while the current level computes
+  // the next level's body inputs (motion axis, I6 row, right-hand side x_b, dt kd; the last two in
+  // the axis row's padding), loaded while the current level computes
   float Sn[6], In[6], xn, kn;
   // every hinge has the same armature (the model's 0.01): a constant, not a per-body gather
   constexpr float kArm = MF::dof_armature[6];
   static_assert(hinge_armature_uniform(), "one armature for every hinge dof");
   // per-lane base pointers: depth cd's operands and results sit at constant offsets from them
   const float* const pSc = &s.u.fac.S[c_off + 4][0];
-  const float* pIc[6];
-#pragma unroll
-  for (int j = 0; j < 6; ++j) pIc[j] = I6 + 21 * c_off + symidx(rowc, j);
+  const float* const pIc = &s.I6r[c_off][rowc][0];
   float* const pUc = &s.u.fac.U[c_off][crow];
   float* const pDc = &s.u.fac.invD[c_off];
   float* const pUs = &s.u.fac.us[c_off];
   // two levels in flight: level cd computes from (Sn, In, xn, kn) while the next level's inputs
   // (Sm, Im, xm, km) arrive and the one after it is requested
   float Sm[6], Im[6], xm, km;
+  static_assert(kRow == 8, "axis row: six components, dt kd, x_b");
   auto prefetch = [&](int cd) {
-    const int b = chain_body(cd);
 #pragma unroll
     for (int j = 0; j < 6; ++j) { Sn[j] = Sm[j]; In[j] = Im[j]; }
     xn = xm;
     kn = km;
 #pragma unroll
-    for (int j = 0; j < 6; ++j) { Sm[j] = pSc[kRow * cd + j]; Im[j] = pIc[j][21 * cd]; }
-    xm = pUs[cd];
-    km = gshfl(L.bdt, b);
+    for (int j = 0; j < 6; ++j) { Sm[j] = pSc[kRow * cd + j]; Im[j] = pIc[36 * cd + j]; }
+    km = pSc[kRow * cd + 6];
+    xm = pSc[kRow * cd + 7];
   };
   // one level of the chains; `junction` adds the right arm's downdate and bias force (gD, gc)
   // to the torso before its own child's
@@ -1087,7 +1095,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     for (int j = 0; j < 6; ++j) {
       const float d14 = from_upper_row(Dlr[j]), d8 = from_next_chain(Dlr[j]);
       const float c14 = from_upper_row(cs[j]), c8 = from_next_chain(cs[j]);
-      I1[j] = ((I6[1 * 21 + symidx(rowc, j)] + d14) + d8) + Dlr[j];
+      I1[j] = ((s.I6r[1][rowc][j] + d14) + d8) + Dlr[j];
       pAs[j] = (c14 + c8) + cs[j];
     }
     if (l < 6) {
