@@ -37,8 +37,9 @@ using MF = ModelT<float>;
 constexpr int kCols = 1 + 3 * kNFoot;  // smooth column + 3 basis columns per contact
 constexpr int kChainSolveCon = 2;      // contacts per world up to which the M^-1 solves use the chain layout
 constexpr int kMmStride = 37;          // odd stride: column-parallel LDS reads are conflict-free
-constexpr int kRow = 8;              // row stride of the motion axes S and factor columns U (6 used):
+constexpr int kRow = 8;              // row stride of the motion axes S and factor rows U (6 + 2 used):
                                      // 16-byte rows, read whole by 16-byte LDS instructions
+constexpr int kInvD = 6, kUs = 7;    // columns of a hinge factor row past I^A S
 constexpr int kPairs = kNFoot * (kNFoot + 1) / 2;
 
 struct V3 { float x, y, z; };
@@ -300,11 +301,11 @@ struct WorldLds {
   union {
     struct {
       alignas(16) float S[kNV][kRow];      // motion axes (world axes about the pelvis origin)
-      alignas(16) float U[kNBody][kRow];   // hinge factor columns I^A S
-      alignas(16) float invD[kNBody];   // hinge 1/(S'I^A S + armature + dt kd)
+      // hinge factor rows: I^A S (0..5), 1/(S'I^A S + armature + dt kd) (kInvD), the smooth
+      // solve's bias u = x - S.pA (kUs); one row is read whole by two 16-byte reads
+      alignas(16) float U[kNBody][kRow];
       alignas(16) float Dfac[36];       // Cholesky factor of the free-joint 6x6 block
       alignas(16) float Dinv[6];        // RN(1 / diagonal of Dfac)
-      alignas(16) float us[kNBody];     // hinge bias u = x - S.pA of the smooth solve
       alignas(16) float IA1[21];        // articulated inertia of the pelvis (packed)
       alignas(16) float Dm[36];         // free-joint 6x6 block before factoring
     } fac;
@@ -995,8 +996,6 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   const float* const pSc = &s.u.fac.S[c_off + 4][0];
   const float* const pIc = &s.I6r[c_off][rowc][0];
   float* const pUc = &s.u.fac.U[c_off][crow];
-  float* const pDc = &s.u.fac.invD[c_off];
-  float* const pUs = &s.u.fac.us[c_off];
   // two levels in flight: level cd computes from (Sn, In, xn, kn) while the next level's inputs
   // (Sm, Im, xm, km) arrive and the one after it is requested
   float Sm[6], Im[6], xm, km;
@@ -1051,9 +1050,9 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       Dlr[j] = dl;
       cs[j] = c;
     }
-    // lanes 6 and 7 of a chain store into the row's padding (columns 6, 7 are never read)
-    if (act) pUc[kRow * cd] = ur;
-    if (act && crow == 0) { pDc[cd] = invD; pUs[cd] = u; }
+    // one store per level for the whole row: lanes 0..5 their column entry, lanes 6 and 7 (which
+    // compute invD and u as the others do) the reciprocal pivot and the bias
+    if (act) pUc[kRow * cd] = crow < 6 ? ur : (crow == kInvD ? invD : u);
   };
   // Issue priority (s_setprio): two waves share a SIMD, and the phases that are dependency chains
   // over the tree or the PGS rows (this factor: 1; the contact pipeline from PASS 1 through PGS: 3)
@@ -1216,8 +1215,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const int b = chain_body(r);
 #pragma unroll
       for (int k = 0; k < 6; ++k) { U[k] = s.u.fac.U[b][k]; S[k] = s.u.fac.S[b + 4][k]; }
-      us = s.u.fac.us[b];
-      iD = s.u.fac.invD[b];
+      us = s.u.fac.U[b][kUs];
+      iD = s.u.fac.U[b][kInvD];
     };
     ld(2);
 #pragma unroll
@@ -1330,12 +1329,12 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     {
       const float* const pS = &s.u.fac.S[loff + 4][0];
       const float* const pU = &s.u.fac.U[loff][0];
-      const float* const pD = &s.u.fac.invD[loff];
+      const float* const pD = &s.u.fac.U[loff][kInvD];
       float nS[6], nU[6], nD, nE;
       auto ld = [&](int d) {
 #pragma unroll
         for (int k = 0; k < 6; ++k) { nS[k] = pS[kRow * d + k]; nU[k] = pU[kRow * d + k]; }
-        nD = pD[d];
+        nD = pD[kRow * d];
         nE = eb[7 - d];   // xrhs(d + loff + 4) before its select (both legs: entry 7 - d)
       };
       ld(7);
@@ -1381,14 +1380,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     {
       const float* const pS = &s.u.fac.S[c_off + 4][0];
       const float* const pU = &s.u.fac.U[c_off][0];
-      const float* const pD = &s.u.fac.invD[c_off];
-      const float* const pUs = &s.u.fac.us[c_off];
+      const float* const pD = &s.u.fac.U[c_off][kInvD];
+      const float* const pUs = &s.u.fac.U[c_off][kUs];
       float nS[6], nU[6], nD, nUs;
       auto ld = [&](int d) {
 #pragma unroll
         for (int k = 0; k < 6; ++k) { nS[k] = pS[kRow * d + k]; nU[k] = pU[kRow * d + k]; }
-        nD = pD[d];
-        nUs = pUs[d];
+        nD = pD[kRow * d];
+        nUs = pUs[kRow * d];
       };
       ld(2);
       float ac[6];
@@ -1447,7 +1446,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     auto ld_up = [&](int b, UpIn& f) {
 #pragma unroll
       for (int k = 0; k < 6; ++k) { f.S[k] = s.u.fac.S[b + 4][k]; f.U[k] = s.u.fac.U[b][k]; }
-      f.iD = s.u.fac.invD[b];
+      f.iD = s.u.fac.U[b][kInvD];
       f.e = eb[b < 8 ? 7 - b : 13 - b];   // xrhs(b + 4) before its select
     };
     constexpr int kUpOrder[12] = {13, 7, 12, 6, 11, 5, 10, 4, 9, 3, 8, 2};
@@ -1501,8 +1500,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     auto ld_dn = [&](int b, DnIn& f) {
 #pragma unroll
       for (int k = 0; k < 6; ++k) { f.U[k] = s.u.fac.U[b][k]; f.S[k] = s.u.fac.S[b + 4][k]; }
-      f.iD = s.u.fac.invD[b];
-      f.us = s.u.fac.us[b];
+      f.iD = s.u.fac.U[b][kInvD];
+      f.us = s.u.fac.U[b][kUs];
     };
     constexpr int kDownOrder[29] = {2, 8, 14, 3, 9, 15, 4, 10, 16, 5, 11, 6, 12, 7, 13,
                                     17, 24, 18, 25, 19, 26, 20, 27, 21, 28, 22, 29, 23, 30};
