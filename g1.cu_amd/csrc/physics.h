@@ -792,12 +792,17 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   static_assert(kMaxDepth + 19 < kNBody, "chain bodies in range");
   static_assert(body_parent[2] == 1 && body_parent[8] == 1 && body_parent[14] == 1 && body_parent[24] == 16 &&
                 body_depth[24] == 5 && body_depth[2] == 2, "chain roots");
-  float* const V6 = &s.Mm[0][0];          // [kNBody][6] body velocities about the pelvis origin
-  float* const A6 = V6 + kNBody * 6;      // [kNBody][6] body accelerations
-  static_assert(kCols * kMmStride >= 2 * kNBody * 6, "RNE staging fits the solve-output region");
+  // body velocity and acceleration about the pelvis origin, interleaved per body (w, v of the
+  // velocity, two floats of padding where chain lanes 6 and 7 store, the acceleration likewise, four
+  // more): a lane stores both components of a level with one two-address LDS write, and the body
+  // stride of 20 words puts the four chains' rows of a level on different LDS banks
+  constexpr int kVA = 20;
+  float* const V6 = &s.Mm[0][0];
+  float* const A6 = V6 + kVA / 2;
+  static_assert(kCols * kMmStride >= kNBody * kVA && kVA / 2 >= 8, "RNE staging fits the solve-output region");
   if (base) {
-    V6[6 + 0] = vw.x; V6[6 + 1] = vw.y; V6[6 + 2] = vw.z; V6[6 + 3] = vv.x; V6[6 + 4] = vv.y; V6[6 + 5] = vv.z;
-    A6[6 + 0] = aw.x; A6[6 + 1] = aw.y; A6[6 + 2] = aw.z; A6[6 + 3] = av.x; A6[6 + 4] = av.y; A6[6 + 5] = av.z;
+    V6[kVA + 0] = vw.x; V6[kVA + 1] = vw.y; V6[kVA + 2] = vw.z; V6[kVA + 3] = vv.x; V6[kVA + 4] = vv.y; V6[kVA + 5] = vv.z;
+    A6[kVA + 0] = aw.x; A6[kVA + 1] = aw.y; A6[kVA + 2] = aw.z; A6[kVA + 3] = av.x; A6[kVA + 4] = av.y; A6[kVA + 5] = av.z;
   }
   wave_sync();   // pelvis velocity / acceleration and every motion axis and hinge qvel in LDS
   {
@@ -813,8 +818,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const float* const pS3 = Sl + k1;
     const float* const pS4 = Sl + k2;
     const float* const pq = &s.qvel[c_off + 4];
-    float* const pV = V6 + 6 * c_off + crow;
-    float* const pA = A6 + 6 * c_off + crow;
+    float* const pV = V6 + kVA * c_off + crow;
+    float* const pA = A6 + kVA * c_off + crow;
     float nS[5], nq;
     auto ld = [&](int r) {
       nS[0] = pS0[kRow * r]; nS[1] = pS1[kRow * r]; nS[2] = pS2[kRow * r]; nS[3] = pS3[kRow * r]; nS[4] = pS4[kRow * r];
@@ -838,9 +843,9 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       chain_rot3(pc, X1, X2, Y1, Y2);
       float P = pc, PA = pac;
       if (r == 2 && r == c_lo) {
-        const float* pv6 = V6 + 6;
+        const float* pv6 = V6 + kVA;
         X1 = pv6[k1]; X2 = pv6[k2]; Y1 = pv6[3 + k1]; Y2 = pv6[3 + k2];
-        P = pv6[rowc]; PA = A6[6 + rowc];
+        P = pv6[rowc]; PA = A6[kVA + rowc];
       }
       const float vn = fmaf_(Sr, qd, P);
       const float t1 = fmaf_(-X2, Sw1, X1 * Sw2);   // (w_p x s_w)_k, or (w_p x s_v)_k
@@ -851,13 +856,17 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       // from LDS, its results are stored only while active), so no select keeps them
       pc = vn;
       pac = an;
-      if (act && crow < 6) { pV[6 * r] = pc; pA[6 * r] = pac; }
+      // Stores: lanes 6 and 7 into the padding. Up to depth 7 every lane stores: the only inactive
+      // chain there, the right arm before its first body (depths 2..4), writes rows 21..23, which
+      // chain 2 stores again at depths 9..11. Beyond depth 7 the legs are past their last body and
+      // would overwrite rows that chains 1 and 2 stored at depths 2..5, so `act` guards.
+      if (r <= 7 || act) { pV[kVA * r] = pc; pA[kVA * r] = pac; }
     }
   }
   wave_sync();
   if (L.hinge) {
-    const float* v6 = V6 + 6 * L.b;
-    const float* a6 = A6 + 6 * L.b;
+    const float* v6 = V6 + kVA * L.b;
+    const float* a6 = A6 + kVA * L.b;
     vw = {v6[0], v6[1], v6[2]}; vv = {v6[3], v6[4], v6[5]};
     aw = {a6[0], a6[1], a6[2]}; av = {a6[3], a6[4], a6[5]};
   }
@@ -952,8 +961,11 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         F = grp == 2 ? F + g24 : F;
       }
       F = cd == c_hi ? F : F + Fc;
-      // lanes 6 and 7 of a chain repeat row 5 (rowc) and store the same value to the same slot
-      if (act) pF[6 * cd] = F;
+      // lanes 6 and 7 of a chain repeat row 5 (rowc) and store the same value to the same slot.
+      // From depth 5 up every lane stores: the legs past their last body (depths 8..11) write
+      // rows 8..11 and 14..17, which chains 1 and 2 store again at depths 2..5 (every own force was
+      // read before the sweep); below, the right arm past its root would overwrite rows 21..23.
+      if (cd > kTorsoDepth || act) pF[6 * cd] = F;
       Fc = F;
     }
     // pelvis, component r on lane r of chain 0 (chain 2's and chain 1's roots reach chain 0's
@@ -1051,8 +1063,11 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       cs[j] = c;
     }
     // one store per level for the whole row: lanes 0..5 their column entry, lanes 6 and 7 (which
-    // compute invD and u as the others do) the reciprocal pivot and the bias
-    if (act) pUc[kRow * cd] = crow < 6 ? ur : (crow == kInvD ? invD : u);
+    // compute invD and u as the others do) the reciprocal pivot and the bias. From depth 5 up every
+    // lane stores (the legs' rows beyond their leaf are stored again by chains 1 and 2 at depths
+    // 2..5, and nothing reads U during the sweep); below, the right arm past its root would
+    // overwrite rows 21..23.
+    if (cd > kTorsoDepth || act) pUc[kRow * cd] = crow < 6 ? ur : (crow == kInvD ? invD : u);
   };
   // Issue priority (s_setprio): two waves share a SIMD, and the phases that are dependency chains
   // over the tree or the PGS rows (this factor: 1; the contact pipeline from PASS 1 through PGS: 3)
