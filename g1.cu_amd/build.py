@@ -31,22 +31,22 @@ FLAGS = [
 ]
 
 
-# translation units and their own flags: both are scheduled for instruction-level parallelism.
-# k_physics and k_policy with LLVM's max-ilp machine scheduler, since the physics lost its force
+# translation units and their own flags: both are scheduled for instruction-level parallelism with
+# LLVM's max-ilp machine scheduler. k_physics and k_policy since the physics lost its force
 # broadcast and select cascades (config 4 rollout 185.4 -> 183.5 ms; with the older physics the
-# same flag had made it 3% slower). The one-launch rollout kernel had max-ilp from its first version
-# (config 3 12.83 -> 12.77 ms) and now the iterative ILP scheduler, which keeps the better of
-# several schedules per region: config 3 9.358 -> 9.320 ms, config 4 167.6 -> 166.9 ms same-box; on
-# k_physics it measured 0.3% slower in the standing regime and the default scheduler 1.4% slower.
+# same flag had made it 3% slower); the iterative ILP scheduler measured 2.5% slower and the default
+# 2.1% slower in the standing regime. The one-launch rollout kernel had max-ilp from its first version
+# (config 3 12.83 -> 12.77 ms), then for a while the iterative ILP scheduler (9.358 -> 9.320 ms),
+# and with the physics' current LDS layouts max-ilp again: config 3 8.36 -> 8.25 ms, config 4 151.7
+# -> 151.0 ms same-box (the default scheduler and max-memory-clause: 8.36).
 ILP_FIRST = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
-ILP_ITERATIVE = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
 # k_rollout's policy tiles keep their MFMA accumulators in VGPRs: the physics items need ~230
 # VGPRs, which the policy path does not use at the same time, while accumulators in AGPRs add to
 # that count (the wide tile's 8 groups of accumulators took 48 AGPRs: 278 registers, one wave per SIMD)
 MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 SOURCES = (
     ("g1env.hip", ILP_FIRST),
-    ("rollout_kernel.hip", ILP_ITERATIVE + MFMA_VGPR),
+    ("rollout_kernel.hip", ILP_FIRST + MFMA_VGPR),
 )
 
 
