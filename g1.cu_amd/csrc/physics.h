@@ -606,6 +606,23 @@ __device__ __forceinline__ void wave_sync() { __builtin_amdgcn_fence(__ATOMIC_AC
 __device__ __forceinline__ void wave_sync() { __syncthreads(); }
 #endif
 
+// The chain layout's stores without a lane test (the factor, the force gather, the RNE staging): a
+// chain outside its depth range writes the row of body c_off + depth, which its owner must store
+// again later in the same sweep: in the leaf -> root sweeps above the torso depth (the legs past
+// their leaf) at a smaller depth, in the root -> leaf RNE staging up to depth 7 (the right arm before
+// its first body) at a larger one. Chain g: c_off, first and last depth as in world_qacc.
+constexpr bool chain_stray_rows_rewritten() {
+  const int off[4] = {0, 6, 12, 19}, lo[4] = {2, 2, 2, 5}, hi[4] = {7, 7, kMaxDepth, kMaxDepth};
+  for (int g = 0; g < 4; ++g) {
+    for (int cd = hi[g] + 1; cd <= kMaxDepth; ++cd)
+      if (cd > body_depth[16] && !(body_depth[off[g] + cd] < cd)) return false;
+    for (int r = 2; r < lo[g] && r <= 7; ++r)
+      if (!(body_depth[off[g] + r] > r)) return false;
+  }
+  return true;
+}
+static_assert(chain_stray_rows_rewritten(), "rows stored outside a chain's range are stored again by their owners");
+
 constexpr bool hinge_armature_uniform() {
   for (int d = 7; d < kNV; ++d)
     if (MF::dof_armature[d] != MF::dof_armature[6]) return false;
@@ -784,9 +801,9 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   const int c_off = grp == 0 ? 0 : (grp == 1 ? 6 : (grp == 2 ? 12 : 19));
   const int c_lo = grp == 3 ? 5 : 2, c_hi = grp >= 2 ? kMaxDepth : 7;
   // Body of chain g at depth cd. Outside the chain's depth range this is another in-range body
-  // (cd + c_off lies in 1..30 for every cd in 1..11) whose data is read but never stored: keeping
-  // the index linear in cd lets every per-level LDS address be a loop-invariant register plus an
-  // immediate offset.
+  // (cd + c_off lies in 1..30 for every cd in 1..11) whose data is read, and stored only where its
+  // owner stores it again later in the sweep (chain_stray_rows_rewritten): keeping the index linear
+  // in cd lets every per-level LDS address be a loop-invariant register plus an immediate offset.
   auto chain_body = [&](int cd) { return cd + c_off; };
   constexpr int kTorsoDepth = body_depth[16];   // the arms' parent, the waist chain's last body
   static_assert(kMaxDepth + 19 < kNBody, "chain bodies in range");
