@@ -438,8 +438,9 @@ __device__ __forceinline__ LaneModel lane_model(int l) {
 }
 
 // ---------------------------------------------------------------- per-lane world state
-// Lane 1 carries the free joint (qpos[0:7], qvel[0:6]); hinge lane b carries qpos[b+5], qvel[b+4]
-// and actuator b-2 (PD target, previous and current action).
+// Every lane carries the free joint (qpos[0:7], qvel[0:6]; lane 1 is its lane in the tree and the
+// one that stores it); hinge lane b carries qpos[b+5], qvel[b+4] and actuator b-2 (PD target,
+// previous and current action).
 struct LaneState {
   float bq[7], bqd[6];
   float jq, jqd;
@@ -631,7 +632,7 @@ constexpr bool hinge_armature_uniform() {
 
 // ================================================================ substep: qacc of one world
 // Inputs: lane state, PD torque of the lane's hinge dof (jtau). Output: qacc of the lane's dofs
-// (lane 1: 6 base dofs into bqacc[], hinge lanes: jqacc). Returns this world's contact count.
+// (every lane: the 6 base dofs into bqacc[]; hinge lanes: jqacc). Returns this world's contact count.
 // Must be called by all 64 lanes of the block in uniform control flow.
 __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState& st, float jtau,
                                           const SolveParams& P, float (&bqacc)[6], float& jqacc) {
@@ -688,8 +689,17 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
     for (int r = 0; r < kFkRounds; ++r) {
       const int an = (anc >> (8 * r)) & 0xff;
-      const Q4d qa{gshfld(dq.w, an), gshfld(dq.x, an), gshfld(dq.y, an), gshfld(dq.z, an)};
-      const V3d pa{gshfld(dp.x, an), gshfld(dp.y, an), gshfld(dp.z, an)};
+      Q4d qa;
+      V3d pa;
+      if (r == 0) {
+        // the parents' transforms are still the fp32 ones, exactly widened: move the floats (7 lane
+        // exchanges instead of 14) and widen after the move
+        qa = {gshfl(xq.w, an), gshfl(xq.x, an), gshfl(xq.y, an), gshfl(xq.z, an)};
+        pa = {gshfl(xp.x, an), gshfl(xp.y, an), gshfl(xp.z, an)};
+      } else {
+        qa = {gshfld(dq.w, an), gshfld(dq.x, an), gshfld(dq.y, an), gshfld(dq.z, an)};
+        pa = {gshfld(dp.x, an), gshfld(dp.y, an), gshfld(dp.z, an)};
+      }
       if (an > 0) {
         dp = vaddd(pa, qrotd(qa, dp));
         dq = qmuld(qa, dq);
@@ -700,7 +710,9 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     xq = {(float)dq.w, (float)dq.x, (float)dq.y, (float)dq.z};
     xip = {(float)dip.x, (float)dip.y, (float)dip.z};
   }
-  const V3 p{gshfl(xp.x, 1), gshfl(xp.y, 1), gshfl(xp.z, 1)};   // pelvis origin
+  // pelvis origin: every lane carries the free joint's state (integrate_lane), and the pelvis' frame
+  // is its position as it stands (no ancestor to compose with)
+  const V3 p{st.bq[0], st.bq[1], st.bq[2]};
 
   // ---------------- contact detection: lane s = foot sphere s (reference: src/contact.cuh:31-46)
   int ncon = 0;
@@ -1559,10 +1571,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   wave_sync();
 
   if (ncon_max == 0) {
-    if (base) {
 #pragma unroll
-      for (int k = 0; k < 6; ++k) bqacc[k] = s.Mm[0][k];
-    }
+    for (int k = 0; k < 6; ++k) bqacc[k] = s.Mm[0][k];   // every lane: each integrates the free joint
     jqacc = L.hinge ? s.Mm[0][L.b + 4] : 0.f;
     __builtin_amdgcn_s_setprio(0);
     wave_sync();
@@ -1808,10 +1818,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     if (kGroup + l < kNV) s.qacc[d2] = s.Mm[0][d2] + dq2;
   }
   wave_sync();
-  if (base) {
 #pragma unroll
-    for (int k = 0; k < 6; ++k) bqacc[k] = s.qacc[k];
-  }
+  for (int k = 0; k < 6; ++k) bqacc[k] = s.qacc[k];   // every lane: each integrates the free joint
   jqacc = L.hinge ? s.qacc[L.b + 4] : 0.f;
   wave_sync();
   return ncon;
@@ -1835,7 +1843,9 @@ __device__ __forceinline__ void integrate_lane(const LaneModel& L, LaneState& st
     st.jqd = upd(st.jqd, jqacc);
     st.jq = fmaf_(dt, st.jqd, st.jq);
   }
-  if (L.l == 1) {
+  {
+    // the free joint on every lane (the same operations on the same values, so every lane holds the
+    // pelvis state; lane 1 is the one that stores it)
 #pragma unroll
     for (int k = 0; k < 6; ++k) st.bqd[k] = upd(st.bqd[k], bqacc[k]);
     st.bq[0] = fmaf_(dt, st.bqd[0], st.bq[0]); st.bq[1] = fmaf_(dt, st.bqd[1], st.bq[1]);
