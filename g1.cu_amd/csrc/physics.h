@@ -679,9 +679,11 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       xq = qmul(L.bquat, aa);
     }
   }
+  // the pelvis' orientation, on every lane (every lane carries the free joint's state)
+  const Q4 qpel = qnorm(Q4{st.bq[3], st.bq[4], st.bq[5], st.bq[6]});
   if (base) {
     xp = {st.bq[0], st.bq[1], st.bq[2]};
-    xq = qnorm(Q4{st.bq[3], st.bq[4], st.bq[5], st.bq[6]});
+    xq = qpel;
   }
   {
     V3d dp{xp.x, xp.y, xp.z};
@@ -741,7 +743,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 
   // ---------------- motion axes (reference: src/aba_bias.cuh:25-43)
   V3 sw{0.f, 0.f, 0.f}, sv{0.f, 0.f, 0.f};   // hinge axis (angular; linear)
-  M3 R1{};
+  // the pelvis rotation on every lane (the free joint's right-hand side and base solve use it)
+  const M3 R1 = quat2mat(qpel);
   if (L.hinge) {
     sw = qrot(xq, L.axis);
     sv = cross(vsub(xp, p), sw);
@@ -752,7 +755,6 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     s.qvel[d] = st.jqd;
   }
   if (base) {
-    R1 = quat2mat(xq);
     // only the rotations' angular parts (R1 columns) are stored: every use of the free joint's
     // subspace takes its structure from sbase_dot / sbase_col
 #pragma unroll
@@ -1125,8 +1127,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   float pAs[6];
   float xb[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   {
-    // the free joint's right-hand side -S_base.F_1 on lane 1 (F_1 from the force gather)
-    if (base) {
+    // the free joint's right-hand side -S_base.F_1 on every lane (F_1 from the force gather)
+    {
       const V3 Fw{Fo[6], Fo[7], Fo[8]}, Fv{Fo[9], Fo[10], Fo[11]};
       // x_base = 0 - S_base.F_1 (see sbase_dot): translation k takes Fv_k, rotation k R1 col k . Fw
       xb[0] = -Fv.x; xb[1] = -Fv.y; xb[2] = -Fv.z;
@@ -1348,7 +1350,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   float xb0[6];   // the smooth right-hand side on the base dofs (lane 1 holds it)
   if (ncon_max > 0) {
 #pragma unroll
-    for (int k = 0; k < 6; ++k) xb0[k] = gshfl(xb[k], 1);
+    for (int k = 0; k < 6; ++k) xb0[k] = xb[k];
   }
   if (ncon_max > 0 && ncon_max <= kChainSolveCon) {
     // Chain layout (waves with at most two contacts per world, at most seven columns): lane
