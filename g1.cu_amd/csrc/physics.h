@@ -863,28 +863,24 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       const bool act = r >= c_lo && r <= c_hi;
       const float Sr = nS[0], Sw1 = nS[1], Sw2 = nS[2], Sv1 = nS[3], Sv2 = nS[4], qd = nq;
       if (r < kMaxDepth) ld(r + 1);
-      // parent's components: the chain's previous level; the right arm's first body takes the
-      // torso from chain 2's lanes (row_shr:8), the other chains' first bodies the pelvis from LDS
-      if (r == kTorsoDepth + 1) {
-        const float tp = from_prev_chain(pc), ta = from_prev_chain(pac);
-        pc = grp == 3 ? tp : pc;
-        pac = grp == 3 ? ta : pac;
-      }
-      float X1, X2, Y1, Y2;   // w_p[k+1], w_p[k+2], v_p[k+1], v_p[k+2]
-      chain_rot3(pc, X1, X2, Y1, Y2);
+      // The parent's row, as this chain stored it at the previous level (the LDS staging doubles as
+      // the exchange: four reads at per-lane columns instead of nine DPP moves): at depth 2 the
+      // pelvis, for the right arm's first body the torso (chain 2's depth-4 row). Its own component
+      // rowc is the lane's register from the previous level, read from the row where the parent is
+      // another chain's body.
+      const float* const prow = r == 2 ? V6 + kVA
+                                       : (r == kTorsoDepth + 1 && grp == 3 ? V6 + kVA * 16 : V6 + kVA * (c_off + r - 1));
+      const float X1 = prow[k1], X2 = prow[k2];           // w_p[k+1], w_p[k+2]
+      const float Y1 = prow[3 + k1], Y2 = prow[3 + k2];   // v_p[k+1], v_p[k+2]
       float P = pc, PA = pac;
-      if (r == 2 && r == c_lo) {
-        const float* pv6 = V6 + kVA;
-        X1 = pv6[k1]; X2 = pv6[k2]; Y1 = pv6[3 + k1]; Y2 = pv6[3 + k2];
-        P = pv6[rowc]; PA = A6[kVA + rowc];
-      }
+      if (r == 2 || r == kTorsoDepth + 1) { P = prow[rowc]; PA = prow[kVA / 2 + rowc]; }
       const float vn = fmaf_(Sr, qd, P);
       const float t1 = fmaf_(-X2, Sw1, X1 * Sw2);   // (w_p x s_w)_k, or (w_p x s_v)_k
       const float t2 = fmaf_(-Y2, Sv1, Y1 * Sv2);   // (v_p x s_w)_k
       const float sd = isv ? t1 + t2 : t1;
       const float an = fmaf_(sd, qd, PA);
       // a chain's values outside its depth range are never read (its first body takes the parent
-      // from LDS, its results are stored only while active), so no select keeps them
+      // from the pelvis' or the torso's row), so no select keeps them
       pc = vn;
       pac = an;
       // Stores: lanes 6 and 7 into the padding. Up to depth 7 every lane stores: the only inactive
