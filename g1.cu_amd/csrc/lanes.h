@@ -93,12 +93,6 @@ template <int A, int B, int C, int D>
 __device__ __forceinline__ float quad_perm(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), A | (B << 2) | (C << 4) | (D << 6), 0xF, 0xF, true));
 }
-__device__ __forceinline__ float row_shl3(float v) {   // lane i <- lane i + 3 of its row
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x103, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float shr3_upper_quads(float x) {   // lanes 4..7 of each 8 <- lanes 1..4
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x113, 0xF, 0xA, false));
-}
 
 // Chain-to-chain moves at the factor's junctions (chains g on lanes 8g..8g+7 of the group): lane i
 // of a 16-lane row takes lane i + 8 (row_shl:8; the upper half of the row reads 0) or lane i - 8
@@ -116,19 +110,6 @@ __device__ __forceinline__ float from_upper_row(float v) {
 }
 __device__ __forceinline__ float from_lower_row(float v) {
   return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[0]);
-}
-
-// A chain holds a spatial vector as (w0 w1 w2 v0 v1 v2) in lanes 0..5 of its aligned 8 lanes;
-// lane r < 6, k = r mod 3, gets w[(k+1) mod 3], w[(k+2) mod 3], v[(k+1) mod 3], v[(k+2) mod 3],
-// the operands of component k of a cross product (lanes 6, 7: unspecified). Lanes 0..3 permute
-// their quad, lanes 4, 5 take lanes 1, 2 of the permuted lower quad; the v parts are first moved
-// down by three lanes. DPP only: no LDS round trip.
-__device__ __forceinline__ void chain_rot3(float pc, float& X1, float& X2, float& Y1, float& Y2) {
-  X1 = shr3_upper_quads(quad_perm<1, 2, 0, 1>(pc));
-  X2 = shr3_upper_quads(quad_perm<2, 0, 1, 2>(pc));
-  const float v = row_shl3(pc);
-  Y1 = shr3_upper_quads(quad_perm<1, 2, 0, 1>(v));
-  Y2 = shr3_upper_quads(quad_perm<2, 0, 1, 2>(v));
 }
 
 // Value of lane I of this lane's group, of its 16-lane row or of its quad, in every lane of that
