@@ -71,7 +71,8 @@ __device__ __forceinline__ V3 qrot(Q4 q, V3 v) {
   const V3 ut = cross(u, t);
   return {fmaf_(q.w, t.x, v.x) + ut.x, fmaf_(q.w, t.y, v.y) + ut.y, fmaf_(q.w, t.z, v.z) + ut.z};
 }
-// fp64 forms of the above for the forward-kinematics compositions (same operation order)
+// fp64 forms of the above for the forward-kinematics compositions (same operation order; qrotd the
+// same values)
 struct V3d { double x, y, z; };
 struct Q4d { double w, x, y, z; };
 __device__ __forceinline__ double fmad_(double a, double b, double c) { return __builtin_fma(a, b, c); }
@@ -85,12 +86,16 @@ __device__ __forceinline__ Q4d qmuld(Q4d a, Q4d b) {
           fmad_(a.z, b.x, fmad_(a.y, b.w, fmad_(-a.x, b.z, a.w * b.y))),
           fmad_(a.z, b.w, fmad_(-a.y, b.x, fmad_(a.x, b.y, a.w * b.z)))};
 }
+// The same values as qrot's sequence in fp64, in two fewer operations: with c = u x v, t = 2c and
+// u x t = 2 (u x c) are exact doublings (the operands are fp32 values and products of them, far from
+// fp64's underflow), so fma(w, t, v) + u x t = fma(2, u x c, fma(2w, c, v)) bit for bit.
 __device__ __forceinline__ V3d qrotd(Q4d q, V3d v) {
   const V3d u{q.x, q.y, q.z};
   const V3d c = crossd(u, v);
-  const V3d t{2.0 * c.x, 2.0 * c.y, 2.0 * c.z};
-  const V3d ut = crossd(u, t);
-  return {fmad_(q.w, t.x, v.x) + ut.x, fmad_(q.w, t.y, v.y) + ut.y, fmad_(q.w, t.z, v.z) + ut.z};
+  const V3d X = crossd(u, c);
+  const double w2 = q.w + q.w;
+  return {fmad_(2.0, X.x, fmad_(w2, c.x, v.x)), fmad_(2.0, X.y, fmad_(w2, c.y, v.y)),
+          fmad_(2.0, X.z, fmad_(w2, c.z, v.z))};
 }
 __device__ __forceinline__ double gshfld(double v, int src) { return __shfl(v, src, kGroup); }
 
@@ -108,11 +113,14 @@ __device__ __forceinline__ void sincos_rn(float x, float& sn, float& cs) {
   cs = (float)cd;
 }
 
-// A double constant materialised in scalar registers where it is used: the polynomial
-// coefficients below would otherwise be hoisted out of the substep loop into ~20 vector registers.
-__device__ __forceinline__ double kc(double c) {
-  __asm__ volatile("" : "+s"(c));
-  return c;
+// One Horner step fma(z, p, c) as the three-address v_fma_f64. The coefficients below stay in
+// vector registers across the substep loop, and for fma(z, p, c) the compiler otherwise copies c
+// into the accumulator (v_mov_b64) for the two-address v_fmac_f64: one VALU instruction per step
+// fewer, the same operation.
+__device__ __forceinline__ double horner_d(double z, double p, double c) {
+  double r;
+  __asm__("v_fma_f64 %0, %1, %2, %3" : "=v"(r) : "v"(z), "v"(p), "v"(c));
+  return r;
 }
 // sin_rn and cos_rn of one argument for the hinge half-angles on a short fp64 path for |x| <= 4:
 // k = rint(x 2/pi), r = (x - k P1) - k P2 with P1 + P2 = pi/2 (P1 = RN(pi/2), so x - k P1 is exact
@@ -131,18 +139,18 @@ __device__ __forceinline__ void sincos_hinge_rn(float x, float& sn, float& cs) {
     const double r = __builtin_fma(-kd, 6.123233995736766e-17, __builtin_fma(-kd, 1.5707963267948966, xd));
     const double z = r * r;
     double ps = -1.0 / 1307674368000.0;
-    ps = __builtin_fma(z, ps, 1.0 / 6227020800.0);
-    ps = __builtin_fma(z, ps, -1.0 / 39916800.0);
-    ps = __builtin_fma(z, ps, 1.0 / 362880.0);
-    ps = __builtin_fma(z, ps, -1.0 / 5040.0);
-    ps = __builtin_fma(z, ps, 1.0 / 120.0);
-    ps = __builtin_fma(z, ps, -1.0 / 6.0);
+    ps = horner_d(z, ps, 1.0 / 6227020800.0);
+    ps = horner_d(z, ps, -1.0 / 39916800.0);
+    ps = horner_d(z, ps, 1.0 / 362880.0);
+    ps = horner_d(z, ps, -1.0 / 5040.0);
+    ps = horner_d(z, ps, 1.0 / 120.0);
+    ps = horner_d(z, ps, -1.0 / 6.0);
     double pc = -1.0 / 87178291200.0;
-    pc = __builtin_fma(z, pc, 1.0 / 479001600.0);
-    pc = __builtin_fma(z, pc, -1.0 / 3628800.0);
-    pc = __builtin_fma(z, pc, 1.0 / 40320.0);
-    pc = __builtin_fma(z, pc, -1.0 / 720.0);
-    pc = __builtin_fma(z, pc, 1.0 / 24.0);
+    pc = horner_d(z, pc, 1.0 / 479001600.0);
+    pc = horner_d(z, pc, -1.0 / 3628800.0);
+    pc = horner_d(z, pc, 1.0 / 40320.0);
+    pc = horner_d(z, pc, -1.0 / 720.0);
+    pc = horner_d(z, pc, 1.0 / 24.0);
     pc = __builtin_fma(z, pc, -0.5);
     const double sr = __builtin_fma(r * z, ps, r), cr = __builtin_fma(z, pc, 1.0);
     // (sin x, cos x) = (sin r, cos r), (cos r, -sin r), (-sin r, -cos r), (-cos r, sin r) for k mod 4
@@ -165,15 +173,15 @@ __device__ __forceinline__ void sincos_small_rn(float x, float& sn, float& cs) {
   if (fabsf(x) <= 0.125f) {
     const double xd = x, z = xd * xd;
     double ps = -1.0 / 39916800.0;
-    ps = __builtin_fma(z, ps, 1.0 / 362880.0);
-    ps = __builtin_fma(z, ps, -1.0 / 5040.0);
-    ps = __builtin_fma(z, ps, 1.0 / 120.0);
-    ps = __builtin_fma(z, ps, -1.0 / 6.0);
+    ps = horner_d(z, ps, 1.0 / 362880.0);
+    ps = horner_d(z, ps, -1.0 / 5040.0);
+    ps = horner_d(z, ps, 1.0 / 120.0);
+    ps = horner_d(z, ps, -1.0 / 6.0);
     double pc = 1.0 / 479001600.0;
-    pc = __builtin_fma(z, pc, -1.0 / 3628800.0);
-    pc = __builtin_fma(z, pc, 1.0 / 40320.0);
-    pc = __builtin_fma(z, pc, -1.0 / 720.0);
-    pc = __builtin_fma(z, pc, 1.0 / 24.0);
+    pc = horner_d(z, pc, -1.0 / 3628800.0);
+    pc = horner_d(z, pc, 1.0 / 40320.0);
+    pc = horner_d(z, pc, -1.0 / 720.0);
+    pc = horner_d(z, pc, 1.0 / 24.0);
     pc = __builtin_fma(z, pc, -0.5);
     const float s_ = (float)__builtin_fma(xd * z, ps, xd);
     sn = (x == 0.f) ? x : s_;   // sin(-0) = -0
@@ -702,10 +710,13 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         qa = {gshfld(dq.w, an), gshfld(dq.x, an), gshfld(dq.y, an), gshfld(dq.z, an)};
         pa = {gshfld(dp.x, an), gshfld(dp.y, an), gshfld(dp.z, an)};
       }
-      if (an > 0) {
-        dp = vaddd(pa, qrotd(qa, dp));
-        dq = qmuld(qa, dq);
-      }
+      // Every lane composes, also where the 2^r-th ancestor would lie beyond the world: there `an`
+      // is 0, the world body's lane, whose transform is the identity (zero translation, quaternion
+      // (1, 0, 0, 0)) and stays exactly that under its own compositions. Composing with it returns
+      // the transform unchanged except for the sign of an exact zero, and the CPU restatement
+      // composes the same way: no branch and no selects around the composition.
+      dp = vaddd(pa, qrotd(qa, dp));
+      dq = qmuld(qa, dq);
     }
     const V3d dip = vaddd(dp, qrotd(dq, V3d{L.ipos.x, L.ipos.y, L.ipos.z}));
     xp = {(float)dp.x, (float)dp.y, (float)dp.z};

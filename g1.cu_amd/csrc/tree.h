@@ -13,7 +13,8 @@ constexpr int kFkRounds = 4;
 constexpr int kTreeLanes = 32;   // one entry per lane of a 32-lane world group (lanes >= kNBody: none)
 
 // a[r][b]: the 2^r-th ancestor of body b, or 0 when that would be the world body or lie beyond it
-// (then b's transform is already relative to the world and round r leaves it unchanged).
+// (then b's transform is already relative to the world, and round r composes it with the world
+// body's identity, which leaves it unchanged up to the sign of an exact zero).
 struct AncestorTable {
   int a[kFkRounds][kTreeLanes];
 };

@@ -106,6 +106,7 @@ static void init_tables() {
 
 namespace orc {
 template <> struct ComposePrec<flc::F> { using type = flc::F; };   // count the fp64 compositions too
+template <> struct FkComposeIdentity<flc::F> { static constexpr bool value = false; };   // padding, not work
 }
 
 static void out_counts(double* out7) {

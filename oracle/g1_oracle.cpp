@@ -82,6 +82,10 @@ template <class R> static inline R exp_(R x) { return std::exp(x); }
 // Precision of the forward-kinematics compositions (fk below); a customisation point for the
 // operation-counting instantiation (flop_count.cpp), which counts them as its own scalar type.
 template <class R> struct ComposePrec { using type = double; };
+// Whether fk composes the transforms already in the world frame with the world body's identity (the
+// GPU's branch-free form; the same values up to the sign of an exact zero). The counting
+// instantiation leaves them out: they move no transform and are not part of the algorithm's work.
+template <class R> struct FkComposeIdentity { static constexpr bool value = true; };
 // (reference: src/dynamics.cuh:36-39)
 template <class R> static inline Q4<R> qnorm(Q4<R> q) {
   R n = rsqrt_(fma_(q.z, q.z, fma_(q.y, q.y, fma_(q.x, q.x, q.w * q.w))));
@@ -192,12 +196,14 @@ template <class R> void fk(const R* qpos, R* xpos, R* xquat, R* xipos) {
     Q4<C> oq[kNBody];
     std::copy(tp, tp + kNBody, op);
     std::copy(tq, tq + kNBody, oq);
+    // every body composes, with the world body's identity (a = 0) where the 2^r-th ancestor would
+    // lie beyond the world: the GPU's branch-free form, equal to leaving the transform unchanged
+    // except for the sign of an exact zero
     for (int b = 1; b < kNBody; ++b) {
       const int a = kAncestors.a[r][b];
-      if (a > 0) {
-        tp[b] = vadd(op[a], qrot(oq[a], op[b]));
-        tq[b] = qmul(oq[a], oq[b]);
-      }
+      if (a == 0 && !FkComposeIdentity<R>::value) continue;
+      tp[b] = vadd(op[a], qrot(oq[a], op[b]));
+      tq[b] = qmul(oq[a], oq[b]);
     }
   }
   for (int b = 0; b < kNBody; ++b) {
