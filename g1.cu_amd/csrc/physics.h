@@ -1813,18 +1813,33 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     static_assert(kNV <= 2 * kGroup, "two dofs per lane");
     const int d1 = l, d2 = kGroup + l < kNV ? kGroup + l : l;
     float dq1 = 0.f, dq2 = 0.f;
+    const float s1 = s.Mm[0][d1], s2 = s.Mm[0][d2];
+    // Contact c's four forces and its three solve columns at the lane's dofs, read one contact
+    // ahead (every index stays inside f and Mm), so that the next contact's reads overlap this one's
+    // arithmetic instead of each contact waiting on its own reads; a contact the lane's world does
+    // not have (c >= ncon) is computed and not added.
+    float F[4], M1[3], M2[3];
+    auto ld = [&](int c) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) F[k] = s.f[4 * c + k];
+#pragma unroll
+      for (int a = 0; a < 3; ++a) { M1[a] = s.Mm[1 + a + 3 * c][d1]; M2[a] = s.Mm[1 + a + 3 * c][d2]; }
+    };
+    ld(0);
 #pragma unroll
     for (int c = 0; c < kNFoot; ++c) {
       if (c >= ncon_max) break;
-      if (c < ncon) {
-        const float f0 = s.f[4 * c], f1 = s.f[4 * c + 1], f2 = s.f[4 * c + 2], f3 = s.f[4 * c + 3];
-        const float fb0 = f0 + f1 + f2 + f3, fb1 = f0 - f1, fb2 = f2 - f3;
-        dq1 += fmaf_(fb2, s.Mm[3 + 3 * c][d1], fmaf_(fb1, s.Mm[2 + 3 * c][d1], fb0 * s.Mm[1 + 3 * c][d1]));
-        dq2 += fmaf_(fb2, s.Mm[3 + 3 * c][d2], fmaf_(fb1, s.Mm[2 + 3 * c][d2], fb0 * s.Mm[1 + 3 * c][d2]));
-      }
+      const float f0 = F[0], f1 = F[1], f2 = F[2], f3 = F[3];
+      const float m10 = M1[0], m11 = M1[1], m12 = M1[2], m20 = M2[0], m21 = M2[1], m22 = M2[2];
+      if (c + 1 < kNFoot) ld(c + 1);
+      const float fb0 = f0 + f1 + f2 + f3, fb1 = f0 - f1, fb2 = f2 - f3;
+      const float t1 = fmaf_(fb2, m12, fmaf_(fb1, m11, fb0 * m10));
+      const float t2 = fmaf_(fb2, m22, fmaf_(fb1, m21, fb0 * m20));
+      dq1 = c < ncon ? dq1 + t1 : dq1;
+      dq2 = c < ncon ? dq2 + t2 : dq2;
     }
-    s.qacc[d1] = s.Mm[0][d1] + dq1;
-    if (kGroup + l < kNV) s.qacc[d2] = s.Mm[0][d2] + dq2;
+    s.qacc[d1] = s1 + dq1;
+    if (kGroup + l < kNV) s.qacc[d2] = s2 + dq2;
   }
   wave_sync();
 #pragma unroll
