@@ -1130,7 +1130,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
   for (int cd = kTorsoDepth - 1; cd >= 2; --cd) level(cd, false, none, none);
   // pelvis: I^A_1 = I6_1 + D_14 + D_8 + D_2 and pA_1 = cs_14 + cs_8 + cs_2 (descending children),
-  // row r on lane r of chain 0; lane 1 keeps pA_1 for the base solve
+  // row r on lane r of chain 0, which all hold pA_1
   float pAs[6];
   float xb[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   {
@@ -1158,8 +1158,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   }
   __builtin_amdgcn_s_setprio(0);
   // ---------------- free-joint 6x6 block (reference: src/aba_factor.cuh:90-108): lane c < 6
-  // builds column c of U6 = I^A S_base and of D = S_base' U6; lane 1 factors D and solves the
-  // base of the smooth system.
+  // builds column c of U6 = I^A S_base and of D = S_base' U6; every lane then factors D and solves
+  // the base of the smooth system.
   wave_sync();   // I^A of the pelvis and the hinge factor complete in LDS
   if (l < 6) {
     // column l of U6 = I^A S_base: translation l < 3 picks column 3 + l of I^A, rotation l >= 3
@@ -1195,12 +1195,27 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
     for (int k = 0; k < 6; ++k) s.u.fac.Dm[k * 6 + l] = sbase_dot(k, S3[k < 3 ? 0 : k - 3], U6c);
   }
+  // pA_1 from lane 1 (chain 0's lanes hold it) to every lane for the smooth base solve (waves
+  // without contacts), while D is built and read
+  float pA1[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (ncon_max == 0) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) pA1[k] = gshfl(pAs[k], 1);
+  }
   wave_sync();
+  // Every lane factors D and, without contacts, solves the base of the smooth system: the same
+  // operations on the same values (D's lower triangle read whole, the same addresses on every lane;
+  // S_base's rotation rows are R1's columns, on every lane), so that the base acceleration and
+  // qacc are local to every lane for the root -> leaf sweep and the integration: no exec-mask region
+  // and no lane exchange after the serial chain.
   float a6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (base) {
+  float qb[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // the smooth solve's base qacc (no contacts)
+  {
     float Dm[36], Dinv[6];
 #pragma unroll
-    for (int i = 0; i < 36; ++i) Dm[i] = s.u.fac.Dm[i];
+    for (int i = 0; i < 6; ++i)
+#pragma unroll
+      for (int j = 0; j <= i; ++j) Dm[i * 6 + j] = s.u.fac.Dm[i * 6 + j];
 #pragma unroll
     for (int i = 0; i < 6; ++i)
 #pragma unroll
@@ -1215,18 +1230,28 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
           Dm[i * 6 + j] = div_rn(a, Dm[j * 6 + j], Dinv[j]);
         }
       }
-#pragma unroll
-    for (int i = 0; i < 36; ++i) s.u.fac.Dfac[i] = Dm[i];
-#pragma unroll
-    for (int i = 0; i < 6; ++i) s.u.fac.Dinv[i] = Dinv[i];
     // With contacts the smooth solve's base and root -> leaf parts run as column 0 of the contact
-    // solves below (lane 0, the same operations in the same order); without, here and in the
-    // level-synchronous sweep.
-    if (ncon_max == 0) {
+    // solves below (lane 0, the same operations in the same order), which read the factor from LDS
+    // (the lower triangle); without, here and in the level-synchronous sweep.
+    if (ncon_max > 0) {
+      if (base) {
+#pragma unroll
+        for (int i = 0; i < 6; ++i)
+#pragma unroll
+          for (int j = 0; j <= i; ++j) s.u.fac.Dfac[i * 6 + j] = Dm[i * 6 + j];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) s.u.fac.Dinv[i] = Dinv[i];
+      }
+    } else {
       // smooth solve, free joint: L L' qdd = x_base - S_base.pA_1 (reference: src/aba_factor.cuh:139-155)
+      float S3[3][3];   // S3[k][i] = S_base rotation k, component i = R1 column k
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+#pragma unroll
+        for (int i = 0; i < 3; ++i) S3[k][i] = R1.m[3 * i + k];
       float qdd[6];
 #pragma unroll
-      for (int k = 0; k < 6; ++k) qdd[k] = xb[k] - sbase_dot(k, s.u.fac.S[k], pAs);
+      for (int k = 0; k < 6; ++k) qdd[k] = xb[k] - sbase_dot(k, S3[k < 3 ? 0 : k - 3], pA1);
 #pragma unroll
       for (int i = 0; i < 6; ++i) {
         float a = qdd[i];
@@ -1242,12 +1267,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
         qdd[i] = div_rn(a, Dm[i * 6 + i], Dinv[i]);
       }
 #pragma unroll
-      for (int k = 0; k < 6; ++k) s.Mm[0][k] = qdd[k];
-      float S3[3][3];
-#pragma unroll
-      for (int k = 0; k < 3; ++k)
-#pragma unroll
-        for (int i = 0; i < 3; ++i) S3[k][i] = s.u.fac.S[3 + k][i];
+      for (int k = 0; k < 6; ++k) qb[k] = qdd[k];
 #pragma unroll
       for (int i = 0; i < 6; ++i) a6[i] = sbase_col(i, S3, qdd);
     }
@@ -1256,13 +1276,14 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // In the factor's chain layout: the four chains walk root -> leaf in lock-step over depth, every
   // lane of a chain carrying the whole 6-vector acceleration (the per-body operations of the
   // lane-per-body form, redundantly on the chain's lanes), so a level has no cross-lane exchange;
-  // the chains start from the pelvis (lane 1), the right arm from the torso (chain 2, depth 4).
+  // the chains start from the pelvis' acceleration (on every lane), the right arm from the torso
+  // (chain 2, depth 4).
   // A chain's values outside its depth range are never stored, and the right arm's are replaced
   // at its first level. Each level's LDS operands are read one level ahead.
   if (ncon_max == 0) {
     float a[6];
 #pragma unroll
-    for (int k = 0; k < 6; ++k) a[k] = gshfl(a6[k], 1);
+    for (int k = 0; k < 6; ++k) a[k] = a6[k];
     float U[6], S[6], us, iD;
     auto ld = [&](int r) {
       const int b = chain_body(r);
@@ -1581,7 +1602,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 
   if (ncon_max == 0) {
 #pragma unroll
-    for (int k = 0; k < 6; ++k) bqacc[k] = s.Mm[0][k];   // every lane: each integrates the free joint
+    for (int k = 0; k < 6; ++k) bqacc[k] = qb[k];   // every lane: each integrates the free joint
     jqacc = L.hinge ? s.Mm[0][L.b + 4] : 0.f;
     __builtin_amdgcn_s_setprio(0);
     wave_sync();
