@@ -314,7 +314,6 @@ struct WorldLds {
       alignas(16) float U[kNBody][kRow];
       alignas(16) float Dfac[36];       // Cholesky factor of the free-joint 6x6 block
       alignas(16) float Dinv[6];        // RN(1 / diagonal of Dfac)
-      alignas(16) float IA1[21];        // articulated inertia of the pelvis (packed)
       alignas(16) float Dm[36];         // free-joint 6x6 block before factoring
     } fac;
     alignas(16) float G[kPairs][9];     // 3x3 Gram blocks of contact pairs c <= c' (after the solves)
@@ -1131,7 +1130,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   for (int cd = kTorsoDepth - 1; cd >= 2; --cd) level(cd, false, none, none);
   // pelvis: I^A_1 = I6_1 + D_14 + D_8 + D_2 and pA_1 = cs_14 + cs_8 + cs_2 (descending children),
   // row r on lane r of chain 0, which all hold pA_1
-  float pAs[6];
+  float pAs[6], I1[6];
   float xb[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   {
     // the free joint's right-hand side -S_base.F_1 on every lane (F_1 from the force gather)
@@ -1142,7 +1141,6 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
 #pragma unroll
       for (int k = 0; k < 3; ++k) xb[3 + k] = -fmaf_(R1.m[6 + k], Fw.z, fmaf_(R1.m[3 + k], Fw.y, R1.m[k] * Fw.x));
     }
-    float I1[6];
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
       const float d14 = from_upper_row(Dlr[j]), d8 = from_next_chain(Dlr[j]);
@@ -1150,46 +1148,41 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       I1[j] = ((s.I6r[1][rowc][j] + d14) + d8) + Dlr[j];
       pAs[j] = (c14 + c8) + cs[j];
     }
-    if (l < 6) {
-#pragma unroll
-      for (int j = 0; j < 6; ++j)
-        if (j >= l) s.u.fac.IA1[symidx(l, j)] = I1[j];
-    }
   }
   __builtin_amdgcn_s_setprio(0);
   // ---------------- free-joint 6x6 block (reference: src/aba_factor.cuh:90-108): lane c < 6
   // builds column c of U6 = I^A S_base and of D = S_base' U6; every lane then factors D and solves
   // the base of the smooth system.
-  wave_sync();   // I^A of the pelvis and the hinge factor complete in LDS
+  // I^A rows from chain 0's lanes (lane r holds row r; I^A is symmetric bit for bit, the downdate
+  // products commuting, so row r is also column r): lanes c < 3 take row 3 + c, their translation
+  // column; lanes c >= 3 rows 0..2, the angular columns. Lane exchanges instead of a staging
+  // round trip through LDS.
+  float Ir[3][6];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const int src = l < 3 ? (q == 0 ? 3 + l : 0) : q;
+#pragma unroll
+    for (int j = 0; j < 6; ++j) Ir[q][j] = gshfl(I1[j], src);
+  }
   if (l < 6) {
     // column l of U6 = I^A S_base: translation l < 3 picks column 3 + l of I^A, rotation l >= 3
-    // is I^A's angular columns times R1 col (l - 3) (structural zeros skipped, see sbase_dot).
-    // The packed I^A and the rows S[3..5] are read whole (the same addresses on every lane); the
-    // lane's own operands (its translation column, its rotation row) are read at lane-dependent
-    // addresses rather than selected among registers, which the compiler turned into divergent
-    // branches (an exec-mask diamond per select).
-    float IA[21], S3[3][3];
-#pragma unroll
-    for (int i = 0; i < 21; ++i) IA[i] = s.u.fac.IA1[i];
+    // is I^A's angular columns times R1 col (l - 3) (structural zeros skipped, see sbase_dot). The
+    // lane's rotation column is read at a lane-dependent LDS address rather than selected among
+    // registers, which the compiler turned into divergent branches (an exec-mask diamond per select).
+    float S3[3][3];   // S3[k][i] = S_base rotation k, component i = R1 column k
 #pragma unroll
     for (int k = 0; k < 3; ++k)
 #pragma unroll
-      for (int i = 0; i < 3; ++i) S3[k][i] = s.u.fac.S[3 + k][i];
+      for (int i = 0; i < 3; ++i) S3[k][i] = R1.m[3 * i + k];
     const int rl = l < 3 ? 0 : l - 3;   // the lane's rotation (translation lanes: row 0, unused)
-    const int tl = l < 3 ? l : 0;       // the lane's translation (rotation lanes: 0, unused)
     float Sc[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) Sc[i] = s.u.fac.S[3 + rl][i];
     float U6c[6];
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
-      const float rot = fmaf_(IA[symidx(i, 2)], Sc[2], fmaf_(IA[symidx(i, 1)], Sc[1], IA[symidx(i, 0)] * Sc[0]));
-      // I^A[i][3 + tl] in the 21-packed upper triangle (i <= 3 + tl for i < 3; (3 + tl, i) else)
-      const int ti = i <= 3 ? i * 6 - (i * (i - 1)) / 2 + (3 + tl - i) : symidx(i, 3);
-      const int tj = i < 3 ? ti : (i <= 3 + tl ? i * 6 - (i * (i - 1)) / 2 + (3 + tl - i)
-                                               : (3 + tl) * 6 - ((3 + tl) * (2 + tl)) / 2 + (i - 3 - tl));
-      const float tr = s.u.fac.IA1[i < 3 ? ti : tj];
-      U6c[i] = l < 3 ? tr : rot;
+      const float rot = fmaf_(Ir[2][i], Sc[2], fmaf_(Ir[1][i], Sc[1], Ir[0][i] * Sc[0]));
+      U6c[i] = l < 3 ? Ir[0][i] : rot;
     }
     // D = S_base' U6 (+ armature and dt*damping, both 0 on the free joint)
 #pragma unroll
