@@ -835,8 +835,8 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
                 body_depth[24] == 5 && body_depth[2] == 2, "chain roots");
   // body velocity and acceleration about the pelvis origin, interleaved per body (w, v of the
   // velocity, two floats of padding where chain lanes 6 and 7 store, the acceleration likewise, four
-  // more): a lane stores both components of a level with one two-address LDS write, and the body
-  // stride of 20 words puts the four chains' rows of a level on different LDS banks
+  // more): every level's slot sits at an immediate offset from the lane's base, and the body stride
+  // of 20 words puts the four chains' rows of a level on different LDS banks
   constexpr int kVA = 20;
   float* const V6 = &s.Mm[0][0];
   float* const A6 = V6 + kVA / 2;
@@ -850,8 +850,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const int k = rowc < 3 ? rowc : rowc - 3, k1 = k == 2 ? 0 : k + 1, k2 = k == 0 ? 2 : k - 1;
     const bool isv = rowc >= 3;
     const int so = isv ? 3 : 0;
-    // per-lane base pointers: depth r's operands sit at a constant offset from them, and the next
-    // level's are read before this level's stores (which the compiler cannot tell apart from them)
+    // per-lane base pointers: depth r's operands sit at a constant offset from them
     const float* const Sl = &s.u.fac.S[c_off + 4][0];
     const float* const pS0 = Sl + rowc;
     const float* const pS1 = Sl + so + k1;
@@ -861,43 +860,65 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     const float* const pq = &s.qvel[c_off + 4];
     float* const pV = V6 + kVA * c_off + crow;
     float* const pA = A6 + kVA * c_off + crow;
-    float nS[5], nq;
-    auto ld = [&](int r) {
-      nS[0] = pS0[kRow * r]; nS[1] = pS1[kRow * r]; nS[2] = pS2[kRow * r]; nS[3] = pS3[kRow * r]; nS[4] = pS4[kRow * r];
-      nq = pq[r];
-    };
-    ld(2);
-    float pc = 0.f, pac = 0.f;   // component rowc of the current body's v and a
+    // The velocities first: v = vp + S qd is a sum per component, so lane rowc needs nothing from
+    // the other lanes of its chain (the right arm's first body takes the torso's component from
+    // chain 2's lanes by row_shr:8); every level's operands are read before the sweep.
+    float Sr[kMaxDepth + 1], qd[kMaxDepth + 1];
+#pragma unroll
+    for (int r = 2; r <= kMaxDepth; ++r) { Sr[r] = pS0[kRow * r]; qd[r] = pq[r]; }
+    float pc = V6[kVA + rowc];   // component rowc of the current body's v (the pelvis' first)
 #pragma unroll
     for (int r = 2; r <= kMaxDepth; ++r) {
       const bool act = r >= c_lo && r <= c_hi;
-      const float Sr = nS[0], Sw1 = nS[1], Sw2 = nS[2], Sv1 = nS[3], Sv2 = nS[4], qd = nq;
-      if (r < kMaxDepth) ld(r + 1);
-      // The parent's row, as this chain stored it at the previous level (the LDS staging doubles as
-      // the exchange: four reads at per-lane columns instead of nine DPP moves): at depth 2 the
-      // pelvis, for the right arm's first body the torso (chain 2's depth-4 row). Its own component
-      // rowc is the lane's register from the previous level, read from the row where the parent is
-      // another chain's body.
-      const float* const prow = r == 2 ? V6 + kVA
-                                       : (r == kTorsoDepth + 1 && grp == 3 ? V6 + kVA * 16 : V6 + kVA * (c_off + r - 1));
-      const float X1 = prow[k1], X2 = prow[k2];           // w_p[k+1], w_p[k+2]
-      const float Y1 = prow[3 + k1], Y2 = prow[3 + k2];   // v_p[k+1], v_p[k+2]
-      float P = pc, PA = pac;
-      if (r == 2 || r == kTorsoDepth + 1) { P = prow[rowc]; PA = prow[kVA / 2 + rowc]; }
-      const float vn = fmaf_(Sr, qd, P);
-      const float t1 = fmaf_(-X2, Sw1, X1 * Sw2);   // (w_p x s_w)_k, or (w_p x s_v)_k
-      const float t2 = fmaf_(-Y2, Sv1, Y1 * Sv2);   // (v_p x s_w)_k
-      const float sd = isv ? t1 + t2 : t1;
-      const float an = fmaf_(sd, qd, PA);
+      float P = pc;
+      if (r == kTorsoDepth + 1) {
+        const float t = from_prev_chain(pc);   // chain 2 -> 3: the torso's component
+        P = grp == 3 ? t : pc;
+      }
       // a chain's values outside its depth range are never read (its first body takes the parent
-      // from the pelvis' or the torso's row), so no select keeps them
-      pc = vn;
-      pac = an;
+      // from the pelvis or the torso), so no select keeps them
+      pc = fmaf_(Sr[r], qd[r], P);
       // Stores: lanes 6 and 7 into the padding. Up to depth 7 every lane stores: the only inactive
       // chain there, the right arm before its first body (depths 2..4), writes rows 21..23, which
       // chain 2 stores again at depths 9..11. Beyond depth 7 the legs are past their last body and
       // would overwrite rows that chains 1 and 2 stored at depths 2..5, so `act` guards.
-      if (r <= 7 || act) { pV[kVA * r] = pc; pA[kVA * r] = pac; }
+      if (r <= 7 || act) pV[kVA * r] = pc;
+    }
+    // Then the accelerations a = ap + (vp x S) qd: the cross products take the parent's other
+    // components from its velocity row as just stored (four reads at per-lane columns; at depth 2
+    // the pelvis' row, for the right arm's first body the torso's, chain 2's depth-4 row). Those
+    // reads do not wait on the acceleration chain, so only one fma per level is serial; each
+    // level's operands are read two levels ahead.
+    auto ldc = [&](int r, float (&o)[8]) {
+      const float* const prow = r == 2 ? V6 + kVA
+                                       : (r == kTorsoDepth + 1 && grp == 3 ? V6 + kVA * 16 : V6 + kVA * (c_off + r - 1));
+      o[0] = prow[k1]; o[1] = prow[k2];           // w_p[k+1], w_p[k+2]
+      o[2] = prow[3 + k1]; o[3] = prow[3 + k2];   // v_p[k+1], v_p[k+2]
+      o[4] = pS1[kRow * r]; o[5] = pS2[kRow * r]; o[6] = pS3[kRow * r]; o[7] = pS4[kRow * r];
+    };
+    float cur[8], nxt[8];
+    ldc(2, cur);
+    ldc(3, nxt);
+    float pac = A6[kVA + rowc];   // component rowc of the current body's a (the pelvis' first)
+#pragma unroll
+    for (int r = 2; r <= kMaxDepth; ++r) {
+      const bool act = r >= c_lo && r <= c_hi;
+      float nn[8];
+      if (r + 2 <= kMaxDepth) ldc(r + 2, nn);
+      const float X1 = cur[0], X2 = cur[1], Y1 = cur[2], Y2 = cur[3];
+      const float Sw1 = cur[4], Sw2 = cur[5], Sv1 = cur[6], Sv2 = cur[7];
+      const float t1 = fmaf_(-X2, Sw1, X1 * Sw2);   // (w_p x s_w)_k, or (w_p x s_v)_k
+      const float t2 = fmaf_(-Y2, Sv1, Y1 * Sv2);   // (v_p x s_w)_k
+      const float sd = isv ? t1 + t2 : t1;
+      float PA = pac;
+      if (r == kTorsoDepth + 1) {
+        const float t = from_prev_chain(pac);   // chain 2 -> 3: the torso's component
+        PA = grp == 3 ? t : pac;
+      }
+      pac = fmaf_(sd, qd[r], PA);
+      if (r <= 7 || act) pA[kVA * r] = pac;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { cur[e] = nxt[e]; nxt[e] = nn[e]; }
     }
   }
   wave_sync();
