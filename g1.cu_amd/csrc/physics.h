@@ -733,8 +733,20 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     static_assert(foot_body[0] == foot_body[kNFoot / 2 - 1] && foot_body[kNFoot / 2] == foot_body[kNFoot - 1],
                   "foot spheres in two halves");
     const int fb = sph < kNFoot / 2 ? foot_body[0] : foot_body[kNFoot - 1];
-    Q4 fq{gshfl(xq.w, fb), gshfl(xq.x, fb), gshfl(xq.y, fb), gshfl(xq.z, fb)};
-    V3 fp{gshfl(xp.x, fb), gshfl(xp.y, fb), gshfl(xp.z, fb)};
+    // the foot bodies' lanes lie in the sphere lanes' 16-lane row: their frames by DPP row
+    // broadcasts and a select instead of lane exchanges through LDS
+    static_assert(foot_body[0] < 16 && foot_body[kNFoot - 1] < 16 && kNFoot <= 16, "feet in row 0");
+    constexpr int kL = foot_body[0], kR = foot_body[kNFoot - 1];
+    const bool left = sph < kNFoot / 2;
+    // (both broadcasts on every lane before the select: a DPP move inside a lane-divergent branch
+    // would read a source lane that the branch has switched off)
+    auto foot = [&](float v) {
+      float a = group_bcast<kL, 16>(v), b = group_bcast<kR, 16>(v);
+      __asm__ volatile("" : "+v"(a), "+v"(b));
+      return left ? a : b;
+    };
+    Q4 fq{foot(xq.w), foot(xq.x), foot(xq.y), foot(xq.z)};
+    V3 fp{foot(xp.x), foot(xp.y), foot(xp.z)};
     V3 c = vadd(fp, qrot(fq, foot_lp));
     const float pen = c.z - MF::foot_radius;
     const bool hit = (l < kNFoot) && (pen < 0.f);
