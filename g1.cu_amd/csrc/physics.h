@@ -99,8 +99,8 @@ __device__ __forceinline__ V3d qrotd(Q4d q, V3d v) {
 }
 __device__ __forceinline__ double gshfld(double v, int src) { return __shfl(v, src, kGroup); }
 
-// Correctly rounded fp32 transcendentals (evaluated in fp64, rounded once; fp64 VALU runs at the
-// fp32 rate on CDNA4 and these sit outside the inner loops). The contact force is stiff in the
+// Correctly rounded fp32 transcendentals (evaluated in fp64, rounded once; fp64 VALU issues like
+// fp32, at about twice its VALU time, and these sit outside the inner loops). The contact force is stiff in the
 // foot height, so a 1-ulp difference in an FK rotation moves qacc by up to ~1e-4 relative on
 // shallow penetrations; correct rounding makes every transcendental reproducible bit-for-bit.
 __device__ __forceinline__ float sin_rn(float x) { return (float)sin((double)x); }
@@ -672,7 +672,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // in fp64 and the frames are rounded to fp32 once: the foot-ground contact is stiff in the foot
   // height, and fp64 compositions halve the fp32 error against MuJoCo's contact fixture (1.3e-5
   // against 2.9e-5 for fp32 doubling and 2.2e-5 for the reference's fp32 recursion). fp64 FMAs
-  // issue at the rate of unpacked fp32 ones on CDNA4.
+  // issue like fp32 ones and take about twice their VALU time.
   V3 xp{0.f, 0.f, 0.f};
   Q4 xq{1.f, 0.f, 0.f, 0.f};
   V3 xip{0.f, 0.f, 0.f};
