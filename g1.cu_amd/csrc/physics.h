@@ -668,8 +668,9 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
   // (4 rounds instead of 10 levels); the CPU oracle composes in the same association. Hinge
   // anchors sit at the body origin (jnt_pos == 0, generator-checked), so the reference's anchor
   // shift pos = (pos + q*0) - q'*0 is the identity and is omitted.
-  // The per-body transforms are formed in fp32, the compositions and the inertial-frame offset run
-  // in fp64 and the frames are rounded to fp32 once: the foot-ground contact is stiff in the foot
+  // The per-body transforms are formed in fp32, the compositions of every round but the last run in
+  // fp64 and the frames are rounded to fp32 once before the last round (which only the arms' distal
+  // links need; it and the inertial-frame offset run in fp32): the foot-ground contact is stiff in the foot
   // height, and fp64 compositions halve the fp32 error against MuJoCo's contact fixture (1.3e-5
   // against 2.9e-5 for fp32 doubling and 2.2e-5 for the reference's fp32 recursion). fp64 FMAs
   // issue like fp32 ones and take about twice their VALU time.
@@ -696,7 +697,7 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
     V3d dp{xp.x, xp.y, xp.z};
     Q4d dq{xq.w, xq.x, xq.y, xq.z};
 #pragma unroll
-    for (int r = 0; r < kFkRounds; ++r) {
+    for (int r = 0; r < kFkRounds - 1; ++r) {
       const int an = (anc >> (8 * r)) & 0xff;
       Q4d qa;
       V3d pa;
@@ -717,10 +718,22 @@ __device__ __forceinline__ int world_qacc(int lane, WorldLds& s, const LaneState
       dp = vaddd(pa, qrotd(qa, dp));
       dq = qmuld(qa, dq);
     }
-    const V3d dip = vaddd(dp, qrotd(dq, V3d{L.ipos.x, L.ipos.y, L.ipos.z}));
+    // The last round in fp32, on the frames rounded once: only the arms' distal bodies (depth >=
+    // 2^(kFkRounds-1) + 1) have an ancestor left, and every other lane composes with the world's
+    // identity, which is exact, so its frame (the feet's among them) is the fp64 one rounded once.
+    // The inertial-frame offset then follows in fp32 from the final frame.
+    static_assert(body_depth[foot_body[0]] <= (1 << (kFkRounds - 1)) &&
+                  body_depth[foot_body[kNFoot - 1]] <= (1 << (kFkRounds - 1)), "the feet are final before the fp32 round");
     xp = {(float)dp.x, (float)dp.y, (float)dp.z};
     xq = {(float)dq.w, (float)dq.x, (float)dq.y, (float)dq.z};
-    xip = {(float)dip.x, (float)dip.y, (float)dip.z};
+    {
+      const int an = (anc >> (8 * (kFkRounds - 1))) & 0xff;
+      const Q4 qa{gshfl(xq.w, an), gshfl(xq.x, an), gshfl(xq.y, an), gshfl(xq.z, an)};
+      const V3 pa{gshfl(xp.x, an), gshfl(xp.y, an), gshfl(xp.z, an)};
+      xp = vadd(pa, qrot(qa, xp));
+      xq = qmul(qa, xq);
+    }
+    xip = vadd(xp, qrot(xq, L.ipos));
   }
   // pelvis origin: every lane carries the free joint's state (integrate_lane), and the pelvis' frame
   // is its position as it stands (no ancestor to compose with)

@@ -21,6 +21,7 @@
 #include <cstdint>
 #include <cstring>
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 #ifdef _OPENMP
 #include <omp.h>
@@ -163,9 +164,11 @@ template <class R> static inline V3<R> ldv(const R* p) { return {p[0], p[1], p[2
 // body_quat (x) rot(axis, qpos); the pelvis: its free-joint pose) by ancestor doubling, the
 // association the GPU uses: round r sets T_b <- T_a o T_b with a the 2^r-th ancestor of b, reading
 // the transforms of the previous round (tree.h). The per-body transforms are formed in R; the
-// compositions and the inertial-frame offsets run in fp64 for both instantiations and the frames
-// are rounded to R once. In fp32 that keeps the world frames within about one rounding of the exact
-// ones: the foot-ground contact is stiff in the foot height, and fp32 compositions (either
+// compositions of every round but the last run in fp64 for both instantiations, the frames are
+// rounded to R once, and the last round (only the arms' distal links have an ancestor left; the
+// feet are final before it) and the inertial-frame offsets run in R. In fp32 that keeps the foot
+// frames within about one rounding of the exact ones: the foot-ground contact is stiff in the foot
+// height, and fp32 compositions (either
 // association) move qacc on MuJoCo's contact fixture by up to 2.2e-5 (root -> leaf) or 2.9e-5
 // (doubling) relative, fp64 compositions by 1.3e-5 (fp64 everywhere: 9.2e-6). The fp64
 // instantiation is pinned against the MuJoCo frames of bench/ref_traj.npz, and
@@ -191,28 +194,40 @@ template <class R> void fk(const R* qpos, R* xpos, R* xquat, R* xipos) {
     tp[b] = {C(p.x), C(p.y), C(p.z)};
     tq[b] = {C(q.w), C(q.x), C(q.y), C(q.z)};
   }
-  for (int r = 0; r < kFkRounds; ++r) {
-    V3<C> op[kNBody];
-    Q4<C> oq[kNBody];
-    std::copy(tp, tp + kNBody, op);
-    std::copy(tq, tq + kNBody, oq);
-    // every body composes, with the world body's identity (a = 0) where the 2^r-th ancestor would
-    // lie beyond the world: the GPU's branch-free form, equal to leaving the transform unchanged
-    // except for the sign of an exact zero
+  // every body composes, with the world body's identity (a = 0) where the 2^r-th ancestor would lie
+  // beyond the world: the GPU's branch-free form, equal to leaving the transform unchanged except
+  // for the sign of an exact zero
+  auto round = [](auto* p, auto* q, int r) {
+    using P = typename std::remove_reference<decltype(*p)>::type;
+    using Q = typename std::remove_reference<decltype(*q)>::type;
+    P op[kNBody];
+    Q oq[kNBody];
+    std::copy(p, p + kNBody, op);
+    std::copy(q, q + kNBody, oq);
     for (int b = 1; b < kNBody; ++b) {
       const int a = kAncestors.a[r][b];
       if (a == 0 && !FkComposeIdentity<R>::value) continue;
-      tp[b] = vadd(op[a], qrot(oq[a], op[b]));
-      tq[b] = qmul(oq[a], oq[b]);
+      p[b] = vadd(op[a], qrot(oq[a], op[b]));
+      q[b] = qmul(oq[a], oq[b]);
     }
-  }
+  };
+  for (int r = 0; r < kFkRounds - 1; ++r) round(tp, tq, r);
+  // The last round in R on the frames rounded once (the GPU's form): only the bodies deeper than
+  // 2^(kFkRounds-1), the arms' distal links, have an ancestor left, every other body composes with
+  // the identity exactly, so the feet keep the fp64 frames rounded once; the inertial-frame offset
+  // follows in R from the final frame (the reference's formula on these frames).
+  V3<R> fp[kNBody];
+  Q4<R> fq[kNBody];
   for (int b = 0; b < kNBody; ++b) {
-    xpos[3 * b] = R(tp[b].x); xpos[3 * b + 1] = R(tp[b].y); xpos[3 * b + 2] = R(tp[b].z);
-    xquat[4 * b] = R(tq[b].w); xquat[4 * b + 1] = R(tq[b].x); xquat[4 * b + 2] = R(tq[b].y);
-    xquat[4 * b + 3] = R(tq[b].z);
-    const V3<R> ip = ldv(&M<R>::body_ipos[3 * b]);
-    V3<C> cw = vadd(tp[b], qrot(tq[b], V3<C>{C(ip.x), C(ip.y), C(ip.z)}));
-    xipos[3 * b] = R(cw.x); xipos[3 * b + 1] = R(cw.y); xipos[3 * b + 2] = R(cw.z);
+    fp[b] = {R(tp[b].x), R(tp[b].y), R(tp[b].z)};
+    fq[b] = {R(tq[b].w), R(tq[b].x), R(tq[b].y), R(tq[b].z)};
+  }
+  round(fp, fq, kFkRounds - 1);
+  for (int b = 0; b < kNBody; ++b) {
+    xpos[3 * b] = fp[b].x; xpos[3 * b + 1] = fp[b].y; xpos[3 * b + 2] = fp[b].z;
+    xquat[4 * b] = fq[b].w; xquat[4 * b + 1] = fq[b].x; xquat[4 * b + 2] = fq[b].y; xquat[4 * b + 3] = fq[b].z;
+    const V3<R> cw = vadd(fp[b], qrot(fq[b], ldv(&M<R>::body_ipos[3 * b])));
+    xipos[3 * b] = cw.x; xipos[3 * b + 1] = cw.y; xipos[3 * b + 2] = cw.z;
   }
   xipos[0] = xipos[1] = xipos[2] = 0;
 }
