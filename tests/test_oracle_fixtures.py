@@ -131,8 +131,8 @@ def test_implicit_pd_matches_mujoco_implicitfast(orc):
 @pytest.mark.parametrize("dtype,tol", [(np.float64, 1.2e-5), (np.float32, 1.5e-5)])
 def test_contact_qacc_matches_mujoco(orc, dtype, tol):
     """Pure foot-ground states vs MuJoCo's converged qacc at 2000 PGS sweeps (reference worst
-    relerr 2.24e-5 on its fp32 CUDA path, DEVLOG.md:250-251; this fp32 path composes FK in fp64
-    and measures 1.28e-5)."""
+    relerr 2.24e-5 on its fp32 CUDA path, DEVLOG.md:250-251; this fp32 path composes FK's first
+    three doubling rounds in fp64, the feet's frames among them, and measures 1.27e-5)."""
     cv = load_contact_validate()
     qa, nc = orc.qacc(cv["qpos"], cv["qvel"], pgs=2000, mu=0.6, dtype=dtype)
     assert list(nc) == [0, 0, 0, 8, 8, 4, 8, 8, 8]
